@@ -1,0 +1,117 @@
+"""ctypes binding of libresident_epoch.so (include/resident_epoch.h).
+
+The library is the product path: if it is missing the import fails loudly,
+there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "lib" / "libresident_epoch.so"
+
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# Every symbol declared in include/resident_epoch.h with (restype, argtypes).
+SIGNATURES: dict[str, tuple] = {
+    "resident_epoch_create": (
+        ctypes.c_void_p,
+        [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _c_i32p],
+    ),
+    "resident_epoch_execute": (
+        ctypes.c_int32,
+        [
+            ctypes.c_void_p,  # opaque
+            ctypes.c_int32,  # request_count
+            ctypes.c_int32,  # max_steps
+            _c_i64p,  # input_token_ids
+            _c_i64p,  # input_positions
+            _c_i32p,  # input_sequence_lengths
+            _c_i32p,  # input_eos_token_ids
+            _c_i32p,  # input_row_generations
+            _c_i64p,  # output_token_ids
+            _c_i32p,  # output_executed
+            _c_i32p,  # output_row_generations
+            _c_i32p,  # output_model_calls
+            _c_i32p,  # output_device_status
+            _c_i32p,  # output_feed_calls
+            _c_i32p,  # output_fetch_calls
+            _c_i32p,  # output_commit_state
+            _c_i32p,  # output_kv_import_checksum
+            _c_i64p,  # output_wall_us
+            _c_i64p,  # output_native_cpu_us
+            _c_i64p,  # output_declared_input_bytes
+            _c_i64p,  # output_declared_output_bytes
+            ctypes.c_char_p,  # transfer_path
+            ctypes.c_uint64,  # transfer_id
+            ctypes.c_void_p,  # ipc metadata
+        ],
+    ),
+    "resident_epoch_destroy": (None, [ctypes.c_void_p]),
+    "resident_epoch_proc": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64],
+    ),
+    "resident_decoder_step": (
+        ctypes.c_int32,
+        [ctypes.c_void_p] + [ctypes.c_void_p] * 11,
+    ),
+    "resident_epoch_prefill": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "resident_epoch_read_state": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int64],
+    ),
+    "resident_epoch_write_state": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int64],
+    ),
+    "resident_epoch_info": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_char_p, _c_i64p]),
+    "resident_epoch_kernel_timing": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int32]),
+    "resident_epoch_read_kernel_timing": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.c_int32],
+    ),
+    "resident_epoch_time_ops": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_float)],
+    ),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    override = os.getenv("CRUISE_RESIDENT_EPOCH_LIBRARY")
+    return Path(override) if override else LIBRARY_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library (once) and bind every declared symbol."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    # PyTorch-ROCm ships its own libamdhip64.so.7.  Importing it first makes
+    # the library bind that same HIP runtime (same soname), so torch tensors
+    # and the engine share one runtime and one device context per process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:  # pragma: no cover - torch is part of this image
+        pass
+    path = library_path()
+    if not path.is_file():
+        raise RuntimeError(
+            f"libresident_epoch.so is not built ({path}); run `python -m cruise_amd.build` "
+            "or __graft_entry__.build() first"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = lib
+    return lib

@@ -1,0 +1,494 @@
+// Epoch controller kernels of the resident decode epoch (gfx950): validation,
+// generation continuity, row clear / KV import, per-step argmax and row update,
+// finish and emit (controller/g4c_b4_resident_epoch.cpp:177-622), plus the
+// synthetic weight fill.  Integer state, bit-exact with the reference.
+#include "re_device.h"
+#include "re_layout.h"
+
+namespace re {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Epoch controller (controller/g4c_b4_resident_epoch.cpp).
+// ---------------------------------------------------------------------------
+struct CtrlArgs {
+  StatePtrs st;
+  int B, bpr, physical_blocks, block_size, capacity, vocab;
+  int lm_wg;          // argmax partial rows
+  const float* am_val;
+  const int32_t* am_idx;
+  const int32_t* am_bad;
+  int has_payload;
+};
+
+__device__ __forceinline__ int compute_slot(const int32_t* table, const CtrlArgs& a, int request,
+                                            long long position) {
+  // ComputeSlot, CTRL:84-97, with the capacity / blocks-per-row parameters.
+  if (request < 0 || request >= a.B || position < 0 || position >= a.capacity) return -1;
+  const int logical = static_cast<int>(position / a.block_size);
+  const int offset = static_cast<int>(position % a.block_size);
+  if (logical >= a.bpr) return -1;
+  const int physical = table[request * a.bpr + logical];
+  if (physical < 0 || physical >= a.physical_blocks) return -1;
+  return physical * a.block_size + offset;
+}
+
+struct FeedView {
+  const int64_t* token;
+  const int64_t* pos;
+  const int32_t* len;
+  const int32_t* slot;  // nullptr in import mode
+  const int32_t* active;
+  const int32_t* table;
+  const int32_t* control;
+};
+
+__device__ FeedView feed_view(const uint8_t* feed, int B, int bpr, bool importing, long long payload_bytes) {
+  FeedView f;
+  const uint8_t* p = feed + (importing ? payload_bytes : 0);
+  f.token = reinterpret_cast<const int64_t*>(p);
+  p += 8 * B;
+  f.pos = reinterpret_cast<const int64_t*>(p);
+  p += 8 * B;
+  f.len = reinterpret_cast<const int32_t*>(p);
+  p += 4 * B;
+  if (importing) {
+    f.slot = nullptr;
+  } else {
+    f.slot = reinterpret_cast<const int32_t*>(p);
+    p += 4 * B;
+  }
+  f.active = reinterpret_cast<const int32_t*>(p);
+  p += 4 * B;
+  f.table = reinterpret_cast<const int32_t*>(p);
+  p += 4 * B * bpr;
+  p += kTilingBytes;
+  f.control = reinterpret_cast<const int32_t*>(p);
+  return f;
+}
+
+// Validation, import bookkeeping, generation continuity (CTRL:204-471) and the
+// loop's initial state (CTRL:473-483).  Single thread: B rows of integer work.
+__global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  StatePtrs& s = a.st;
+  const int B = a.B;
+  // The control vector sits at the same place in both feed forms; read the
+  // variant first to learn the form (CTRL:209-217).
+  const FeedView plain = feed_view(s.feed, B, a.bpr, false, 0);
+  const int32_t* ctl_plain = plain.control;  // valid only for the plain form
+  (void)ctl_plain;
+  // In import mode the payload precedes everything and the slot input is
+  // absent, so the control offset differs; the host tells us the form.
+  const bool importing = a.has_payload != 0;
+  const FeedView f = feed_view(s.feed, B, a.bpr, importing, payload_bytes);
+  const int32_t* ctl = f.control;
+  const int32_t encoded_variant = ctl[2 + B];
+  const bool flagged = (encoded_variant & kImportGraphFlag) != 0;
+  const int32_t import_mask = flagged ? (encoded_variant & (kImportGraphFlag - 1)) : 0;
+  const int32_t graph_variant = flagged ? (encoded_variant & ~(kImportGraphFlag | 0xF)) : encoded_variant;
+  const int32_t max_steps = ctl[0];
+  const int32_t sampling = ctl[1 + B];
+  s.misc[0] = max_steps;
+  s.misc[1] = sampling;
+  s.misc[2] = graph_variant;
+  s.misc[3] = flagged ? 1 : 0;
+  s.misc[4] = import_mask;
+  *s.model_calls = 0;
+  *s.status = kStatusOk;
+  *s.done = 0;
+  int64_t* history = reinterpret_cast<int64_t*>(s.fetch);
+  for (int i = 0; i < kMaxEpochSteps * B; ++i) history[i] = -1;
+  for (int r = 0; r < B; ++r) {
+    s.executed[r] = 0;
+    s.reason[r] = kFinishNone;
+    s.clear_row[r] = 0;
+    s.eos[r] = ctl[1 + r];
+    s.initial_active[r] = f.active[r];
+    s.generation[r] = ctl[3 + B + r];
+    s.cur_token[r] = f.token[r];
+    s.cur_pos[r] = f.pos[r];
+    s.cur_len[r] = f.len[r];
+    s.cur_active[r] = f.active[r];
+  }
+  for (int i = 0; i < B * a.bpr; ++i) s.table[i] = f.table[i];
+  for (int r = 0; r < B; ++r) s.cur_slot[r] = f.slot ? f.slot[r] : compute_slot(s.table, a, r, f.pos[r]);
+
+  int32_t status = kStatusOk;
+  if (flagged != importing) {
+    status = kStatusInvalidMetadata;  // feed form and flag disagree
+  } else if (max_steps < 1 || max_steps > kMaxEpochSteps || sampling != 0 || graph_variant != 0) {
+    // CTRL:335-340
+    status = sampling != 0 ? kStatusUnsupportedSampling
+             : graph_variant != 0 ? kStatusUnsupportedGraph
+                                  : kStatusInvalidMetadata;
+  }
+  if (status == kStatusOk) {
+    for (int r = 0; r < B; ++r)
+      if (s.eos[r] < 0 || s.eos[r] >= a.vocab) { status = kStatusInvalidMetadata; break; }  // 341-345
+  }
+  if (status == kStatusOk) {  // 346-353: blocks in range and unique
+    for (int i = 0; i < B * a.bpr && status == kStatusOk; ++i) {
+      const int blk = s.table[i];
+      if (blk < 0 || blk >= a.physical_blocks) { status = kStatusInvalidBlockTable; break; }
+      for (int j = 0; j < i; ++j)
+        if (s.table[j] == blk) { status = kStatusInvalidBlockTable; break; }
+    }
+  }
+  if (status == kStatusOk) {  // 354-385
+    for (int r = 0; r < B; ++r) {
+      const int32_t act = f.active[r];
+      const int64_t tok = f.token[r], pos = f.pos[r];
+      const int32_t len = f.len[r];
+      if ((act != 0 && act != 1) || tok < 0 || tok >= a.vocab || pos < 0 || pos >= a.capacity) {
+        status = kStatusInvalidMetadata;
+        break;
+      }
+      if (act == 1) {
+        if (s.generation[r] <= 0 || len != pos + 1) { status = kStatusInvalidMetadata; break; }
+        if (pos + max_steps > a.capacity) { status = kStatusCapacityExceeded; break; }
+      } else if (len == 0) {
+        if (s.generation[r] != 0) { status = kStatusInvalidMetadata; break; }
+        s.reason[r] = kFinishEmpty;
+      } else if (len == pos + 1) {
+        s.reason[r] = kFinishAlreadyFinished;
+      } else {
+        status = kStatusInvalidMetadata;
+        break;
+      }
+      if (compute_slot(s.table, a, r, pos) != s.cur_slot[r]) { status = kStatusSlotMismatch; break; }
+    }
+  }
+  if (status == kStatusOk && importing) {  // 387-429 (the copy itself runs in k_clear_rows)
+    if (import_mask <= 0 || import_mask >= (1 << B)) status = kStatusInvalidMetadata;
+    for (int r = 0; r < B && status == kStatusOk; ++r) {
+      if ((import_mask & (1 << r)) == 0) continue;
+      if (f.active[r] != 1 || s.generation[r] <= 0) { status = kStatusInvalidMetadata; break; }
+      s.clear_row[r] = 2;  // clear, then import block 0 of the row
+      s.res_gen[r] = s.generation[r];
+      s.res_token[r] = f.token[r];
+      s.res_pos[r] = f.pos[r];
+      s.res_len[r] = f.len[r];
+      s.res_valid[r] = 1;
+    }
+  }
+  if (status == kStatusOk) {  // 448-464
+    for (int r = 0; r < B; ++r) {
+      if (f.active[r] == 0) continue;
+      if (s.res_gen[r] == s.generation[r]) {
+        if (s.res_valid[r] == 0 || s.res_token[r] != f.token[r] || s.res_pos[r] != f.pos[r] ||
+            s.res_len[r] != f.len[r]) {
+          status = kStatusResidentContinuity;
+          break;
+        }
+      } else {
+        if (f.pos[r] != 0 || f.len[r] != 1) { status = kStatusResidentContinuity; break; }
+        s.clear_row[r] = 1;
+      }
+    }
+  }
+  if (status != kStatusOk) {
+    for (int r = 0; r < B; ++r) {
+      s.reason[r] = kFinishFallback;
+      s.clear_row[r] = 0;
+    }
+    *s.status = status;
+    *s.done = 1;
+  } else {
+    int count = 0;
+    for (int r = 0; r < B; ++r) count += s.cur_active[r] != 0;
+    if (count == 0) *s.done = 1;  // the loop runs no step (CTRL:488)
+  }
+}
+
+// Row clear (ClearCacheRow, CTRL:129-147, following the row's table entries)
+// and, in import mode, the copy of one block per layer from the payload
+// (CTRL:411-423).  Grid-stride over 16-byte words of all flagged blocks.
+struct ClearArgs {
+  const int32_t* clear_row;
+  const int32_t* table;
+  const uint8_t* payload;  // nullptr unless importing
+  uint8_t* key_cache;
+  uint8_t* value_cache;
+  int B, bpr, layers;
+  long long block_bytes, layer_bytes;  // bytes of one block / one layer of a cache
+};
+
+__global__ void k_clear_rows(ClearArgs a) {
+  const long long words_per_block = a.block_bytes / 16;
+  const long long per_row = (long long)a.layers * a.bpr * words_per_block;
+  const long long total = 2LL * a.B * per_row;  // key and value
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int cache = static_cast<int>(i / (a.B * per_row));
+    long long rem = i - (long long)cache * a.B * per_row;
+    const int r = static_cast<int>(rem / per_row);
+    const int flag = a.clear_row[r];
+    if (flag == 0) continue;
+    rem -= (long long)r * per_row;
+    const int layer = static_cast<int>(rem / (a.bpr * words_per_block));
+    rem -= (long long)layer * a.bpr * words_per_block;
+    const int local = static_cast<int>(rem / words_per_block);
+    const long long w = rem - (long long)local * words_per_block;
+    const int blk = a.table[r * a.bpr + local];
+    uint8_t* base = cache == 0 ? a.key_cache : a.value_cache;
+    uint4* dst = reinterpret_cast<uint4*>(base + layer * a.layer_bytes + blk * a.block_bytes) + w;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (flag == 2 && local == 0 && a.payload != nullptr) {
+      // payload [K|V][layers][B][block]
+      const uint8_t* src = a.payload + ((size_t)cache * a.layers * a.B + (size_t)layer * a.B + r) * a.block_bytes;
+      v = reinterpret_cast<const uint4*>(src)[w];
+    }
+    *dst = v;
+  }
+}
+
+// One step of the loop body after the model call (CTRL:496-589): argmax over
+// the LM-head partials, position progress, history, EOS, slot and length.
+__global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
+  StatePtrs& s = a.st;
+  if (*s.done != 0) return;
+  const int B = a.B;
+  __shared__ float bv_s[1024];
+  __shared__ int bi_s[1024];
+  __shared__ int bb_s[1024];
+  __shared__ int tok_s[64 * 4];
+  __shared__ int bad_s[64 * 4];
+  const int tid = threadIdx.x;
+  // Final argmax pass: threads stride over workgroup partials per row.
+  for (int b = 0; b < B; ++b) {
+    float bv = 0.f;
+    int bi = -1, bb = 0;
+    for (int w = tid; w < a.lm_wg; w += blockDim.x) {
+      const size_t o = (size_t)w * B + b;
+      const int i = a.am_idx[o];
+      const float v = a.am_val[o];
+      bb |= a.am_bad[o];
+      if (i < 0) continue;
+      if (bi < 0 || v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    }
+    bv_s[tid] = bv;
+    bi_s[tid] = bi;
+    bb_s[tid] = bb;
+    __syncthreads();
+    for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+      if (tid < stride) {
+        const float v = bv_s[tid + stride];
+        const int i = bi_s[tid + stride];
+        bb_s[tid] |= bb_s[tid + stride];
+        if (i >= 0 && (bi_s[tid] < 0 || v > bv_s[tid] || (v == bv_s[tid] && i < bi_s[tid]))) {
+          bv_s[tid] = v;
+          bi_s[tid] = i;
+        }
+      }
+      __syncthreads();
+    }
+    if (tid == 0) {
+      tok_s[b] = bi_s[0];
+      bad_s[b] = bb_s[0];
+    }
+    __syncthreads();
+  }
+  if (tid != 0) return;
+  const int call = ++(*s.model_calls);
+  int64_t* history = reinterpret_cast<int64_t*>(s.fetch);
+  int32_t status = kStatusOk;
+  // next_position = where(active, pos + 1, pos) (batched_decoder_step.py:409-411)
+  for (int r = 0; r < B; ++r) {
+    const int64_t next_pos = s.cur_active[r] != 0 ? s.cur_pos[r] + 1 : s.cur_pos[r];
+    if (s.cur_active[r] == 0) {
+      if (next_pos != s.cur_pos[r]) { status = kStatusPositionProgress; break; }
+      continue;
+    }
+    if (bad_s[r] != 0 || tok_s[r] < 0) { status = kStatusNonFiniteLogits; break; }
+    const int64_t tok = tok_s[r];
+    if (next_pos != s.cur_pos[r] + 1) { status = kStatusPositionProgress; break; }
+    history[(call - 1) * B + r] = tok;
+    s.executed[r] += 1;
+    s.cur_pos[r] = next_pos;
+    s.cur_token[r] = tok;
+    s.cur_len[r] = static_cast<int32_t>(next_pos + 1);
+    if (next_pos == a.capacity) {
+      s.cur_slot[r] = -1;
+    } else {
+      const int slot = compute_slot(s.table, a, r, next_pos);
+      if (slot < 0) { status = kStatusCapacityExceeded; break; }
+      s.cur_slot[r] = slot;
+    }
+    if (tok == s.eos[r]) {
+      s.cur_active[r] = 0;
+      s.reason[r] = kFinishEos;
+    }
+  }
+  if (status != kStatusOk) {
+    for (int r = 0; r < B; ++r) s.reason[r] = kFinishFallback;
+    *s.status = status;
+    *s.done = 1;
+    return;
+  }
+  int count = 0;
+  for (int r = 0; r < B; ++r) count += s.cur_active[r] != 0;
+  if (count == 0) *s.done = 1;
+}
+
+// Finish reasons, resident save and emit (CTRL:296-324, 592-621).
+__global__ void k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
+  (void)import_checksum_unused;
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  StatePtrs& s = a.st;
+  const int B = a.B;
+  const int32_t status = *s.status;
+  const bool fallback = status != kStatusOk;
+  if (!fallback) {
+    for (int r = 0; r < B; ++r)
+      if (s.initial_active[r] == 1 && s.reason[r] == kFinishNone) s.reason[r] = kFinishMaxSteps;
+    for (int r = 0; r < B; ++r) {
+      if (s.initial_active[r] == 0) continue;
+      s.res_gen[r] = s.generation[r];
+      s.res_token[r] = s.cur_token[r];
+      s.res_pos[r] = s.cur_pos[r];
+      s.res_len[r] = s.cur_len[r];
+      s.res_valid[r] = 1;
+    }
+  }
+  int32_t* control = reinterpret_cast<int32_t*>(s.fetch + 8 * kMaxEpochSteps * B);
+  const bool importing = s.misc[3] != 0;
+  control[0] = s.misc[0];
+  control[1] = s.misc[1];
+  control[2] = s.misc[2];
+  control[3] = status;
+  control[4] = *s.model_calls;
+  control[5] = importing ? 0 : (fallback ? 1 : 0);  // the import checksum is added by the host
+  int initial = 0, final_count = 0;
+  for (int r = 0; r < B; ++r) {
+    control[6 + r] = s.eos[r];
+    control[6 + B + r] = s.initial_active[r];
+    control[6 + 2 * B + r] = s.executed[r];
+    control[6 + 3 * B + r] = s.reason[r];
+    control[6 + 4 * B + 2 + r] = s.initial_active[r] == 1 ? s.generation[r] : 0;
+    initial += s.initial_active[r] != 0;
+    final_count += (fallback ? s.initial_active[r] : s.cur_active[r]) != 0;
+  }
+  control[6 + 4 * B] = initial;
+  control[6 + 4 * B + 1] = final_count;
+}
+
+// Counter-based N(0, std) fill for synthetic weights: a 64-bit mix of
+// (seed, stream, index) gives two uniforms, Box-Muller in fp32.
+__device__ __forceinline__ unsigned long long mix64(unsigned long long x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__global__ void k_fill_normal(void* dst, long long elems, int dtype_bytes, unsigned long long seed,
+                              unsigned long long stream_id, float std_dev) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < elems;
+       i += (long long)gridDim.x * blockDim.x) {
+    const unsigned long long h = mix64(mix64(seed ^ (stream_id * 0xD1B54A32D192ED03ull)) + (unsigned long long)i);
+    const float u1 = (static_cast<float>(h >> 40) + 1.0f) * (1.0f / 16777216.0f);          // (0, 1]
+    const float u2 = static_cast<float>((h >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);    // [0, 1)
+    const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    const float v = z * std_dev;
+    if (dtype_bytes == 2)
+      static_cast<bf16_t*>(dst)[i] = f_to_bf16(v);
+    else
+      static_cast<float*>(dst)[i] = v;
+  }
+}
+
+}  // namespace
+
+static CtrlArgs ctrl_args(const KernelEnv& env, const StatePtrs& st) {
+  CtrlArgs a{};
+  a.st = st;
+  a.B = env.dims.batch;
+  a.bpr = env.dims.blocks_per_row;
+  a.physical_blocks = env.dims.physical_blocks;
+  a.block_size = env.dims.block_size;
+  a.capacity = env.dims.capacity;
+  a.vocab = env.dims.vocab;
+  a.lm_wg = env.plan.lm_wg;
+  a.am_val = env.scratch.am_val;
+  a.am_idx = env.scratch.am_idx;
+  a.am_bad = env.scratch.am_bad;
+  return a;
+}
+
+static long long payload_bytes_of(const Dims& d) {
+  return 2LL * d.layers * d.batch * d.block_size * d.kv_dim() * d.dtype_bytes;
+}
+
+hipError_t launch_ctrl_init(const KernelEnv& env, const StatePtrs& st, int has_payload, hipStream_t stream) {
+  CtrlArgs a = ctrl_args(env, st);
+  a.has_payload = has_payload;
+  k_ctrl_init<<<1, 64, 0, stream>>>(a, has_payload ? payload_bytes_of(env.dims) : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_clear_rows(const KernelEnv& env, const StatePtrs& st, void* key_cache, void* value_cache,
+                             hipStream_t stream) {
+  const Dims& d = env.dims;
+  ClearArgs c{};
+  c.clear_row = st.clear_row;
+  c.table = st.table;
+  c.payload = st.feed;  // payload leads the feed in import mode; rows flagged 2 only then
+  c.key_cache = static_cast<uint8_t*>(key_cache);
+  c.value_cache = static_cast<uint8_t*>(value_cache);
+  c.B = d.batch;
+  c.bpr = d.blocks_per_row;
+  c.layers = d.layers;
+  c.block_bytes = (long long)d.block_size * d.kv_dim() * d.dtype_bytes;
+  c.layer_bytes = (long long)d.slots() * d.kv_dim() * d.dtype_bytes;
+  k_clear_rows<<<1024, 256, 0, stream>>>(c);
+  return hipGetLastError();
+}
+
+hipError_t launch_ctrl_step(const KernelEnv& env, const StatePtrs& st, hipStream_t stream) {
+  k_ctrl_step<<<1, 1024, 0, stream>>>(ctrl_args(env, st));
+  return hipGetLastError();
+}
+
+hipError_t launch_ctrl_finish(const KernelEnv& env, const StatePtrs& st, hipStream_t stream) {
+  k_ctrl_finish<<<1, 64, 0, stream>>>(ctrl_args(env, st), 0u);
+  return hipGetLastError();
+}
+
+namespace {
+__global__ void k_clear_blocks(uint8_t* kc, uint8_t* vc, const int32_t* blocks, int nblocks, int layers,
+                               long long block_bytes, long long layer_bytes) {
+  const long long words = block_bytes / 16;
+  const long long total = 2LL * layers * nblocks * words;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int cache = static_cast<int>(i / ((long long)layers * nblocks * words));
+    long long rem = i - (long long)cache * layers * nblocks * words;
+    const int layer = static_cast<int>(rem / (nblocks * words));
+    rem -= (long long)layer * nblocks * words;
+    const int bi = static_cast<int>(rem / words);
+    const long long w = rem - (long long)bi * words;
+    uint8_t* base = cache == 0 ? kc : vc;
+    reinterpret_cast<uint4*>(base + layer * layer_bytes + (long long)blocks[bi] * block_bytes)[w] =
+        make_uint4(0, 0, 0, 0);
+  }
+}
+}  // namespace
+
+hipError_t launch_clear_blocks(const KernelEnv& env, void* key_cache, void* value_cache, const int32_t* blocks,
+                               int nblocks, hipStream_t stream) {
+  const Dims& d = env.dims;
+  k_clear_blocks<<<512, 256, 0, stream>>>(static_cast<uint8_t*>(key_cache), static_cast<uint8_t*>(value_cache),
+                                          blocks, nblocks, d.layers,
+                                          (long long)d.block_size * d.kv_dim() * d.dtype_bytes,
+                                          (long long)d.slots() * d.kv_dim() * d.dtype_bytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_synthetic(void* dst, long long elems, int dtype_bytes, unsigned long long seed,
+                                 unsigned long long stream_id, float std_dev, hipStream_t stream) {
+  k_fill_normal<<<4096, 256, 0, stream>>>(dst, elems, dtype_bytes, seed, stream_id, std_dev);
+  return hipGetLastError();
+}
+
+}  // namespace re

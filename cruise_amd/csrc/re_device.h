@@ -1,0 +1,168 @@
+// Device-side helpers shared by the resident-epoch kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+typedef __bf16 re_bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t re_u32x4 __attribute__((ext_vector_type(4)));
+typedef float re_f32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 <-> fp32.  The fp32 -> bf16 rounding is round-to-nearest-even with
+// NaN mapped to 0x7FC0, the conversion torch applies on ``.to(bfloat16)``.
+__device__ __forceinline__ float bf16_to_f(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+__device__ __forceinline__ bf16_t f_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>(0x7fc0);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
+
+// Element traits: the compute dtype T of a model is bf16 or fp32.
+template <typename T>
+struct Elt;
+
+template <>
+struct Elt<bf16_t> {
+  static constexpr int kBytes = 2;
+  __device__ __forceinline__ static float f(bf16_t v) { return bf16_to_f(v); }
+  __device__ __forceinline__ static bf16_t t(float v) { return f_to_bf16(v); }
+  __device__ __forceinline__ static float r(float v) { return round_bf16(v); }
+};
+
+template <>
+struct Elt<float> {
+  static constexpr int kBytes = 4;
+  __device__ __forceinline__ static float f(float v) { return v; }
+  __device__ __forceinline__ static float t(float v) { return v; }
+  __device__ __forceinline__ static float r(float v) { return v; }
+};
+
+// Eight consecutive elements (16 bytes of bf16, 32 bytes of fp32).
+template <typename T>
+struct Vec8;
+
+template <>
+struct Vec8<bf16_t> {
+  re_u32x4 v;
+  __device__ __forceinline__ static Vec8 load(const bf16_t* p) {
+    Vec8 r;
+    r.v = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(p));
+    return r;
+  }
+  __device__ __forceinline__ static Vec8 load_cached(const bf16_t* p) {
+    Vec8 r;
+    r.v = *reinterpret_cast<const re_u32x4*>(p);
+    return r;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    const uint32_t w = v[i >> 1];
+    return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+  // Round eight floats to bf16 (RNE) and pack them.
+  __device__ __forceinline__ static Vec8 from_floats(const float (&f)[8]) {
+    Vec8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r.v[i] = static_cast<uint32_t>(f_to_bf16(f[2 * i])) | (static_cast<uint32_t>(f_to_bf16(f[2 * i + 1])) << 16);
+    return r;
+  }
+};
+
+template <>
+struct Vec8<float> {
+  re_f32x4 a, b;
+  __device__ __forceinline__ static Vec8 load(const float* p) {
+    Vec8 r;
+    r.a = __builtin_nontemporal_load(reinterpret_cast<const re_f32x4*>(p));
+    r.b = __builtin_nontemporal_load(reinterpret_cast<const re_f32x4*>(p) + 1);
+    return r;
+  }
+  __device__ __forceinline__ static Vec8 load_cached(const float* p) {
+    Vec8 r;
+    r.a = reinterpret_cast<const re_f32x4*>(p)[0];
+    r.b = reinterpret_cast<const re_f32x4*>(p)[1];
+    return r;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    return i < 4 ? a[i] : b[i - 4];
+  }
+  __device__ __forceinline__ static Vec8 from_floats(const float (&f)[8]) {
+    Vec8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.a[i] = f[i];
+      r.b[i] = f[i + 4];
+    }
+    return r;
+  }
+};
+
+// acc + w.lo*x.lo + w.hi*x.hi for one packed pair of bf16 (fp32 accumulate).
+// The operands arrive as plain 32-bit scalars: clang's __builtin_bit_cast of
+// an ext-vector element (v.y, v.z, ...) reads element 0 whatever the index,
+// so elements are copied out before the cast.
+__device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(re_bf16x2, w), __builtin_bit_cast(re_bf16x2, x), acc,
+                                         false);
+}
+
+// acc + sum_i w[i] * x[i] over eight elements, fp32 accumulation.
+__device__ __forceinline__ float dot8(const Vec8<bf16_t>& w, const Vec8<bf16_t>& x, float acc) {
+  const uint32_t w0 = w.v[0], w1 = w.v[1], w2 = w.v[2], w3 = w.v[3];
+  const uint32_t x0 = x.v[0], x1 = x.v[1], x2 = x.v[2], x3 = x.v[3];
+  acc = dot2_bf16(w0, x0, acc);
+  acc = dot2_bf16(w1, x1, acc);
+  acc = dot2_bf16(w2, x2, acc);
+  acc = dot2_bf16(w3, x3, acc);
+  return acc;
+}
+__device__ __forceinline__ float dot8(const Vec8<float>& w, const Vec8<float>& x, float acc) {
+  acc = fmaf(w.a.x, x.a.x, acc);
+  acc = fmaf(w.a.y, x.a.y, acc);
+  acc = fmaf(w.a.z, x.a.z, acc);
+  acc = fmaf(w.a.w, x.a.w, acc);
+  acc = fmaf(w.b.x, x.b.x, acc);
+  acc = fmaf(w.b.y, x.b.y, acc);
+  acc = fmaf(w.b.z, x.b.z, acc);
+  acc = fmaf(w.b.w, x.b.w, acc);
+  return acc;
+}
+
+// Sum N values (a power of two <= 64) over the 64 lanes of a wavefront by
+// halving exchanges: afterwards lane (64/N)*i holds the total of value i.
+template <int N>
+__device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+  int mask = 32;
+#pragma unroll
+  for (int n = N; n > 1; n >>= 1) {
+    const int h = n >> 1;
+    const bool upper = (lane & mask) != 0;
+#pragma unroll
+    for (int i = 0; i < h; ++i) {
+      float send = upper ? v[i] : v[i + h];
+      float keep = upper ? v[i + h] : v[i];
+      float recv = __shfl_xor(send, mask, 64);
+      v[i] = keep + recv;
+    }
+    mask >>= 1;
+  }
+#pragma unroll
+  for (; mask >= 1; mask >>= 1) v[0] += __shfl_xor(v[0], mask, 64);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}

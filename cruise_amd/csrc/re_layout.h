@@ -1,0 +1,187 @@
+// Host/device shared layout of the resident-epoch engine: model dims, the
+// weight arena offsets, device state pointers and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace re {
+
+constexpr int kMaxEpochSteps = 8;       // controller/g4c_b4_resident_epoch.cpp:17
+constexpr int kImportGraphFlag = 0x100;  // controller/g4c_b4_resident_epoch.cpp:27
+constexpr int kTilingBytes = 72;        // native/resident_epoch_bridge.cpp:61
+
+// Device statuses (controller/g4c_b4_resident_epoch.cpp:60-74) and finish
+// reasons (51-58).
+enum Status : int32_t {
+  kStatusOk = 0,
+  kStatusInvalidMetadata = 201,
+  kStatusCapacityExceeded = 202,
+  kStatusInvalidBlockTable = 203,
+  kStatusSlotMismatch = 204,
+  kStatusUnsupportedSampling = 205,
+  kStatusUnsupportedGraph = 206,
+  kStatusModelError = 207,
+  kStatusInvalidModelOutput = 208,
+  kStatusNonFiniteLogits = 209,
+  kStatusPositionProgress = 210,
+  kStatusAllocationFailure = 211,
+  kStatusResidentContinuity = 212,
+};
+enum Finish : int32_t {
+  kFinishNone = 0,
+  kFinishEos = 1,
+  kFinishMaxSteps = 2,
+  kFinishFallback = 3,
+  kFinishEmpty = 4,
+  kFinishAlreadyFinished = 5,
+};
+
+struct Dims {
+  int layers, hidden, heads, kv_heads, head_dim, intermediate, vocab;
+  float rope_theta, rms_eps;
+  int dtype_bytes;  // 2 = bf16, 4 = fp32
+  // paged geometry
+  int batch, physical_blocks, block_size, blocks_per_row, capacity;
+  int configured_eos;
+
+  int groups() const { return heads / kv_heads; }
+  int q_dim() const { return heads * head_dim; }
+  int kv_dim() const { return kv_heads * head_dim; }
+  int qkv_rows() const { return q_dim() + 2 * kv_dim(); }
+  long long slots() const { return (long long)physical_blocks * block_size; }
+  long long cache_elems() const { return (long long)layers * slots() * kv_dim(); }
+};
+
+// Byte offsets of one layer's tensors inside the weight arena (each 256-byte
+// aligned).  q, k and v rows are stacked into one [qkv_rows, hidden] matrix.
+struct LayerOffsets {
+  size_t input_norm, post_norm, qkv_w, qkv_b, o_w, gate_w, up_w, down_w;
+};
+
+// The epoch's device state.  Feed and fetch are contiguous byte buffers in
+// the ABI order so one copy moves each; the rest persists across epochs.
+struct StatePtrs {
+  // feed (H2D once per epoch)
+  uint8_t* feed;
+  // working rows of the current step (CTRL:473-483)
+  int64_t* cur_token;
+  int64_t* cur_pos;
+  int32_t* cur_len;
+  int32_t* cur_slot;
+  int32_t* cur_active;
+  int32_t* table;  // [B * BPR]
+  // epoch bookkeeping
+  int32_t* done;        // 1 = remaining steps are skipped
+  int32_t* status;      // device status
+  int32_t* model_calls;
+  int32_t* executed;    // [B]
+  int32_t* reason;      // [B]
+  int32_t* clear_row;   // [B] new generation -> clear the row's blocks
+  int32_t* eos;         // [B]
+  int32_t* initial_active;  // [B]
+  int32_t* generation;  // [B] from control
+  int32_t* misc;        // [0] K, [1] sampling, [2] variant, [3] importing, [4] import mask
+  // resident state (CTRL:624-631)
+  int32_t* res_gen;
+  int64_t* res_token;
+  int64_t* res_pos;
+  int32_t* res_len;
+  int32_t* res_valid;
+  // fetch (D2H once per epoch): history i64[8,B] then control i32[6+4B+2+B]
+  uint8_t* fetch;
+};
+
+// Inputs of one decoder step (the 9-input decoder ABI, resolved to device
+// pointers) plus the step's outputs.
+struct StepPtrs {
+  const int64_t* token;
+  const int64_t* pos;
+  const int32_t* len;
+  const int32_t* slot;
+  const int32_t* active;
+  const int32_t* table;
+  void* key_cache;
+  void* value_cache;
+  float* logits;          // [B, V]
+  int64_t* next_pos;      // [B] (nullptr: not written)
+  const int32_t* done;    // early-exit flag (nullptr: always run)
+};
+
+// Activation and scratch buffers of one engine.
+struct Scratch {
+  void* hidden;       // T [B, H] residual stream
+  void* q;            // T [B, NH*d] post-RoPE queries
+  void* attn;         // T [B, NH*d]
+  void* mlp;          // T [B, I]
+  float* partial;     // K-segment partial sums [segments, B, H]
+  float* am_val;      // argmax partial values [nwg, B]
+  int32_t* am_idx;    // argmax partial indices [nwg, B]
+  int32_t* am_bad;    // non-finite flags [nwg, B]
+  float* inv_freq;    // fp32 [d/2]
+};
+
+struct LaunchPlan {
+  int mb;          // batch rows per GEMV pass (4 or 8)
+  int row_tiles;   // ceil(B / mb)
+  int waves;       // waves per GEMV workgroup
+  int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
+  int o_segments, down_segments;  // K-segments of 3584 elements
+  int lm_wg;       // workgroups of the LM head (= argmax partial count)
+};
+
+// Arguments of the paged decode attention (re_attn.hip).
+struct AttnArgs {
+  const int32_t* done;
+  const void* q;           // T [B, NH*d]
+  const void* key_cache;   // this layer [slots, KVH, d]
+  const void* value_cache;
+  const int32_t* len;
+  const int32_t* table;    // [B, BPR]
+  void* out;               // T [B, NH*d]
+  int B, heads, kv_heads, head_dim, block_size, blocks_per_row, window;
+  long long slots;
+};
+size_t attention_lds_bytes(const Dims& d);
+hipError_t prepare_attention(const Dims& d);
+hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream);
+
+// LDS bytes of the projection kernels and their K-segment length (re_step.hip).
+size_t normed_lds_bytes(int mb, int hidden, int dtype_bytes, int waves);
+size_t resid_lds_bytes(int mb, int dtype_bytes, int waves);
+int k_segment_elems();
+
+// ---- kernel launchers (re_kernels.hip) ----
+struct KernelEnv {
+  Dims dims;
+  LaunchPlan plan;
+  const uint8_t* weights;  // arena base
+  const LayerOffsets* layer_off;  // host array [layers]
+  size_t embedding_off, final_norm_off, lm_head_off;
+  Scratch scratch;
+};
+
+// One decoder step: embedding, L layers, final norm + LM head with argmax
+// partials.  The step is an indexed list of launches; launch_step_ops runs the
+// range [begin, end) of it (re_step.hip).
+hipError_t launch_decoder_step(const KernelEnv& env, const StepPtrs& step, hipStream_t stream);
+hipError_t launch_step_ops(const KernelEnv& env, const StepPtrs& step, hipStream_t stream, int begin, int end);
+int step_op_count(const KernelEnv& env);
+int gateup_op_index(int layer);
+// Grid sizes of the grid-stride projections from the kernels' occupancy.
+void plan_grids(LaunchPlan& p, const Dims& d, int cus);
+// Controller kernels.
+hipError_t launch_ctrl_init(const KernelEnv& env, const StatePtrs& st, int has_payload,
+                            hipStream_t stream);
+hipError_t launch_clear_rows(const KernelEnv& env, const StatePtrs& st, void* key_cache,
+                             void* value_cache, hipStream_t stream);
+hipError_t launch_ctrl_step(const KernelEnv& env, const StatePtrs& st, hipStream_t stream);
+hipError_t launch_ctrl_finish(const KernelEnv& env, const StatePtrs& st, hipStream_t stream);
+// Helpers for prefill / state management.
+hipError_t launch_clear_blocks(const KernelEnv& env, void* key_cache, void* value_cache,
+                               const int32_t* blocks, int nblocks, hipStream_t stream);
+hipError_t launch_fill_synthetic(void* dst, long long elems, int dtype_bytes, unsigned long long seed,
+                                 unsigned long long stream_id, float std_dev, hipStream_t stream);
+
+}  // namespace re
