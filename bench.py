@@ -181,7 +181,7 @@ def main() -> int:
         "d2h_copies_per_epoch": 1,
         "roofline": {
             "bound": "hbm",
-            "kernel": "gate/up projection (k_normed<bf16,4,4,GateUp>)",
+            "kernel": "gate/up projection (k_proj<bf16,4,4,GateUp>)",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -42,15 +42,18 @@ def hipcc() -> str:
     return found
 
 
-def build(verbose: bool = False) -> Path:
-    LIBDIR.mkdir(parents=True, exist_ok=True)
-    build_dir = PACKAGE / "_build"
-    build_dir.mkdir(exist_ok=True)
+def build(verbose: bool = False, defines: tuple[str, ...] = (), output: Path | None = None) -> Path:
+    """Compile the library.  ``defines`` are extra ``-D`` macros (tuning
+    variants such as ``NORMED_MIN_WAVES=3``); ``output`` another .so path."""
+    library = Path(output) if output is not None else LIBRARY
+    library.parent.mkdir(parents=True, exist_ok=True)
+    build_dir = PACKAGE / "_build" / (library.stem if output is not None else "default")
+    build_dir.mkdir(parents=True, exist_ok=True)
     objects = []
 
     def compile_one(src: str) -> Path:
         obj = build_dir / (Path(src).stem + ".o")
-        cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr[-6000:]}")
@@ -63,13 +66,13 @@ def build(verbose: bool = False) -> Path:
 
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
         objects = list(pool.map(compile_one, SOURCES))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+    tmp = library.with_suffix(".so.tmp")
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, library)
+    return library
 
 
 if __name__ == "__main__":

@@ -67,10 +67,22 @@ __device__ __forceinline__ void store_tile(const Vec8<T> (&v)[NPT], T* tile) {
   }
 }
 
+// Tiles gi*kGroupTiles .. +kGroupTiles-1 (those below ntiles) into registers.
+constexpr int kGroupTiles = 4;
+
+template <typename T, int D, int NPT>
+__device__ __forceinline__ void load_group(Vec8<T> (&v)[kGroupTiles][NPT], const T* cache, const int32_t* tab, int gi,
+                                           int ntiles, int neff, const AttnArgs& a, int g) {
+#pragma unroll
+  for (int tt = 0; tt < kGroupTiles; ++tt) {
+    const int t = gi * kGroupTiles + tt;
+    if (t < ntiles) load_tile<T, D>(v[tt], cache, tab, t * kTile, neff, a, g);
+  }
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) k_attn(AttnArgs a) {
   using S = AttnShape<T, D>;
-  if (a.done != nullptr && __builtin_nontemporal_load(a.done) != 0) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int G = a.heads / a.kv_heads, W = a.window;
   float* qs = reinterpret_cast<float*>(smem_raw);   // [G, D]
@@ -87,43 +99,52 @@ __global__ void __launch_bounds__(kThreads) k_attn(AttnArgs a) {
   const T* VC = static_cast<const T*>(a.value_cache);
   const int32_t* tab = a.table + (size_t)b * a.blocks_per_row;
 
-  // One round trip: query heads, first key tile, first value tile.
+  // One round trip: query heads and the keys and values of the first
+  // kGroupTiles tiles (256 positions) are requested together.
   Vec8<T> qv = Vec8<T>{};
   const int qvecs = G * D / 8;
   if (tid < qvecs) qv = Vec8<T>::load_cached(Q + tid * 8);
-  Vec8<T> kr[S::kPerThread], vr[S::kPerThread];
-  load_tile<T, D>(kr, KC, tab, 0, neff, a, g);
-  load_tile<T, D>(vr, VC, tab, 0, neff, a, g);
+  Vec8<T> kr[kGroupTiles][S::kPerThread], vr[kGroupTiles][S::kPerThread];
+  load_group<T, D>(kr, KC, tab, 0, ntiles, neff, a, g);
+  load_group<T, D>(vr, VC, tab, 0, ntiles, neff, a, g);
+  if (a.done != nullptr && __builtin_nontemporal_load(a.done) != 0) return;  // read while loads fly
   if (tid < qvecs) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) qs[tid * 8 + e] = qv.get(e);
   }
   const float scale_div = sqrtf(static_cast<float>(D));
+  const int ngroups = (ntiles + kGroupTiles - 1) / kGroupTiles;
   // Pass 1: scores of every tile.
-  for (int t = 0; t < ntiles; ++t) {
-    store_tile<T, D>(kr, kt);
-    __syncthreads();
-    if (t + 1 < ntiles) load_tile<T, D>(kr, KC, tab, (t + 1) * kTile, neff, a, g);
-    const int t0 = t * kTile;
-    for (int p = tid; p < G * kTile; p += kThreads) {
-      const int h = p / kTile, jj = p - h * kTile, j = t0 + jj;
-      if (j < neff) {
-        const T* krow = kt + jj * S::kRow;
-        const float* qrow = qs + h * D;
-        float s = 0.f;
+  for (int gi = 0; gi < ngroups; ++gi) {
+    if (gi > 0) load_group<T, D>(kr, KC, tab, gi, ntiles, neff, a, g);
 #pragma unroll
-        for (int c = 0; c < S::kVecRow; ++c) {
-          const Vec8<T> k8 = Vec8<T>::load_cached(krow + c * 8);
+    for (int tt = 0; tt < kGroupTiles; ++tt) {
+      const int t = gi * kGroupTiles + tt;
+      if (t < ntiles) {
+        store_tile<T, D>(kr[tt], kt);
+        __syncthreads();
+        const int t0 = t * kTile;
+        for (int p = tid; p < G * kTile; p += kThreads) {
+          const int h = p / kTile, jj = p - h * kTile, j = t0 + jj;
+          if (j < neff) {
+            const T* krow = kt + jj * S::kRow;
+            const float* qrow = qs + h * D;
+            float s = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) s = fmaf(qrow[c * 8 + e], k8.get(e), s);
+            for (int c = 0; c < S::kVecRow; ++c) {
+              const Vec8<T> k8 = Vec8<T>::load_cached(krow + c * 8);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) s = fmaf(qrow[c * 8 + e], k8.get(e), s);
+            }
+            if constexpr (sizeof(T) == 2) s = round_bf16(s);  // ExactQk output is bf16
+            s = round_bf16(s / scale_div);
+            if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
+            sc[h * W + j] = s;
+          }
         }
-        if constexpr (sizeof(T) == 2) s = round_bf16(s);  // ExactQk output is bf16
-        s = round_bf16(s / scale_div);
-        if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
-        sc[h * W + j] = s;
+        __syncthreads();
       }
     }
-    __syncthreads();
   }
   // Softmax per head (fp32), probabilities rounded to bf16.
   for (int h = wave; h < G; h += nwaves) {
@@ -142,19 +163,25 @@ __global__ void __launch_bounds__(kThreads) k_attn(AttnArgs a) {
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();  // scores final / previous tile consumed
-    store_tile<T, D>(vr, kt);
-    __syncthreads();
-    if (t + 1 < ntiles) load_tile<T, D>(vr, VC, tab, (t + 1) * kTile, neff, a, g);
-    const int t0 = t * kTile;
-    const int tn = min(kTile, neff - t0);
-    for (int jj = 0; jj < tn; ++jj) {
-      const float v = Elt<T>::f(kt[jj * S::kRow + dd]);
+  for (int gi = 0; gi < ngroups; ++gi) {
+    if (gi > 0) load_group<T, D>(vr, VC, tab, gi, ntiles, neff, a, g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int h = part + i * kSplit;
-        if (i * kSplit < 8 && h < G) acc[i] = fmaf(sc[h * W + t0 + jj], v, acc[i]);
+    for (int tt = 0; tt < kGroupTiles; ++tt) {
+      const int t = gi * kGroupTiles + tt;
+      if (t < ntiles) {
+        __syncthreads();  // scores final / previous tile consumed
+        store_tile<T, D>(vr[tt], kt);
+        __syncthreads();
+        const int t0 = t * kTile;
+        const int tn = min(kTile, neff - t0);
+        for (int jj = 0; jj < tn; ++jj) {
+          const float v = Elt<T>::f(kt[jj * S::kRow + dd]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int h = part + i * kSplit;
+            if (i * kSplit < 8 && h < G) acc[i] = fmaf(sc[h * W + t0 + jj], v, acc[i]);
+          }
+        }
       }
     }
   }

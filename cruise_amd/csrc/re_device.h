@@ -156,6 +156,15 @@ __device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
   for (; mask >= 1; mask >>= 1) v[0] += __shfl_xor(v[0], mask, 64);
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also orders global
+// memory, so it waits for every global load in flight; this one lets weight
+// loads issued before it stay in flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);

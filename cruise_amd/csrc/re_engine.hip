@@ -211,8 +211,10 @@ bool make_plan(Engine& e, const Json& cfg) {
   p.mb = d.batch <= 4 ? 4 : 8;
   p.row_tiles = (d.batch + p.mb - 1) / p.mb;
   p.waves = 4;
-  // Normed projections hold the whole hidden row in one K-segment.
-  if (d.hidden > k_segment_elems()) return false;
+  // Normed projections hold the whole hidden row in one K-segment; the row
+  // kernels hold it as one 8-element vector per thread.
+  if (d.hidden > k_segment_elems() || d.hidden > row_kernel_max_hidden() || d.hidden % 8 != 0) return false;
+  if (d.head_dim % 2 != 0) return false;
   const size_t normed_lds = normed_lds_bytes(p.mb, d.hidden, d.dtype_bytes, p.waves);
   if (normed_lds > 64 * 1024 || resid_lds_bytes(p.mb, d.dtype_bytes, p.waves) > 64 * 1024) return false;
   if (attention_lds_bytes(d) > 160 * 1024 || prepare_attention(d) != hipSuccess) return false;
@@ -344,6 +346,8 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.am_idx), (size_t)p.lm_wg * B * sizeof(int32_t)},
       {reinterpret_cast<void**>(&e.scratch.am_bad), (size_t)p.lm_wg * B * sizeof(int32_t)},
       {reinterpret_cast<void**>(&e.scratch.inv_freq), (size_t)d.head_dim / 2 * sizeof(float)},
+      {&e.scratch.xn, (size_t)B * d.hidden * T},
+      {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},
   };

@@ -120,6 +120,8 @@ struct Scratch {
   int32_t* am_idx;    // argmax partial indices [nwg, B]
   int32_t* am_bad;    // non-finite flags [nwg, B]
   float* inv_freq;    // fp32 [d/2]
+  void* xn;           // T [B, H] normalized input of the next projection
+  float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
 };
 
 struct LaunchPlan {
@@ -151,6 +153,8 @@ hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream
 size_t normed_lds_bytes(int mb, int hidden, int dtype_bytes, int waves);
 size_t resid_lds_bytes(int mb, int dtype_bytes, int waves);
 int k_segment_elems();
+// Largest hidden size of the row kernels (embed+norm, residual reduce+norm).
+int row_kernel_max_hidden();
 
 // ---- kernel launchers (re_kernels.hip) ----
 struct KernelEnv {

@@ -1,28 +1,43 @@
 // Decoder-step kernels of the resident decode epoch (gfx950).
 //
 // A decoder step (batched_decoder_step.py:277-417) runs as
-//   embed -> L x [qkv | attention | o-proj | gate/up | down (+reduce)] -> LM head.
+//   embed+norm -> L x [qkv | attention | o-proj | reduce+norm | gate/up |
+//   down | reduce+norm] -> LM head.
 //
 // Every projection is a weight-streaming skinny GEMM: M = batch rows (4 at the
 // reference geometry) against an [N, K] weight read exactly once.  A wave owns
 // two weight rows over one K-segment of up to 7 x 512 elements (3584: all of
 // Qwen2.5-7B's hidden size) and issues all 14 of its 16-byte non-temporal loads
-// before touching them -- before the prologue, too -- so one HBM round trip
-// covers a whole row pair.  Activations sit in LDS; bf16 pairs go through
-// v_dot2 into fp32 accumulators; the 64 lanes are combined by a halving
-// exchange.  Norms, RoPE, the paged slot write, SwiGLU, the residual adds and
-// the argmax partials are fused into prologues and epilogues; rounding points
-// follow the reference decoder (see the per-kernel comments).
+// before touching them, so one HBM round trip covers a whole row pair; the
+// first pair is requested before the workgroup stages its activations.
+// Activations sit in LDS; bf16 pairs go through v_dot2 into fp32
+// accumulators; the 64 lanes are combined by a halving exchange.
+//
+// RMSNorm needs a whole hidden row, so it runs once per row in the small
+// row kernels (embedding gather, residual reduce) that precede each normed
+// projection; they write the normalized activations ``xn`` the projections
+// read.  RoPE cos/sin are tabulated once per step.  RoPE, the paged slot
+// write, SwiGLU and the argmax partials are fused into the projection
+// epilogues; rounding points follow the reference decoder (see the
+// per-kernel comments).
 #include "re_device.h"
 #include "re_layout.h"
 
 namespace re {
 namespace {
 
+// Minimum waves per SIMD the bf16 projections are compiled for (register
+// budget 512 / NORMED_MIN_WAVES per lane): four resident waves per SIMD with
+// one row pair in flight each keep HBM busy.
+#ifndef NORMED_MIN_WAVES
+#define NORMED_MIN_WAVES 4
+#endif
+
 constexpr int kRowsPerWave = 2;
 constexpr int kChunk = 512;     // elements covered by one wave-wide 16-byte load
 constexpr int kSegChunks = 7;   // chunks per K-segment
 constexpr int kSeg = kChunk * kSegChunks;
+constexpr int kRowThreads = 512;  // row kernels: one Vec8 of a 3584 row per thread
 
 __device__ __forceinline__ bool skip_step(const int32_t* done) {
   return done != nullptr && __builtin_nontemporal_load(done) != 0;
@@ -30,7 +45,8 @@ __device__ __forceinline__ bool skip_step(const int32_t* done) {
 
 // Issue the loads of RPW weight rows over the segment [k0, k0 + len): chunk c
 // of lane l covers elements k0 + c*512 + l*8 .. +8.  Chunks past len are zero.
-template <typename T, int RPW>
+// FULL: the segment holds all kSegChunks chunks (len == kSeg), no guards.
+template <typename T, int RPW, bool FULL = false>
 __device__ __forceinline__ void load_rows(Vec8<T> (&w)[kSegChunks][RPW], const T* const (&wr)[RPW], int k0,
                                           int len, int lane) {
 #pragma unroll
@@ -38,7 +54,7 @@ __device__ __forceinline__ void load_rows(Vec8<T> (&w)[kSegChunks][RPW], const T
     const int k = c * kChunk + lane * 8;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      if (k < len)
+      if (FULL || k < len)
         w[c][r] = Vec8<T>::load(wr[r] + k0 + k);
       else
         w[c][r] = Vec8<T>{};
@@ -47,13 +63,13 @@ __device__ __forceinline__ void load_rows(Vec8<T> (&w)[kSegChunks][RPW], const T
 }
 
 // acc[r][m] += sum over the segment of W_r[k] * xs[m][k] (xs: LDS, row stride ldx).
-template <typename T, int MB, int RPW>
+template <typename T, int MB, int RPW, bool FULL = false>
 __device__ __forceinline__ void dot_rows(const Vec8<T> (&w)[kSegChunks][RPW], const T* xs, int ldx, int len,
                                          int lane, float (&acc)[RPW][MB]) {
 #pragma unroll
   for (int c = 0; c < kSegChunks; ++c) {
     const int k = c * kChunk + lane * 8;
-    if (k < len) {
+    if (FULL || k < len) {
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
         const Vec8<T> x = Vec8<T>::load_cached(xs + m * ldx + k);
@@ -79,9 +95,6 @@ __device__ __forceinline__ void wave_totals(float (&acc)[RPW][MB], int lane, flo
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 }
 
-// RMSNorm of rows b0..b0+MB-1 of hidden [B, H] into LDS xs [MB, H]
-// (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
-// cast to T, then a T x T product with the weight.  Rows >= B are zero.
 // Vec8 slots a 256-thread workgroup needs to hold MB rows of one K-segment.
 template <int MB>
 constexpr int seg_vecs_per_thread() {
@@ -104,83 +117,146 @@ __device__ __forceinline__ void load_rows_block(Vec8<T> (&v)[seg_vecs_per_thread
   }
 }
 
-// RMSNorm of rows b0..b0+MB-1 of hidden [B, H] into LDS xs [MB, H]
-// (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
-// cast to T, then a T x T product with the weight.  Rows >= B are zero.
-// Requires blockDim.x == 256 and H <= kSeg.
+// Store the block loaded by load_rows_block into LDS xs [MB, ldx], then a
+// workgroup barrier.
 template <typename T, int MB>
-__device__ void rmsnorm_to_lds(const T* __restrict__ hidden, int b0, int B, const T* __restrict__ w, int H,
-                               float eps, T* xs, float* red) {
+__device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per_thread<MB>()], int len, T* xs,
+                                                 int ldx) {
   constexpr int NV = seg_vecs_per_thread<MB>();
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int per_row = H / 8;
-  Vec8<T> hv[NV], wv[NV];
-  load_rows_block<T, MB>(hv, hidden, H, b0, B, 0, H);
+  const int per_row = len / 8;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = tid + 256 * i;
-    wv[i] = Vec8<T>{};
-    if (idx < MB * per_row) wv[i] = Vec8<T>::load_cached(w + (idx % per_row) * 8);
-  }
-  float ss[MB];
-#pragma unroll
-  for (int m = 0; m < MB; ++m) ss[m] = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = tid + 256 * i;
-    const int row = idx / per_row;
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = hv[i].get(e);
-      s = fmaf(x, x, s);
-    }
-#pragma unroll
-    for (int m = 0; m < MB; ++m)
-      if (row == m) ss[m] += s;
-  }
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    const float s = wave_sum(ss[m]);
-    if (lane == 0) red[wave * MB + m] = s;
-  }
-  __syncthreads();
-  float rs[MB];
-  const int nw = blockDim.x >> 6;
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    float s = 0.f;
-    for (int i = 0; i < nw; ++i) s += red[i * MB + m];
-    rs[m] = rsqrtf(s / static_cast<float>(H) + eps);
-  }
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = tid + 256 * i;
+    const int idx = threadIdx.x + 256 * i;
     if (idx < MB * per_row) {
-      const int row = idx / per_row, k = (idx - row * per_row) * 8;
-      float r = 0.f;
-#pragma unroll
-      for (int m = 0; m < MB; ++m)
-        if (row == m) r = rs[m];
-      float out[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        out[e] = b0 + row < B ? Elt<T>::r(Elt<T>::r(hv[i].get(e) * r) * wv[i].get(e)) : 0.f;
-      *reinterpret_cast<Vec8<T>*>(xs + row * H + k) = Vec8<T>::from_floats(out);
+      const int m = idx / per_row, k = (idx - m * per_row) * 8;
+      *reinterpret_cast<Vec8<T>*>(xs + m * ldx + k) = v[i];
     }
   }
-  __syncthreads();
+  lds_barrier();  // weight loads issued before the staging stay in flight
 }
 
 // ---------------------------------------------------------------------------
-// Normed projections: RMSNorm prologue + skinny GEMM + fused epilogue.
+// Row kernels: one workgroup of kRowThreads per batch row, thread t owning
+// elements 8t .. 8t+7 of the hidden row (H <= 8 * kRowThreads).
 // ---------------------------------------------------------------------------
-enum NormedKind { kQkv = 0, kGateUp = 1, kLmHead = 2 };
 
-struct NormedArgs {
+// RMSNorm of one hidden row held as eight values per thread
+// (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
+// cast to T, then a T x T product with the weight.  Writes xn[8t .. 8t+7].
+template <typename T>
+__device__ __forceinline__ void row_rmsnorm(const float (&h)[8], bool has, const T* __restrict__ norm_w, T* xn,
+                                            int H, float eps, float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  Vec8<T> wv = Vec8<T>{};
+  if (has) wv = Vec8<T>::load_cached(norm_w + tid * 8);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(h[e], h[e], ss);
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float total = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) total += red[i];
+  const float rs = rsqrtf(total / static_cast<float>(H) + eps);
+  if (has) {
+    float out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = Elt<T>::r(Elt<T>::r(h[e] * rs) * wv.get(e));
+    *reinterpret_cast<Vec8<T>*>(xn + tid * 8) = Vec8<T>::from_floats(out);
+  }
+}
+
+struct RowArgs {
   const int32_t* done;
-  const void* hidden;     // T [B, H]
-  const void* norm_w;     // T [H]
+  // embed: token ids, embedding table; reduce: fp32 partials [segments, B, H]
+  const int64_t* token;
+  const void* embedding;
+  const float* partial;
+  int segments;
+  void* hidden;          // T [B, H] residual stream
+  const void* norm_w;    // T [H] weight of the norm that follows
+  void* xn;              // T [B, H] normalized activations
+  // embed only: the step's RoPE table
+  const int64_t* pos;
+  const float* inv_freq;  // [d/2]
+  float* rope;            // [B, d/2, 2] cos, sin (rounded to T)
+  int B, H, V, half;
+  float eps;
+};
+
+// Embedding gather (batched_decoder_step.py:289-291), the step's RoPE table
+// (DEC:235-240: fp32 angle pos * inv_freq, cos/sin cast to T; one table for
+// every layer, as DEC computes it once per step) and layer 0's input norm.
+template <typename T>
+__global__ void __launch_bounds__(kRowThreads) k_embed_norm(RowArgs a) {
+  __shared__ float red[kRowThreads / 64];
+  if (skip_step(a.done)) return;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  long long t = a.token[b];
+  if (t < 0 || t >= a.V) t = 0;  // the controller rejects such ids (CTRL:356); reads stay in bounds
+  const bool has = tid * 8 < a.H;
+  Vec8<T> ev = Vec8<T>{};
+  if (has) ev = Vec8<T>::load_cached(static_cast<const T*>(a.embedding) + (size_t)t * a.H + tid * 8);
+  for (int j = tid; j < a.half; j += blockDim.x) {
+    const float ang = static_cast<float>(a.pos[b]) * a.inv_freq[j];
+    a.rope[((size_t)b * a.half + j) * 2] = Elt<T>::r(cosf(ang));
+    a.rope[((size_t)b * a.half + j) * 2 + 1] = Elt<T>::r(sinf(ang));
+  }
+  float h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = ev.get(e);
+  T* hid = static_cast<T*>(a.hidden) + (size_t)b * a.H;
+  if (has) *reinterpret_cast<Vec8<T>*>(hid + tid * 8) = ev;
+  row_rmsnorm<T>(h, has, static_cast<const T*>(a.norm_w), static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps,
+                 red);
+}
+
+// Residual add of a projection and the norm of the next one: the segment
+// partials are summed in segment order (deterministic), rounded to T (the
+// projection output; Bf16Materialize is the identity), added to the residual
+// in T (batched_decoder_step.py:380-386, 399-403), then normalized.
+template <typename T>
+__global__ void __launch_bounds__(kRowThreads) k_resid_norm(RowArgs a) {
+  __shared__ float red[kRowThreads / 64];
+  if (skip_step(a.done)) return;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const bool has = tid * 8 < a.H;
+  T* hid = static_cast<T*>(a.hidden) + (size_t)b * a.H;
+  float h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = 0.f;
+  if (has) {
+    const Vec8<T> hv = Vec8<T>::load_cached(hid + tid * 8);
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = 0.f;
+    for (int sp = 0; sp < a.segments; ++sp) {
+      const re_f32x4* p = reinterpret_cast<const re_f32x4*>(a.partial + ((size_t)sp * a.B + b) * a.H + tid * 8);
+      const re_f32x4 lo = p[0], hi = p[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[e] += lo[e];
+        s[e + 4] += hi[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = Elt<T>::r(hv.get(e) + Elt<T>::r(s[e]));
+    *reinterpret_cast<Vec8<T>*>(hid + tid * 8) = Vec8<T>::from_floats(h);
+  }
+  row_rmsnorm<T>(h, has, static_cast<const T*>(a.norm_w), static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps,
+                 red);
+}
+
+// ---------------------------------------------------------------------------
+// Projections of the normalized activations: skinny GEMM + fused epilogue.
+// Workgroup g owns the contiguous unit range [g*per, (g+1)*per) (per = iters
+// x waves), so each workgroup's outputs (logits, mlp) form whole lines.
+// ---------------------------------------------------------------------------
+enum ProjKind { kQkv = 0, kGateUp = 1, kLmHead = 2 };
+
+struct ProjArgs {
+  const int32_t* done;
+  const void* xn;         // T [B, H]
   const void* w0;         // qkv: stacked [qkv_rows, H]; gate/up: gate [I, H]; lm: [V, H]
   const void* w1;         // gate/up: up [I, H]; qkv: bias [qkv_rows]
   void* out;              // qkv: q [B, NH*d]; gate/up: mlp [B, I]
@@ -189,22 +265,21 @@ struct NormedArgs {
   int32_t* am_idx;
   int32_t* am_bad;
   // qkv epilogue
-  const int64_t* pos;
+  const float* rope;      // [B, d/2, 2]
   const int32_t* slot;
   const int32_t* active;
   void* key_cache;        // this layer: [slots, KVH, d]
   void* value_cache;
-  const float* inv_freq;  // [d/2]
   long long slots;
   int B, H, units, heads, kv_heads, head_dim;
-  float eps;
 };
 
 template <int KIND, typename T>
-__device__ __forceinline__ void normed_rows(const NormedArgs& a, int u, const T* W0, const T* W1,
-                                            const T* (&wr)[kRowsPerWave], int& row0, int& row1) {
+__device__ __forceinline__ void proj_rows(const ProjArgs& a, int u, const T* W0, const T* W1,
+                                          const T* (&wr)[kRowsPerWave], int& row0, int& row1) {
   const int H = a.H;
   if constexpr (KIND == kQkv) {
+    // rows j and j + d/2 of one head: the RoPE pair
     const int half = a.head_dim >> 1;
     const int hg = u / half, j = u - hg * half;
     row0 = hg * a.head_dim + j;
@@ -223,9 +298,9 @@ __device__ __forceinline__ void normed_rows(const NormedArgs& a, int u, const T*
   }
 }
 
-template <typename T, int MB, int WAVES, int KIND>
-__global__ void __launch_bounds__(WAVES * 64) k_normed(NormedArgs a) {
-  if (skip_step(a.done)) return;
+template <typename T, int MB, int WAVES, int KIND, bool FULL>
+__global__ void __launch_bounds__(WAVES * 64, (sizeof(T) == 2 && MB == 4) ? NORMED_MIN_WAVES : 2)
+    k_proj(ProjArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* xs = reinterpret_cast<T*>(smem_raw);
   float* red = reinterpret_cast<float*>(smem_raw + (size_t)MB * a.H * sizeof(T));
@@ -235,30 +310,45 @@ __global__ void __launch_bounds__(WAVES * 64) k_normed(NormedArgs a) {
   const T* W0 = static_cast<const T*>(a.w0);
   const T* W1 = static_cast<const T*>(a.w1);
   float* wred = red + wave * (kRowsPerWave * MB);
-  const int stride = gridDim.x * WAVES;
-  int u = blockIdx.x * WAVES + wave;
+  const int iters = (a.units + gridDim.x * WAVES - 1) / (gridDim.x * WAVES);
+  const int u_end = min((int)(blockIdx.x + 1) * iters * WAVES, a.units);
+  int u = blockIdx.x * iters * WAVES + wave;
 
-  // The first row pair's weights are requested before the prologue.
+  // The early-exit flag, the activations and the first row pair are
+  // requested together, in that order (loads complete in issue order, so
+  // the activations can be staged while the weights are still in flight).
+  // The flag is uniform: the workgroup leaves together, after the barrier.
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  Vec8<T> xv[seg_vecs_per_thread<MB>()];
+  load_rows_block<T, MB>(xv, static_cast<const T*>(a.xn), H, b0, a.B, 0, H);
+  // Unconditional (a wave past its range loads a valid pair it never uses):
+  // with no branch around them the waits below count exactly these 14 loads.
   Vec8<T> w[kSegChunks][kRowsPerWave];
   const T* wr[kRowsPerWave];
   int row0 = 0, row1 = 0;
-  if (u < a.units) {
-    normed_rows<KIND, T>(a, u, W0, W1, wr, row0, row1);
-    load_rows<T, kRowsPerWave>(w, wr, 0, H, lane);
-  }
-  rmsnorm_to_lds<T, MB>(static_cast<const T*>(a.hidden), b0, a.B, static_cast<const T*>(a.norm_w), H, a.eps, xs,
-                        red);
+  proj_rows<KIND, T>(a, min(u, a.units - 1), W0, W1, wr, row0, row1);
+  load_rows<T, kRowsPerWave, FULL>(w, wr, 0, H, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  store_rows_block<T, MB>(xv, H, xs, H);
+  if (stop != 0) return;
   // argmax running state of lane m < MB (batch row b0+m), LM head only
   float best_v = 0.f;
   int best_i = -1;
   int bad = 0;
-  auto process = [&](const Vec8<T>(&wv)[kSegChunks][kRowsPerWave], int u, int row0, int row1) {
+  while (u < u_end) {
+    // One row pair per iteration, its 14 loads issued (before the loop or at
+    // the end of the previous iteration) before the first product waits; the
+    // barriers keep the scheduler from sinking them towards their uses.  The
+    // weights are dead during the epilogue, which keeps the register count at
+    // four waves per SIMD.
+    __builtin_amdgcn_sched_barrier(0);
     float acc[kRowsPerWave][MB];
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r)
 #pragma unroll
       for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
-    dot_rows<T, MB, kRowsPerWave>(wv, xs, H, H, lane, acc);
+    dot_rows<T, MB, kRowsPerWave, FULL>(w, xs, H, H, lane, acc);
+    const int cu = u, c0 = row0, c1 = row1;
     wave_totals<MB, kRowsPerWave>(acc, lane, wred);
     const int m = lane;
     if (m < MB && b0 + m < a.B) {
@@ -270,16 +360,15 @@ __global__ void __launch_bounds__(WAVES * 64) k_normed(NormedArgs a) {
         // rounding to T.  RoPE (batched_decoder_step.py:231-240, 323-324):
         // q' = q*cos + rotate_half(q)*sin, each product and the sum rounded to T.
         const T* bias = W1;
-        const float qa = Elt<T>::r(y0 + Elt<T>::f(bias[row0]));
-        const float qb = Elt<T>::r(y1 + Elt<T>::f(bias[row1]));
+        const float qa = Elt<T>::r(y0 + Elt<T>::f(bias[c0]));
+        const float qb = Elt<T>::r(y1 + Elt<T>::f(bias[c1]));
         const int half = a.head_dim >> 1;
-        const int hg = u / half, j = u - hg * half;
+        const int hg = cu / half, j = cu - hg * half;
         const int nq = a.heads, nkv = a.kv_heads;
         float oa = qa, ob = qb;
         if (hg < nq + nkv) {
-          const float ang = static_cast<float>(a.pos[b]) * a.inv_freq[j];
-          const float c = Elt<T>::r(cosf(ang));
-          const float s = Elt<T>::r(sinf(ang));
+          const float c = a.rope[((size_t)b * half + j) * 2];
+          const float s = a.rope[((size_t)b * half + j) * 2 + 1];
           oa = Elt<T>::r(Elt<T>::r(qa * c) + Elt<T>::r(-qb * s));
           ob = Elt<T>::r(Elt<T>::r(qb * c) + Elt<T>::r(qa * s));
         }
@@ -305,45 +394,31 @@ __global__ void __launch_bounds__(WAVES * 64) k_normed(NormedArgs a) {
         const float g = Elt<T>::r(y0);
         const float up = Elt<T>::r(y1);
         const float sg = Elt<T>::r(g / (1.0f + expf(-g)));
-        static_cast<T*>(a.out)[(size_t)b * a.units + u] = Elt<T>::t(Elt<T>::r(sg * up));
+        static_cast<T*>(a.out)[(size_t)b * a.units + cu] = Elt<T>::t(Elt<T>::r(sg * up));
       } else {
         // LM head in T, then .float() (batched_decoder_step.py:405-408); argmax
         // partials keep the first index of the maximum (CTRL:99-119).
         const float l0 = Elt<T>::r(y0);
         const float l1 = Elt<T>::r(y1);
         const int V = 2 * a.units;
-        a.logits[(size_t)b * V + row0] = l0;
-        a.logits[(size_t)b * V + row1] = l1;
+        a.logits[(size_t)b * V + c0] = l0;
+        a.logits[(size_t)b * V + c1] = l1;
         if (!isfinite(l0) || !isfinite(l1)) bad = 1;
         if (best_i < 0 || l0 > best_v) {
           best_v = l0;
-          best_i = row0;
+          best_i = c0;
         }
         if (l1 > best_v) {
           best_v = l1;
-          best_i = row1;
+          best_i = c1;
         }
       }
     }
-  };
-  // Double buffer: the next row pair's loads are issued before the current
-  // pair is consumed.  Unit indices past the end are clamped to the last unit,
-  // so every iteration issues its loads unconditionally (results unused).
-  Vec8<T> wb[kSegChunks][kRowsPerWave];
-  int rb0 = 0, rb1 = 0;
-  const int last = a.units - 1;
-  while (u < a.units) {
-    int un = u + stride;
-    normed_rows<KIND, T>(a, min(un, last), W0, W1, wr, rb0, rb1);
-    load_rows<T, kRowsPerWave>(wb, wr, 0, H, lane);
-    process(w, u, row0, row1);
-    u = un;
-    if (u >= a.units) break;
-    un = u + stride;
-    normed_rows<KIND, T>(a, min(un, last), W0, W1, wr, row0, row1);
-    load_rows<T, kRowsPerWave>(w, wr, 0, H, lane);
-    process(wb, u, rb0, rb1);
-    u = un;
+    u += WAVES;
+    if (u < u_end) {
+      proj_rows<KIND, T>(a, u, W0, W1, wr, row0, row1);
+      load_rows<T, kRowsPerWave, FULL>(w, wr, 0, H, lane);
+    }
   }
   if constexpr (KIND == kLmHead) {
     // Combine the waves of this workgroup; ties go to the lowest index.
@@ -379,103 +454,67 @@ __global__ void __launch_bounds__(WAVES * 64) k_normed(NormedArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Residual projections (o-proj, down-proj): h = h + T(x W^T).  Grid:
-// (row groups, K-segments, row tiles).  One segment: the residual epilogue
-// runs here.  Several segments: fp32 partials, combined by k_resid_reduce in a
-// fixed order (deterministic, no atomics).
+// Residual projections (o-proj, down-proj): fp32 partials x W^T per K-segment.
+// Grid: (row groups, K-segments, row tiles); k_resid_norm adds them to the
+// residual.
 // ---------------------------------------------------------------------------
 struct ResidArgs {
   const int32_t* done;
   const void* x;      // T [B, K]
   const void* w;      // T [N, K]
-  void* hidden;       // T [B, N]
   float* partial;     // [segments, B, N]
-  int B, N, K, segments;
+  int B, N, K;
 };
 
-template <typename T, int MB, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
-  if (skip_step(a.done)) return;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* xs = reinterpret_cast<T*>(smem_raw);  // [MB][kSeg]
-  float* red = reinterpret_cast<float*>(smem_raw + (size_t)MB * kSeg * sizeof(T));
+// The body for one segment kind: FULL segments (len == kSeg) need no guards.
+// Each kind is a complete path (loads, staging, products, stores), so the
+// waits of one path count only its own loads.
+template <typename T, int MB, int WAVES, bool FULL>
+__device__ __forceinline__ void resid_segment(const ResidArgs& a, T* xs, float* red, int seg, int len) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int seg = blockIdx.y, tile = blockIdx.z;
-  const int b0 = tile * MB;
+  const int b0 = blockIdx.z * MB;
   const int k0 = seg * kSeg;
-  const int len = min(a.K - k0, kSeg);
   const int u = blockIdx.x * WAVES + wave;  // rows 2u, 2u+1
   const int units = a.N / 2;
   const T* W = static_cast<const T*>(a.w);
-  Vec8<T> w[kSegChunks][kRowsPerWave];
-  if (u < units) {
-    const T* wr[kRowsPerWave] = {W + (size_t)(2 * u) * a.K, W + (size_t)(2 * u + 1) * a.K};
-    load_rows<T, kRowsPerWave>(w, wr, k0, len, lane);
-  }
-  // stage x[b0.., k0 : k0+len] into LDS: all loads first, then the stores
-  constexpr int NV = seg_vecs_per_thread<MB>();
-  Vec8<T> xv[NV];
+  // Flag, activations, then weights, as in k_proj; the weight loads are
+  // unconditional (clamped to a valid pair).
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  Vec8<T> xv[seg_vecs_per_thread<MB>()];
   load_rows_block<T, MB>(xv, static_cast<const T*>(a.x), a.K, b0, a.B, k0, len);
-  const int per_row = len / 8;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = tid + 256 * i;
-    if (idx < MB * per_row) {
-      const int m = idx / per_row, k = (idx - m * per_row) * 8;
-      *reinterpret_cast<Vec8<T>*>(xs + m * kSeg + k) = xv[i];
-    }
-  }
-  __syncthreads();
-  if (u >= units) return;
+  Vec8<T> w[kSegChunks][kRowsPerWave];
+  const int uc = min(u, units - 1);
+  const T* wr[kRowsPerWave] = {W + (size_t)(2 * uc) * a.K, W + (size_t)(2 * uc + 1) * a.K};
+  load_rows<T, kRowsPerWave, FULL>(w, wr, k0, len, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  store_rows_block<T, MB>(xv, len, xs, kSeg);
+  if (stop != 0 || u >= units) return;
   float acc[kRowsPerWave][MB];
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; ++r)
 #pragma unroll
     for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
-  dot_rows<T, MB, kRowsPerWave>(w, xs, kSeg, len, lane, acc);
+  dot_rows<T, MB, kRowsPerWave, FULL>(w, xs, kSeg, len, lane, acc);
   float* wred = red + wave * (kRowsPerWave * MB);
   wave_totals<MB, kRowsPerWave>(acc, lane, wred);
   if (lane >= MB || b0 + lane >= a.B) return;
   const int b = b0 + lane;
-  if (a.segments == 1) {
-    T* Hd = static_cast<T*>(a.hidden);
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
-      // o/down projection rounded to T (Bf16Materialize is the identity), then
-      // the residual add in T (batched_decoder_step.py:380-386, 399-403).
-      const size_t o = (size_t)b * a.N + 2 * u + r;
-      Hd[o] = Elt<T>::t(Elt<T>::f(Hd[o]) + Elt<T>::r(wred[r * MB + lane]));
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
-      a.partial[((size_t)seg * a.B + b) * a.N + 2 * u + r] = wred[r * MB + lane];
-  }
+  for (int r = 0; r < kRowsPerWave; ++r)
+    a.partial[((size_t)seg * a.B + b) * a.N + 2 * u + r] = wred[r * MB + lane];
 }
 
-// Sum of the segment partials in segment order, rounded to T, residual add.
-template <typename T>
-__global__ void k_resid_reduce(const int32_t* done, const float* partial, void* hidden, int B, int N,
-                               int segments) {
-  if (skip_step(done)) return;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B * N) return;
-  float s = 0.f;
-  for (int sp = 0; sp < segments; ++sp) s += partial[(size_t)sp * B * N + i];
-  T* Hd = static_cast<T*>(hidden);
-  Hd[i] = Elt<T>::t(Elt<T>::f(Hd[i]) + Elt<T>::r(s));
-}
-
-// ---------------------------------------------------------------------------
-// Embedding gather (batched_decoder_step.py:289-291).
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ void k_embed(const int32_t* done, const int64_t* token, const T* emb, T* hidden, int B, int H, int V) {
-  if (skip_step(done)) return;
-  const int b = blockIdx.x;
-  long long t = token[b];
-  if (t < 0 || t >= V) t = 0;  // the controller rejects such ids (CTRL:356); reads stay in bounds
-  for (int k = threadIdx.x; k < H; k += blockDim.x) hidden[(size_t)b * H + k] = emb[(size_t)t * H + k];
+template <typename T, int MB, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* xs = reinterpret_cast<T*>(smem_raw);  // [MB][kSeg]
+  float* red = reinterpret_cast<float*>(smem_raw + (size_t)MB * kSeg * sizeof(T));
+  const int seg = blockIdx.y;
+  const int len = min(a.K - seg * kSeg, kSeg);
+  if (len == kSeg)
+    resid_segment<T, MB, WAVES, true>(a, xs, red, seg, len);
+  else
+    resid_segment<T, MB, WAVES, false>(a, xs, red, seg, len);
 }
 
 }  // namespace
@@ -490,13 +529,22 @@ size_t resid_lds_bytes(int mb, int dtype_bytes, int waves) {
   return (size_t)mb * kSeg * dtype_bytes + (size_t)waves * mb * kRowsPerWave * sizeof(float);
 }
 int k_segment_elems() { return kSeg; }
+int row_kernel_max_hidden() { return 8 * kRowThreads; }
 
-// The step is a fixed list of launches: embed, then per layer
-// [qkv, attention, o-proj, o-reduce, gate/up, down, down-reduce], then the LM
-// head.  Reduce entries launch nothing when their projection has a single
-// K-segment.  [begin, end) selects a contiguous range of the list.
+// The step is a fixed list of launches: embed+norm, then per layer
+// [qkv, attention, o-proj, o-reduce+norm, gate/up, down, down-reduce+norm],
+// then the LM head.  [begin, end) selects a contiguous range of the list.
 constexpr int kOpsPerLayer = 7;
 constexpr int kGateUpOp = 4;
+
+// The guard-free instantiation serves hidden sizes of exactly one K-segment.
+template <typename T, int MB, int WAVES, int KIND>
+static void launch_proj(const ProjArgs& a, dim3 grid, size_t smem, hipStream_t stream) {
+  if (a.H == kSeg)
+    k_proj<T, MB, WAVES, KIND, true><<<grid, WAVES * 64, smem, stream>>>(a);
+  else
+    k_proj<T, MB, WAVES, KIND, false><<<grid, WAVES * 64, smem, stream>>>(a);
+}
 
 template <typename T, int MB>
 static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipStream_t stream, int begin,
@@ -513,29 +561,42 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     ++op;
     return w;
   };
-  if (want())
-    k_embed<T><<<B, 256, 0, stream>>>(st.done, st.token, reinterpret_cast<const T*>(env.weights + env.embedding_off),
-                                       static_cast<T*>(sc.hidden), B, d.hidden, d.vocab);
-  const size_t normed_smem = normed_lds_bytes(MB, d.hidden, sizeof(T), WAVES);
+  RowArgs row{};
+  row.done = st.done;
+  row.hidden = sc.hidden;
+  row.xn = sc.xn;
+  row.B = B;
+  row.H = d.hidden;
+  row.V = d.vocab;
+  row.half = d.head_dim / 2;
+  row.eps = d.rms_eps;
+  if (want()) {
+    RowArgs e = row;
+    e.token = st.token;
+    e.embedding = env.weights + env.embedding_off;
+    e.norm_w = env.weights + env.layer_off[0].input_norm;
+    e.pos = st.pos;
+    e.inv_freq = sc.inv_freq;
+    e.rope = sc.rope;
+    k_embed_norm<T><<<B, kRowThreads, 0, stream>>>(e);
+  }
+  const size_t proj_smem = normed_lds_bytes(MB, d.hidden, sizeof(T), WAVES);
   const size_t resid_smem = resid_lds_bytes(MB, sizeof(T), WAVES);
-  const int reduce_blocks = (B * d.hidden + 255) / 256;
   for (int l = 0; l < d.layers; ++l) {
     const LayerOffsets& lo = env.layer_off[l];
     T* kc = static_cast<T*>(st.key_cache) + l * cache_layer_elems;
     T* vc = static_cast<T*>(st.value_cache) + l * cache_layer_elems;
-    NormedArgs q{};
+    ProjArgs q{};
     q.done = st.done;
-    q.hidden = sc.hidden;
-    q.norm_w = env.weights + lo.input_norm;
+    q.xn = sc.xn;
     q.w0 = env.weights + lo.qkv_w;
     q.w1 = env.weights + lo.qkv_b;
     q.out = sc.q;
-    q.pos = st.pos;
+    q.rope = sc.rope;
     q.slot = st.slot;
     q.active = st.active;
     q.key_cache = kc;
     q.value_cache = vc;
-    q.inv_freq = sc.inv_freq;
     q.slots = d.slots();
     q.B = B;
     q.H = d.hidden;
@@ -543,8 +604,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     q.heads = d.heads;
     q.kv_heads = d.kv_heads;
     q.head_dim = d.head_dim;
-    q.eps = d.rms_eps;
-    if (want()) k_normed<T, MB, WAVES, kQkv><<<dim3(p.qkv_grid, p.row_tiles), WAVES * 64, normed_smem, stream>>>(q);
+    if (want()) launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
 
     AttnArgs at{};
     at.done = st.done;
@@ -571,52 +631,53 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     o.done = st.done;
     o.x = sc.attn;
     o.w = env.weights + lo.o_w;
-    o.hidden = sc.hidden;
     o.partial = sc.partial;
     o.B = B;
     o.N = d.hidden;
     o.K = d.q_dim();
-    o.segments = p.o_segments;
     if (want())
       k_resid<T, MB, WAVES><<<dim3(p.o_grid, p.o_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(o);
-    if (want() && p.o_segments > 1)
-      k_resid_reduce<T><<<reduce_blocks, 256, 0, stream>>>(st.done, sc.partial, sc.hidden, B, d.hidden,
-                                                            p.o_segments);
+    if (want()) {
+      RowArgs r = row;
+      r.partial = sc.partial;
+      r.segments = p.o_segments;
+      r.norm_w = env.weights + lo.post_norm;
+      k_resid_norm<T><<<B, kRowThreads, 0, stream>>>(r);
+    }
 
-    NormedArgs gu{};
+    ProjArgs gu{};
     gu.done = st.done;
-    gu.hidden = sc.hidden;
-    gu.norm_w = env.weights + lo.post_norm;
+    gu.xn = sc.xn;
     gu.w0 = env.weights + lo.gate_w;
     gu.w1 = env.weights + lo.up_w;
     gu.out = sc.mlp;
     gu.B = B;
     gu.H = d.hidden;
     gu.units = d.intermediate;
-    gu.eps = d.rms_eps;
-    if (want())
-      k_normed<T, MB, WAVES, kGateUp><<<dim3(p.gu_grid, p.row_tiles), WAVES * 64, normed_smem, stream>>>(gu);
+    if (want()) launch_proj<T, MB, WAVES, kGateUp>(gu, dim3(p.gu_grid, p.row_tiles), proj_smem, stream);
 
     ResidArgs dn{};
     dn.done = st.done;
     dn.x = sc.mlp;
     dn.w = env.weights + lo.down_w;
-    dn.hidden = sc.hidden;
     dn.partial = sc.partial;
     dn.B = B;
     dn.N = d.hidden;
     dn.K = d.intermediate;
-    dn.segments = p.down_segments;
     if (want())
       k_resid<T, MB, WAVES><<<dim3(p.down_grid, p.down_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(dn);
-    if (want() && p.down_segments > 1)
-      k_resid_reduce<T><<<reduce_blocks, 256, 0, stream>>>(st.done, sc.partial, sc.hidden, B, d.hidden,
-                                                            p.down_segments);
+    if (want()) {
+      // The next norm: layer l+1's input norm, or the final norm before the LM head.
+      RowArgs r = row;
+      r.partial = sc.partial;
+      r.segments = p.down_segments;
+      r.norm_w = env.weights + (l + 1 < d.layers ? env.layer_off[l + 1].input_norm : env.final_norm_off);
+      k_resid_norm<T><<<B, kRowThreads, 0, stream>>>(r);
+    }
   }
-  NormedArgs lm{};
+  ProjArgs lm{};
   lm.done = st.done;
-  lm.hidden = sc.hidden;
-  lm.norm_w = env.weights + env.final_norm_off;
+  lm.xn = sc.xn;
   lm.w0 = env.weights + env.lm_head_off;
   lm.logits = st.logits;
   lm.am_val = sc.am_val;
@@ -625,14 +686,13 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
   lm.B = B;
   lm.H = d.hidden;
   lm.units = d.vocab / 2;
-  lm.eps = d.rms_eps;
-  if (want()) k_normed<T, MB, WAVES, kLmHead><<<dim3(p.lm_grid, p.row_tiles), WAVES * 64, normed_smem, stream>>>(lm);
+  if (want()) launch_proj<T, MB, WAVES, kLmHead>(lm, dim3(p.lm_grid, p.row_tiles), proj_smem, stream);
   return hipGetLastError();
 }
 
-// Workgroups of each grid-stride projection: as many as are resident at once
-// (from the compiled kernels' occupancy), trimmed so every workgroup runs the
-// same number of row groups.
+// Workgroups of each projection: as many as are resident at once (from the
+// compiled kernels' occupancy), trimmed so every workgroup runs the same
+// number of row groups.
 template <typename T, int MB>
 static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
   constexpr int WAVES = 4;
@@ -646,9 +706,13 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
     const int iters = (groups + resident - 1) / resident;
     return (groups + iters - 1) / iters;
   };
-  p.qkv_grid = fit(k_normed<T, MB, WAVES, kQkv>, (d.qkv_rows() / 2 + WAVES - 1) / WAVES);
-  p.gu_grid = fit(k_normed<T, MB, WAVES, kGateUp>, (d.intermediate + WAVES - 1) / WAVES);
-  p.lm_grid = fit(k_normed<T, MB, WAVES, kLmHead>, (d.vocab / 2 + WAVES - 1) / WAVES);
+  const bool full = d.hidden == kSeg;
+  p.qkv_grid = fit(full ? k_proj<T, MB, WAVES, kQkv, true> : k_proj<T, MB, WAVES, kQkv, false>,
+                   (d.qkv_rows() / 2 + WAVES - 1) / WAVES);
+  p.gu_grid = fit(full ? k_proj<T, MB, WAVES, kGateUp, true> : k_proj<T, MB, WAVES, kGateUp, false>,
+                  (d.intermediate + WAVES - 1) / WAVES);
+  p.lm_grid = fit(full ? k_proj<T, MB, WAVES, kLmHead, true> : k_proj<T, MB, WAVES, kLmHead, false>,
+                  (d.vocab / 2 + WAVES - 1) / WAVES);
   p.lm_wg = p.lm_grid;
 }
 
