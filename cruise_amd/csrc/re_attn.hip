@@ -1,241 +1,262 @@
-// GQA paged decode attention of the resident decode epoch (gfx950), one
-// workgroup per (batch row, KV head) (batched_decoder_step.py:265-279, 334-379):
+// GQA paged decode attention of the resident decode epoch (gfx950)
+// (batched_decoder_step.py:265-279, 334-379), one workgroup per
+// (batch row, query head):
 //   window positions j < W gathered through the block table;
 //   s_j = bf16(bf16(q.k_j) / sqrt(d)) -- ExactQk is bf16-out; fp32 models keep
 //   the fp32 product, then the bf16 rounding of the scaled score;
 //   masked (j >= seq_len) positions contribute exp(bf16_min - max) = 0, so the
 //   softmax runs over j < min(seq_len, W); a row with seq_len <= 0 has every
 //   position masked and averages the whole window uniformly, as the reference;
-//   p = bf16(softmax_fp32(s)); o = T(sum_j p_j v_j) with fp32 accumulation.
+//   p = bf16(softmax_fp32(s)) over the whole window (global max and sum first,
+//   then each probability rounded); o = T(sum_j p_j v_j), fp32 accumulation.
 //
-// Positions are processed in tiles of 64: the query heads and the first tile's
-// keys and values are requested together (one memory round trip for the
-// common short context), key rows are staged in LDS with a 16-byte pad so the
-// per-lane row reads hit distinct banks, and the next tile's loads are issued
-// before the current tile is consumed.
+// Layout of the work: LPR = d/8 lanes share one key (or value) row, each
+// holding 8 of its elements, so one wave-wide 16-byte load covers 64/LPR whole
+// rows (contiguous 2d-byte runs of the cache).  A lane issues LPR such loads per
+// tile of 256 positions (4 waves x 64), then a halving exchange over its LPR
+// lanes leaves one complete score per lane.  The keys and values of the first
+// tile are requested together with the query at launch: one memory round
+// trip for contexts up to 256.  The 7 query heads that share a KV head are
+// placed on one XCD (block id = group + groups * head_in_group), so their
+// key/value reads hit the same L2.
 #include "re_device.h"
 #include "re_layout.h"
 
 namespace re {
 namespace {
 
-constexpr int kTile = 64;
 constexpr int kThreads = 256;
+constexpr int kTile = 256;  // positions per tile: 4 waves x 64
 
-template <typename T, int D>
+template <int D>
 struct AttnShape {
-  static constexpr int kVecRow = D / 8;                       // Vec8 per key/value row
-  static constexpr int kTileVecs = kTile * kVecRow;           // Vec8 per tile
-  static constexpr int kPerThread = (kTileVecs + kThreads - 1) / kThreads;
-  static constexpr int kPad = 16 / sizeof(T);                 // elements of padding per staged row
-  static constexpr int kRow = D + kPad;                       // staged row stride (elements)
+  static constexpr int kLpr = D / 8;         // lanes per row
+  static constexpr int kRg = 64 / kLpr;      // rows per wave-wide load
+  static constexpr int kLoads = kLpr;        // loads per lane per tile (64 rows per wave)
 };
 
-__device__ __forceinline__ long long window_slot(const int32_t* tab, int j, int block_size) {
-  return (long long)tab[j / block_size] * block_size + (j % block_size);
-}
-
-// Issue the loads of positions [t0, t0 + kTile) of one KV head (rows past
-// neff or outside the cache read as zero).
-template <typename T, int D, int NPT>
-__device__ __forceinline__ void load_tile(Vec8<T> (&v)[NPT], const T* cache, const int32_t* tab,
-                                          int t0, int neff, const AttnArgs& a, int g) {
-  using S = AttnShape<T, D>;
+// Halving exchange over the N lanes of a group (lane offset c = lane % N):
+// afterwards lane c holds the total over the group of value c.
+template <int N>
+__device__ __forceinline__ void group_reduce_transpose(float (&v)[N], int c) {
+  int mask = N >> 1;
 #pragma unroll
-  for (int i = 0; i < S::kPerThread; ++i) {
-    const int idx = threadIdx.x + kThreads * i;
-    const int jj = idx / S::kVecRow, c = idx - jj * S::kVecRow;
-    const int j = t0 + jj;
-    v[i] = Vec8<T>{};
-    if (idx < S::kTileVecs && j < neff) {
-      const long long slot = window_slot(tab, j, a.block_size);
-      if (slot >= 0 && slot < a.slots) v[i] = Vec8<T>::load_cached(cache + ((size_t)slot * a.kv_heads + g) * D + c * 8);
+  for (int n = N; n > 1; n >>= 1) {
+    const int h = n >> 1;
+    const bool upper = (c & mask) != 0;
+#pragma unroll
+    for (int i = 0; i < h; ++i) {
+      const float send = upper ? v[i] : v[i + h];
+      const float keep = upper ? v[i + h] : v[i];
+      v[i] = keep + __shfl_xor(send, mask, 64);
     }
+    mask >>= 1;
   }
 }
 
-template <typename T, int D, int NPT>
-__device__ __forceinline__ void store_tile(const Vec8<T> (&v)[NPT], T* tile) {
-  using S = AttnShape<T, D>;
+// Position of load i of lane group r in wave w of tile t.
+template <int D>
+__device__ __forceinline__ int tile_pos(int t, int w, int i, int r) {
+  return t * kTile + w * 64 + i * AttnShape<D>::kRg + r;
+}
+
+// Element offsets (within this layer's cache) of the rows of one tile this
+// lane loads: row chunk c of positions tile_pos(t, w, i, r); -1 where the
+// position is >= neff or its slot is outside the cache.  tabs: the row's
+// block table in LDS.
+template <int D>
+__device__ __forceinline__ void tile_offsets(int (&off)[AttnShape<D>::kLoads], const int* tabs, int t, int w,
+                                             int r, int c, int neff, const AttnArgs& a, int g) {
 #pragma unroll
-  for (int i = 0; i < S::kPerThread; ++i) {
-    const int idx = threadIdx.x + kThreads * i;
-    if (idx < S::kTileVecs) {
-      const int jj = idx / S::kVecRow, c = idx - jj * S::kVecRow;
-      *reinterpret_cast<Vec8<T>*>(tile + jj * S::kRow + c * 8) = v[i];
-    }
+  for (int i = 0; i < AttnShape<D>::kLoads; ++i) {
+    const int j = tile_pos<D>(t, w, i, r);
+    const int blk = min(j / a.block_size, a.blocks_per_row - 1);
+    const long long slot = (long long)tabs[blk] * a.block_size + (j % a.block_size);
+    const bool ok = j < neff && slot >= 0 && slot < a.slots;
+    off[i] = ok ? static_cast<int>((slot * a.kv_heads + g) * D + c * 8) : -1;
   }
 }
 
-// Tiles gi*kGroupTiles .. +kGroupTiles-1 (those below ntiles) into registers.
-constexpr int kGroupTiles = 4;
-
-template <typename T, int D, int NPT>
-__device__ __forceinline__ void load_group(Vec8<T> (&v)[kGroupTiles][NPT], const T* cache, const int32_t* tab, int gi,
-                                           int ntiles, int neff, const AttnArgs& a, int g) {
+// Issue the loads of one tile's rows (keys or values): unconditional (a
+// missing row reads row 0 and is zeroed afterwards), so all of them are in
+// flight before the first is used.
+template <typename T, int D>
+__device__ __forceinline__ void load_tile(Vec8<T> (&v)[AttnShape<D>::kLoads], const T* cache,
+                                          const int (&off)[AttnShape<D>::kLoads], int c) {
 #pragma unroll
-  for (int tt = 0; tt < kGroupTiles; ++tt) {
-    const int t = gi * kGroupTiles + tt;
-    if (t < ntiles) load_tile<T, D>(v[tt], cache, tab, t * kTile, neff, a, g);
-  }
+  for (int i = 0; i < AttnShape<D>::kLoads; ++i) v[i] = Vec8<T>::load_cached(cache + (off[i] >= 0 ? off[i] : c * 8));
+}
+
+__device__ __forceinline__ float block_reduce_max(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / 64; ++i) m = fmaxf(m, red[i]);
+  return m;
+}
+
+__device__ __forceinline__ float block_reduce_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) s += red[i];
+  return s;
 }
 
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) k_attn(AttnArgs a) {
-  using S = AttnShape<T, D>;
+  using S = AttnShape<D>;
+  constexpr int L = S::kLpr;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const int G = a.heads / a.kv_heads, W = a.window;
-  float* qs = reinterpret_cast<float*>(smem_raw);   // [G, D]
-  float* sc = qs + G * D;                            // [G, W]
-  T* kt = reinterpret_cast<T*>(sc + G * W);          // [kTile, kRow] keys, then values
-  const int b = blockIdx.x, g = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = kThreads / 64;
+  const int W = a.window;
+  float* sc = reinterpret_cast<float*>(smem_raw);  // [W] scores, then probabilities
+  float* part = sc + W;                            // [4 waves][64 lanes][8] P.V partials
+  __shared__ float red[kThreads / 64];
+  const int G = a.heads / a.kv_heads;
+  const int groups = a.B * a.kv_heads;
+  const int grp = blockIdx.x % groups, hi = blockIdx.x / groups;
+  const int b = grp / a.kv_heads, g = grp - b * a.kv_heads;
+  const int h = g * G + hi;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane / L, c = lane % L;
   const int n = a.len[b];
   const bool uniform = n <= 0;
   const int neff = uniform ? W : min(n, W);
   const int ntiles = (neff + kTile - 1) / kTile;
-  const T* Q = static_cast<const T*>(a.q) + (size_t)b * a.heads * D + (size_t)g * G * D;
   const T* KC = static_cast<const T*>(a.key_cache);
   const T* VC = static_cast<const T*>(a.value_cache);
   const int32_t* tab = a.table + (size_t)b * a.blocks_per_row;
+  int* tabs = reinterpret_cast<int*>(part + kThreads * 8);  // [blocks_per_row]
 
-  // One round trip: query heads and the keys and values of the first
-  // kGroupTiles tiles (256 positions) are requested together.
-  Vec8<T> qv = Vec8<T>{};
-  const int qvecs = G * D / 8;
-  if (tid < qvecs) qv = Vec8<T>::load_cached(Q + tid * 8);
-  Vec8<T> kr[kGroupTiles][S::kPerThread], vr[kGroupTiles][S::kPerThread];
-  load_group<T, D>(kr, KC, tab, 0, ntiles, neff, a, g);
-  load_group<T, D>(vr, VC, tab, 0, ntiles, neff, a, g);
-  if (a.done != nullptr && __builtin_nontemporal_load(a.done) != 0) return;  // read while loads fly
-  if (tid < qvecs) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qs[tid * 8 + e] = qv.get(e);
-  }
+  // Round trip 1: the row's block table (into LDS) and the query chunk.
+  // Round trip 2: the first tile of keys and values, all loads in flight.
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  for (int e = tid; e < a.blocks_per_row; e += kThreads) tabs[e] = tab[e];
+  const Vec8<T> qv = Vec8<T>::load_cached(static_cast<const T*>(a.q) + ((size_t)b * a.heads + h) * D + c * 8);
+  lds_barrier();
+  if (stop != 0) return;  // uniform over the workgroup
+  int off[S::kLoads];
+  tile_offsets<D>(off, tabs, 0, w, r, c, neff, a, g);
+  Vec8<T> kr[S::kLoads], vr[S::kLoads];
+  load_tile<T, D>(kr, KC, off, c);
+  load_tile<T, D>(vr, VC, off, c);
+
+  // Scores of every tile into sc.
   const float scale_div = sqrtf(static_cast<float>(D));
-  const int ngroups = (ntiles + kGroupTiles - 1) / kGroupTiles;
-  // Pass 1: scores of every tile.
-  for (int gi = 0; gi < ngroups; ++gi) {
-    if (gi > 0) load_group<T, D>(kr, KC, tab, gi, ntiles, neff, a, g);
+  float smax = -INFINITY;
+  for (int t = 0; t < ntiles; ++t) {
+    if (t > 0) {
+      tile_offsets<D>(off, tabs, t, w, r, c, neff, a, g);
+      load_tile<T, D>(kr, KC, off, c);
+    }
+    // a missing row (slot outside the cache) is a zero key: score 0
+    float part_dot[L];
 #pragma unroll
-    for (int tt = 0; tt < kGroupTiles; ++tt) {
-      const int t = gi * kGroupTiles + tt;
-      if (t < ntiles) {
-        store_tile<T, D>(kr[tt], kt);
-        __syncthreads();
-        const int t0 = t * kTile;
-        for (int p = tid; p < G * kTile; p += kThreads) {
-          const int h = p / kTile, jj = p - h * kTile, j = t0 + jj;
-          if (j < neff) {
-            const T* krow = kt + jj * S::kRow;
-            const float* qrow = qs + h * D;
-            float s = 0.f;
-#pragma unroll
-            for (int c = 0; c < S::kVecRow; ++c) {
-              const Vec8<T> k8 = Vec8<T>::load_cached(krow + c * 8);
-#pragma unroll
-              for (int e = 0; e < 8; ++e) s = fmaf(qrow[c * 8 + e], k8.get(e), s);
-            }
-            if constexpr (sizeof(T) == 2) s = round_bf16(s);  // ExactQk output is bf16
-            s = round_bf16(s / scale_div);
-            if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
-            sc[h * W + j] = s;
-          }
-        }
-        __syncthreads();
-      }
+    for (int i = 0; i < L; ++i) part_dot[i] = off[i] >= 0 ? dot8(kr[i], qv, 0.f) : 0.f;
+    group_reduce_transpose<L>(part_dot, c);
+    // lane (r, c) now holds the score of position tile_pos(t, w, c, r)
+    const int j = tile_pos<D>(t, w, c, r);
+    float s = part_dot[0];
+    if constexpr (sizeof(T) == 2) s = round_bf16(s);  // ExactQk output is bf16
+    s = round_bf16(s / scale_div);
+    if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
+    if (j < neff) {
+      sc[j] = s;
+      smax = fmaxf(smax, s);
     }
   }
-  // Softmax per head (fp32), probabilities rounded to bf16.
-  for (int h = wave; h < G; h += nwaves) {
-    float mx = -INFINITY;
-    for (int j = lane; j < neff; j += 64) mx = fmaxf(mx, sc[h * W + j]);
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int j = lane; j < neff; j += 64) sum += expf(sc[h * W + j] - mx);
-    sum = wave_sum(sum);
-    const float inv = 1.0f / sum;
-    for (int j = lane; j < neff; j += 64) sc[h * W + j] = round_bf16(expf(sc[h * W + j] - mx) * inv);
-  }
-  // Pass 2: P.V.  Thread (dd, part) accumulates heads h = part, part + nsplit, ...
-  constexpr int kSplit = kThreads / D;  // D divides 256
-  const int dd = tid % D, part = tid / D;
+  const float mx = block_reduce_max(smax, red);
+  float esum = 0.f;
+  for (int j = tid; j < neff; j += kThreads) esum += expf(sc[j] - mx);
+  const float inv = 1.0f / block_reduce_sum(esum, red);
+  for (int j = tid; j < neff; j += kThreads) sc[j] = round_bf16(expf(sc[j] - mx) * inv);
+  __syncthreads();
+
+  // P.V: lane (r, c) accumulates elements c*8..c*8+7 over its rows.
   float acc[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int gi = 0; gi < ngroups; ++gi) {
-    if (gi > 0) load_group<T, D>(vr, VC, tab, gi, ntiles, neff, a, g);
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int t = 0; t < ntiles; ++t) {
+    if (t > 0) {
+      tile_offsets<D>(off, tabs, t, w, r, c, neff, a, g);
+      load_tile<T, D>(vr, VC, off, c);
+    } else if (ntiles > 1) {
+      tile_offsets<D>(off, tabs, 0, w, r, c, neff, a, g);  // the score loop moved on
+    }
 #pragma unroll
-    for (int tt = 0; tt < kGroupTiles; ++tt) {
-      const int t = gi * kGroupTiles + tt;
-      if (t < ntiles) {
-        __syncthreads();  // scores final / previous tile consumed
-        store_tile<T, D>(vr[tt], kt);
-        __syncthreads();
-        const int t0 = t * kTile;
-        const int tn = min(kTile, neff - t0);
-        for (int jj = 0; jj < tn; ++jj) {
-          const float v = Elt<T>::f(kt[jj * S::kRow + dd]);
+    for (int i = 0; i < S::kLoads; ++i) {
+      // positions >= neff have off < 0; a missing row is a zero value
+      const float p = off[i] >= 0 ? sc[tile_pos<D>(t, w, i, r)] : 0.f;
+      const Vec8<T> v = off[i] >= 0 ? vr[i] : Vec8<T>{};
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int h = part + i * kSplit;
-            if (i * kSplit < 8 && h < G) acc[i] = fmaf(sc[h * W + t0 + jj], v, acc[i]);
-          }
-        }
-      }
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, v.get(e), acc[e]);
     }
   }
-  T* O = static_cast<T*>(a.out) + (size_t)b * a.heads * D + (size_t)g * G * D;
+  // Combine the 64/L row groups of each wave and the 4 waves, in a fixed order.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int h = part + i * kSplit;
-    if (i * kSplit < 8 && h < G) O[h * D + dd] = Elt<T>::t(acc[i]);
+  for (int e = 0; e < 8; ++e) part[(w * 64 + lane) * 8 + e] = acc[e];
+  __syncthreads();
+  if (tid < D) {
+    const int cc = tid / 8, e = tid % 8;
+    float o = 0.f;
+    for (int ww = 0; ww < kThreads / 64; ++ww)
+      for (int rr = 0; rr < S::kRg; ++rr) o += part[(ww * 64 + rr * L + cc) * 8 + e];
+    static_cast<T*>(a.out)[((size_t)b * a.heads + h) * D + tid] = Elt<T>::t(o);
   }
 }
 
+size_t smem_bytes(int window, int blocks_per_row) {
+  return (size_t)window * sizeof(float) + (size_t)kThreads * 8 * sizeof(float) + (size_t)blocks_per_row * sizeof(int);
+}
+
 template <typename T, int D>
-hipError_t launch_t(const AttnArgs& a, int G, hipStream_t stream) {
-  using S = AttnShape<T, D>;
-  const size_t smem = (size_t)(G * D + G * a.window) * sizeof(float) + (size_t)kTile * S::kRow * sizeof(T);
-  k_attn<T, D><<<dim3(a.B, a.kv_heads), kThreads, smem, stream>>>(a);
+hipError_t launch_t(const AttnArgs& a, hipStream_t stream) {
+  k_attn<T, D><<<a.B * a.heads, kThreads, smem_bytes(a.window, a.blocks_per_row), stream>>>(a);
   return hipGetLastError();
 }
 
+// Dynamic LDS the launches of this engine need (the window's scores grow
+// with the capacity); the static reduction scratch comes on top of it.
 template <typename T, int D>
-hipError_t allow_t() {
+hipError_t allow_t(size_t bytes) {
   return hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn<T, D>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                             160 * 1024);
+                             static_cast<int>(bytes));
 }
 
 }  // namespace
 
-size_t attention_lds_bytes(const Dims& d) {
-  const int row = d.head_dim + 16 / d.dtype_bytes;
-  return (size_t)(d.groups() * d.head_dim + d.groups() * d.capacity) * sizeof(float) +
-         (size_t)kTile * row * d.dtype_bytes;
-}
+size_t attention_lds_bytes(const Dims& d) { return smem_bytes(d.capacity, d.blocks_per_row); }
 
 hipError_t prepare_attention(const Dims& d) {
+  if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256) return hipErrorInvalidValue;
+  const size_t bytes = attention_lds_bytes(d);
   if (d.dtype_bytes == 2) {
-    if (d.head_dim == 64) return allow_t<bf16_t, 64>();
-    if (d.head_dim == 128) return allow_t<bf16_t, 128>();
-    return allow_t<bf16_t, 256>();
+    if (d.head_dim == 64) return allow_t<bf16_t, 64>(bytes);
+    if (d.head_dim == 128) return allow_t<bf16_t, 128>(bytes);
+    return allow_t<bf16_t, 256>(bytes);
   }
-  if (d.head_dim == 64) return allow_t<float, 64>();
-  if (d.head_dim == 128) return allow_t<float, 128>();
-  return allow_t<float, 256>();
+  if (d.head_dim == 64) return allow_t<float, 64>(bytes);
+  if (d.head_dim == 128) return allow_t<float, 128>(bytes);
+  return allow_t<float, 256>(bytes);
 }
 
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream) {
-  const int G = d.groups();
   if (d.dtype_bytes == 2) {
-    if (d.head_dim == 64) return launch_t<bf16_t, 64>(a, G, stream);
-    if (d.head_dim == 128) return launch_t<bf16_t, 128>(a, G, stream);
-    return launch_t<bf16_t, 256>(a, G, stream);
+    if (d.head_dim == 64) return launch_t<bf16_t, 64>(a, stream);
+    if (d.head_dim == 128) return launch_t<bf16_t, 128>(a, stream);
+    return launch_t<bf16_t, 256>(a, stream);
   }
-  if (d.head_dim == 64) return launch_t<float, 64>(a, G, stream);
-  if (d.head_dim == 128) return launch_t<float, 128>(a, G, stream);
-  return launch_t<float, 256>(a, G, stream);
+  if (d.head_dim == 64) return launch_t<float, 64>(a, stream);
+  if (d.head_dim == 128) return launch_t<float, 128>(a, stream);
+  return launch_t<float, 256>(a, stream);
 }
 
 }  // namespace re

@@ -217,7 +217,10 @@ bool make_plan(Engine& e, const Json& cfg) {
   if (d.head_dim % 2 != 0) return false;
   const size_t normed_lds = normed_lds_bytes(p.mb, d.hidden, d.dtype_bytes, p.waves);
   if (normed_lds > 64 * 1024 || resid_lds_bytes(p.mb, d.dtype_bytes, p.waves) > 64 * 1024) return false;
-  if (attention_lds_bytes(d) > 160 * 1024 || prepare_attention(d) != hipSuccess) return false;
+  // attention: scores of the window + P.V partials + block table, plus 16 bytes of static LDS
+  if (attention_lds_bytes(d) > 160 * 1024 - 64 || prepare_attention(d) != hipSuccess) return false;
+  // cache offsets of one layer are 32-bit in the attention kernel
+  if ((long long)d.slots() * d.kv_dim() >= (1LL << 31)) return false;
   plan_grids(p, d, e.cus);
   // Optional overrides for tuning sweeps ("tuning": {"qkv_grid": n, ...}).
   if (const Json* t = cfg.get("tuning")) {
