@@ -188,7 +188,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(),
             "avg_launch_us": round(gu_avg_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": gu_bytes,
         },
@@ -196,6 +196,18 @@ def main() -> int:
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def traffic_bytes():
+    """HBM bytes per gate/up launch from the committed rocprofv3 PMC passes
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a
+    plain copy of known size): profiles/gate_up_qwen7b_b4_traffic.md."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_qwen7b_b4_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(rt, steps: int):
