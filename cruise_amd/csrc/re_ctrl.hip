@@ -249,46 +249,54 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   StatePtrs& s = a.st;
   if (*s.done != 0) return;
   const int B = a.B;
-  __shared__ float bv_s[1024];
-  __shared__ int bi_s[1024];
-  __shared__ int bb_s[1024];
   __shared__ int tok_s[64 * 4];
   __shared__ int bad_s[64 * 4];
-  const int tid = threadIdx.x;
-  // Final argmax pass: threads stride over workgroup partials per row.
-  for (int b = 0; b < B; ++b) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  // Final argmax over the LM head's workgroup partials (CTRL:99-119): one wave
+  // per batch row; each lane requests its strided share of the partials at
+  // once (clamped, ignored past the count), then a shuffle reduction keeps the
+  // first index of the maximum; any non-finite logit flags the row.
+  constexpr int kUnroll = 16;
+  for (int b = wave; b < B; b += nwaves) {
     float bv = 0.f;
     int bi = -1, bb = 0;
-    for (int w = tid; w < a.lm_wg; w += blockDim.x) {
-      const size_t o = (size_t)w * B + b;
-      const int i = a.am_idx[o];
-      const float v = a.am_val[o];
-      bb |= a.am_bad[o];
-      if (i < 0) continue;
-      if (bi < 0 || v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-    }
-    bv_s[tid] = bv;
-    bi_s[tid] = bi;
-    bb_s[tid] = bb;
-    __syncthreads();
-    for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
-      if (tid < stride) {
-        const float v = bv_s[tid + stride];
-        const int i = bi_s[tid + stride];
-        bb_s[tid] |= bb_s[tid + stride];
-        if (i >= 0 && (bi_s[tid] < 0 || v > bv_s[tid] || (v == bv_s[tid] && i < bi_s[tid]))) {
-          bv_s[tid] = v;
-          bi_s[tid] = i;
+    for (int w0 = 0; w0 < a.lm_wg; w0 += 64 * kUnroll) {
+      float v[kUnroll];
+      int ix[kUnroll], fl[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const size_t o = (size_t)min(w0 + lane + 64 * u, a.lm_wg - 1) * B + b;
+        v[u] = a.am_val[o];
+        ix[u] = a.am_idx[o];
+        fl[u] = a.am_bad[o];
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (w0 + lane + 64 * u >= a.lm_wg) continue;
+        bb |= fl[u];
+        if (ix[u] < 0) continue;
+        if (bi < 0 || v[u] > bv || (v[u] == bv && ix[u] < bi)) {
+          bv = v[u];
+          bi = ix[u];
         }
       }
-      __syncthreads();
     }
-    if (tid == 0) {
-      tok_s[b] = bi_s[0];
-      bad_s[b] = bb_s[0];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(bv, m, 64);
+      const int oi = __shfl_xor(bi, m, 64);
+      bb |= __shfl_xor(bb, m, 64);
+      if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+      }
     }
-    __syncthreads();
+    if (lane == 0) {
+      tok_s[b] = bi;
+      bad_s[b] = bb;
+    }
   }
+  __syncthreads();
   if (tid != 0) return;
   const int call = ++(*s.model_calls);
   int64_t* history = reinterpret_cast<int64_t*>(s.fetch);

@@ -144,11 +144,9 @@ __device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per
 // (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
 // cast to T, then a T x T product with the weight.  Writes xn[8t .. 8t+7].
 template <typename T>
-__device__ __forceinline__ void row_rmsnorm(const float (&h)[8], bool has, const T* __restrict__ norm_w, T* xn,
-                                            int H, float eps, float* red) {
+__device__ __forceinline__ void row_rmsnorm(const float (&h)[8], bool has, const Vec8<T>& wv, T* xn, int H,
+                                            float eps, float* red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  Vec8<T> wv = Vec8<T>{};
-  if (has) wv = Vec8<T>::load_cached(norm_w + tid * 8);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss = fmaf(h[e], h[e], ss);
@@ -195,8 +193,11 @@ __global__ void __launch_bounds__(kRowThreads) k_embed_norm(RowArgs a) {
   long long t = a.token[b];
   if (t < 0 || t >= a.V) t = 0;  // the controller rejects such ids (CTRL:356); reads stay in bounds
   const bool has = tid * 8 < a.H;
-  Vec8<T> ev = Vec8<T>{};
-  if (has) ev = Vec8<T>::load_cached(static_cast<const T*>(a.embedding) + (size_t)t * a.H + tid * 8);
+  Vec8<T> ev = Vec8<T>{}, wv = Vec8<T>{};
+  if (has) {
+    ev = Vec8<T>::load_cached(static_cast<const T*>(a.embedding) + (size_t)t * a.H + tid * 8);
+    wv = Vec8<T>::load_cached(static_cast<const T*>(a.norm_w) + tid * 8);
+  }
   for (int j = tid; j < a.half; j += blockDim.x) {
     const float ang = static_cast<float>(a.pos[b]) * a.inv_freq[j];
     a.rope[((size_t)b * a.half + j) * 2] = Elt<T>::r(cosf(ang));
@@ -207,8 +208,7 @@ __global__ void __launch_bounds__(kRowThreads) k_embed_norm(RowArgs a) {
   for (int e = 0; e < 8; ++e) h[e] = ev.get(e);
   T* hid = static_cast<T*>(a.hidden) + (size_t)b * a.H;
   if (has) *reinterpret_cast<Vec8<T>*>(hid + tid * 8) = ev;
-  row_rmsnorm<T>(h, has, static_cast<const T*>(a.norm_w), static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps,
-                 red);
+  row_rmsnorm<T>(h, has, wv, static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps, red);
 }
 
 // Residual add of a projection and the norm of the next one: the segment
@@ -225,26 +225,48 @@ __global__ void __launch_bounds__(kRowThreads) k_resid_norm(RowArgs a) {
   float h[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) h[e] = 0.f;
+  // every load of the kernel (hidden, norm weight, partials) in one round trip
+  Vec8<T> wv = Vec8<T>{};
   if (has) {
     const Vec8<T> hv = Vec8<T>::load_cached(hid + tid * 8);
+    wv = Vec8<T>::load_cached(static_cast<const T*>(a.norm_w) + tid * 8);
     float s[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) s[e] = 0.f;
-    for (int sp = 0; sp < a.segments; ++sp) {
-      const re_f32x4* p = reinterpret_cast<const re_f32x4*>(a.partial + ((size_t)sp * a.B + b) * a.H + tid * 8);
-      const re_f32x4 lo = p[0], hi = p[1];
+    // The first kUnrolledSegments partials are requested at once (clamped to
+    // a valid segment, added only below the count); more are summed after.
+    constexpr int kUnrolledSegments = 8;
+    re_f32x4 lo[kUnrolledSegments], hi[kUnrolledSegments];
+#pragma unroll
+    for (int sp = 0; sp < kUnrolledSegments; ++sp) {
+      const int spc = min(sp, a.segments - 1);
+      const re_f32x4* p = reinterpret_cast<const re_f32x4*>(a.partial + ((size_t)spc * a.B + b) * a.H + tid * 8);
+      lo[sp] = p[0];
+      hi[sp] = p[1];
+    }
+#pragma unroll
+    for (int sp = 0; sp < kUnrolledSegments; ++sp) {
+      const bool use = sp < a.segments;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        s[e] += lo[e];
-        s[e + 4] += hi[e];
+        s[e] += use ? lo[sp][e] : 0.f;
+        s[e + 4] += use ? hi[sp][e] : 0.f;
+      }
+    }
+    for (int sp = kUnrolledSegments; sp < a.segments; ++sp) {
+      const re_f32x4* p = reinterpret_cast<const re_f32x4*>(a.partial + ((size_t)sp * a.B + b) * a.H + tid * 8);
+      const re_f32x4 l = p[0], u = p[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[e] += l[e];
+        s[e + 4] += u[e];
       }
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) h[e] = Elt<T>::r(hv.get(e) + Elt<T>::r(s[e]));
     *reinterpret_cast<Vec8<T>*>(hid + tid * 8) = Vec8<T>::from_floats(h);
   }
-  row_rmsnorm<T>(h, has, static_cast<const T*>(a.norm_w), static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps,
-                 red);
+  row_rmsnorm<T>(h, has, wv, static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -298,9 +320,16 @@ __device__ __forceinline__ void proj_rows(const ProjArgs& a, int u, const T* W0,
   }
 }
 
+// Waves per SIMD a projection is compiled for.  qkv runs one row pair per
+// wave (2,304 pairs fit the chip at once), so it trades the fourth wave for
+// registers: its RoPE epilogue would spill at 128.
+template <typename T, int MB, int KIND>
+constexpr int proj_min_waves() {
+  return (sizeof(T) == 2 && MB == 4) ? (KIND == 0 ? 3 : NORMED_MIN_WAVES) : 2;
+}
+
 template <typename T, int MB, int WAVES, int KIND, bool FULL>
-__global__ void __launch_bounds__(WAVES * 64, (sizeof(T) == 2 && MB == 4) ? NORMED_MIN_WAVES : 2)
-    k_proj(ProjArgs a) {
+__global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k_proj(ProjArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* xs = reinterpret_cast<T*>(smem_raw);
   float* red = reinterpret_cast<float*>(smem_raw + (size_t)MB * a.H * sizeof(T));
