@@ -15,6 +15,7 @@ struct CtrlArgs {
   StatePtrs st;
   int B, bpr, physical_blocks, block_size, capacity, vocab;
   int lm_wg;          // argmax partial rows
+  int layers, kv_dim, elem_bytes;  // cache geometry (import checksum length)
   const float* am_val;
   const int32_t* am_idx;
   const int32_t* am_bad;
@@ -72,6 +73,10 @@ __device__ FeedView feed_view(const uint8_t* feed, int B, int bpr, bool importin
 __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   StatePtrs& s = a.st;
+  if (threadIdx.x == 0) {  // import checksum accumulators, summed by k_import_checksum
+    s.import_sum[0] = 0;
+    s.import_sum[1] = 0;
+  }
   const int B = a.B;
   // The control vector sits at the same place in both feed forms; read the
   // variant first to learn the form (CTRL:209-217).
@@ -94,6 +99,7 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
   s.misc[2] = graph_variant;
   s.misc[3] = flagged ? 1 : 0;
   s.misc[4] = import_mask;
+  s.misc[5] = 0;  // 1 once the import is applied (copy + checksum run)
   *s.model_calls = 0;
   *s.status = kStatusOk;
   *s.done = 0;
@@ -171,6 +177,7 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
       s.res_len[r] = f.len[r];
       s.res_valid[r] = 1;
     }
+    if (status == kStatusOk) s.misc[5] = 1;
   }
   if (status == kStatusOk) {  // 448-464
     for (int r = 0; r < B; ++r) {
@@ -188,9 +195,12 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
     }
   }
   if (status != kStatusOk) {
+    // An import applied before the continuity check stays applied (its
+    // copy and checksum still run, CTRL:387-446 precede 448-471); the
+    // new-generation clears are dropped.
     for (int r = 0; r < B; ++r) {
       s.reason[r] = kFinishFallback;
-      s.clear_row[r] = 0;
+      if (s.misc[5] == 0 || s.clear_row[r] != 2) s.clear_row[r] = 0;
     }
     *s.status = status;
     *s.done = 1;
@@ -339,6 +349,83 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   if (count == 0) *s.done = 1;
 }
 
+// Adler-32 of the imported blocks as they sit in the resident caches, in the
+// order of CTRL:430-445 (key cache then value cache, layer-major, rows
+// ascending), computed in parallel: over bytes d_0..d_{N-1} with a = 1, b = 0
+// at the start, a = 1 + sum d_i and b = N + sum (N - i) d_i (mod 65521).  Each
+// thread reduces its 16-byte words, each workgroup adds its two residues
+// into s.import_sum with one 64-bit atomic (integer sums: the order does not
+// matter); k_ctrl_finish forms the checksum.
+struct ImportSumArgs {
+  const int32_t* misc;    // [4] import mask, [5] import applied
+  const int32_t* table;
+  const uint8_t* key_cache;
+  const uint8_t* value_cache;
+  unsigned long long* sum;
+  int B, bpr, layers;
+  long long block_bytes, layer_bytes;
+};
+
+constexpr unsigned kAdlerModulus = 65521;
+
+__global__ void __launch_bounds__(256) k_import_checksum(ImportSumArgs a) {
+  __shared__ unsigned long long red[2][4];
+  if (a.misc[5] == 0) return;  // no import applied this epoch
+  const int mask = a.misc[4];
+  int rows[32];
+  int nsel = 0;
+  for (int r = 0; r < a.B && r < 32; ++r)
+    if (mask & (1 << r)) rows[nsel++] = r;
+  const long long words_per_block = a.block_bytes / 16;
+  const long long total_words = 2LL * a.layers * nsel * words_per_block;
+  const unsigned long long n = (unsigned long long)total_words * 16;
+  unsigned long long s1 = 0, s2 = 0;
+  for (long long w = (long long)blockIdx.x * blockDim.x + threadIdx.x; w < total_words;
+       w += (long long)gridDim.x * blockDim.x) {
+    const long long piece = w / words_per_block;  // (cache, layer, k-th selected row)
+    const long long off = w - piece * words_per_block;
+    const int k = static_cast<int>(piece % nsel);
+    const int layer = static_cast<int>((piece / nsel) % a.layers);
+    const int cache = static_cast<int>(piece / ((long long)nsel * a.layers));
+    const int blk = a.table[rows[k] * a.bpr];
+    const uint8_t* base = cache == 0 ? a.key_cache : a.value_cache;
+    const uint4 v = reinterpret_cast<const uint4*>(base + layer * a.layer_bytes + blk * a.block_bytes)[off];
+    const unsigned words[4] = {v.x, v.y, v.z, v.w};
+    const unsigned long long i0 = (unsigned long long)w * 16;  // stream index of the word's first byte
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned long long d = (words[q] >> (8 * e)) & 0xFFu;
+        s1 += d;
+        s2 += d * (n - (i0 + 4 * q + e));
+      }
+    }
+    s1 %= kAdlerModulus;
+    s2 %= kAdlerModulus;
+  }
+  // workgroup sum of the residues (each < 65521), one atomic per workgroup
+  for (int m = 32; m >= 1; m >>= 1) {
+    s1 += __shfl_xor(s1, m, 64);
+    s2 += __shfl_xor(s2, m, 64);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[0][wave] = s1;
+    red[1][wave] = s2;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long t1 = 0, t2 = 0;
+    for (int i = 0; i < 4; ++i) {
+      t1 += red[0][i];
+      t2 += red[1][i];
+    }
+    atomicAdd(&a.sum[0], t1 % kAdlerModulus);
+    atomicAdd(&a.sum[1], t2 % kAdlerModulus);
+  }
+}
+
 // Finish reasons, resident save and emit (CTRL:296-324, 592-621).
 __global__ void k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
   (void)import_checksum_unused;
@@ -366,7 +453,18 @@ __global__ void k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
   control[2] = s.misc[2];
   control[3] = status;
   control[4] = *s.model_calls;
-  control[5] = importing ? 0 : (fallback ? 1 : 0);  // the import checksum is added by the host
+  if (importing && s.misc[5] != 0) {
+    // CTRL:301-303: the import checksum; see k_import_checksum for the sums
+    int nsel = 0;
+    for (int r = 0; r < B; ++r) nsel += (s.misc[4] >> r) & 1;
+    const unsigned long long n =
+        2ULL * a.layers * nsel * (unsigned long long)a.block_size * a.kv_dim * a.elem_bytes;
+    const unsigned first = static_cast<unsigned>((1 + s.import_sum[0]) % kAdlerModulus);
+    const unsigned second = static_cast<unsigned>((n % kAdlerModulus + s.import_sum[1]) % kAdlerModulus);
+    control[5] = static_cast<int32_t>((second << 16) | first);
+  } else {
+    control[5] = importing ? 0 : (fallback ? 1 : 0);  // import rejected before the copy: 0
+  }
   int initial = 0, final_count = 0;
   for (int r = 0; r < B; ++r) {
     control[6 + r] = s.eos[r];
@@ -418,6 +516,9 @@ static CtrlArgs ctrl_args(const KernelEnv& env, const StatePtrs& st) {
   a.capacity = env.dims.capacity;
   a.vocab = env.dims.vocab;
   a.lm_wg = env.plan.lm_wg;
+  a.layers = env.dims.layers;
+  a.kv_dim = env.dims.kv_dim();
+  a.elem_bytes = env.dims.dtype_bytes;
   a.am_val = env.scratch.am_val;
   a.am_idx = env.scratch.am_idx;
   a.am_bad = env.scratch.am_bad;
@@ -450,6 +551,24 @@ hipError_t launch_clear_rows(const KernelEnv& env, const StatePtrs& st, void* ke
   c.block_bytes = (long long)d.block_size * d.kv_dim() * d.dtype_bytes;
   c.layer_bytes = (long long)d.slots() * d.kv_dim() * d.dtype_bytes;
   k_clear_rows<<<1024, 256, 0, stream>>>(c);
+  return hipGetLastError();
+}
+
+hipError_t launch_import_checksum(const KernelEnv& env, const StatePtrs& st, const void* key_cache,
+                                  const void* value_cache, hipStream_t stream) {
+  const Dims& d = env.dims;
+  ImportSumArgs c{};
+  c.misc = st.misc;
+  c.table = st.table;
+  c.key_cache = static_cast<const uint8_t*>(key_cache);
+  c.value_cache = static_cast<const uint8_t*>(value_cache);
+  c.sum = st.import_sum;
+  c.B = d.batch;
+  c.bpr = d.blocks_per_row;
+  c.layers = d.layers;
+  c.block_bytes = (long long)d.block_size * d.kv_dim() * d.dtype_bytes;
+  c.layer_bytes = (long long)d.slots() * d.kv_dim() * d.dtype_bytes;
+  k_import_checksum<<<256, 256, 0, stream>>>(c);
   return hipGetLastError();
 }
 

@@ -96,7 +96,7 @@ struct Engine {
   uint8_t* h_fetch = nullptr;
   size_t feed_bytes = 0, import_feed_bytes = 0, fetch_bytes = 0, payload_bytes = 0;
   uint8_t* import_payload_scratch = nullptr;  // device, for checksum of the imported blocks
-  uint32_t* checksum_dev = nullptr;
+  unsigned long long* checksum_dev = nullptr;  // import Adler-32 partial sums [2]
 
   // graphs keyed by (K * 2 + import) * 4 + part (0 whole epoch; 1 and 2 the
   // halves around the timed launch)
@@ -363,6 +363,7 @@ bool alloc_state(Engine& e) {
   if (hipMalloc(&e.scratch_mem, off) != hipSuccess) return false;
   if (hipMemset(e.scratch_mem, 0, off) != hipSuccess) return false;
   for (size_t i = 0; i < sp.size(); ++i) *sp[i].p = e.scratch_mem + offs[i];
+  e.st.import_sum = e.checksum_dev;
 
   // decoder-step ABI inputs
   std::vector<Part> io = {
@@ -488,6 +489,9 @@ hipError_t record_epoch(Engine& e, int K, bool importing, int part) {
     if ((err = hipMemcpyAsync(e.st.feed, e.h_feed, feed, hipMemcpyHostToDevice, e.stream)) != hipSuccess) return err;
     if ((err = launch_ctrl_init(env, e.st, importing ? 1 : 0, e.stream)) != hipSuccess) return err;
     if ((err = launch_clear_rows(env, e.st, e.key_cache, e.value_cache, e.stream)) != hipSuccess) return err;
+    if (importing &&
+        (err = launch_import_checksum(env, e.st, e.key_cache, e.value_cache, e.stream)) != hipSuccess)
+      return err;
   }
   const StepPtrs sp = epoch_step_ptrs(e);
   for (int k = 0; k < K; ++k) {
@@ -563,23 +567,6 @@ uint8_t* put(uint8_t* p, const void* src, size_t n) {
   return p + n;
 }
 
-// Adler-32 over a byte range (CTRL:149-163), on the host for the transfer
-// file's own checksum check.
-void adler32_update(const uint8_t* data, size_t bytes, uint32_t& first, uint32_t& second) {
-  constexpr uint32_t kModulus = 65521;
-  while (bytes > 0) {
-    const size_t chunk = bytes > 5552 ? 5552 : bytes;
-    for (size_t i = 0; i < chunk; ++i) {
-      first += data[i];
-      second += first;
-    }
-    first %= kModulus;
-    second %= kModulus;
-    data += chunk;
-    bytes -= chunk;
-  }
-}
-
 #pragma pack(push, 1)
 struct TransferHeader {  // resident_epoch_bridge.cpp:72-89
   uint64_t magic;
@@ -634,30 +621,6 @@ bool read_transfer(Engine& e, const char* path, uint64_t transfer_id, const int3
   import_mask = static_cast<int32_t>(h.import_mask);
   expected_checksum = h.checksum;
   return true;
-}
-
-// Adler-32 of the imported blocks as they now sit in the resident caches, in
-// the order of CTRL:430-445 (key then value, layer-major, rows ascending).
-uint32_t device_import_checksum(Engine& e, int32_t import_mask, bool& ok) {
-  const Dims& d = e.dims;
-  const size_t block_bytes = (size_t)d.block_size * d.kv_dim() * d.dtype_bytes;
-  const size_t layer_bytes = (size_t)d.slots() * d.kv_dim() * d.dtype_bytes;
-  std::vector<int32_t> table(d.batch * d.blocks_per_row);
-  ok = hipMemcpy(table.data(), e.st.table, table.size() * 4, hipMemcpyDeviceToHost) == hipSuccess;
-  std::vector<uint8_t> buf(block_bytes);
-  uint32_t first = 1, second = 0;
-  for (int c = 0; c < 2 && ok; ++c) {
-    const uint8_t* cache = static_cast<const uint8_t*>(c == 0 ? e.key_cache : e.value_cache);
-    for (int l = 0; l < d.layers && ok; ++l) {
-      for (int r = 0; r < d.batch && ok; ++r) {
-        if ((import_mask & (1 << r)) == 0) continue;
-        const size_t off = l * layer_bytes + (size_t)table[r * d.blocks_per_row] * block_bytes;
-        ok = hipMemcpy(buf.data(), cache + off, block_bytes, hipMemcpyDeviceToHost) == hipSuccess;
-        adler32_update(buf.data(), block_bytes, first, second);
-      }
-    }
-  }
-  return (second << 16) | first;
 }
 
 // Launch one epoch.  Without timing it is one graph; with timing it is graph
@@ -886,12 +849,6 @@ extern "C" int32_t resident_epoch_execute(
   collect_timing(*e, max_steps);
   const int64_t* history = reinterpret_cast<const int64_t*>(e->h_fetch);
   int32_t* result_control = reinterpret_cast<int32_t*>(e->h_fetch + 8 * kMaxEpochSteps * B);
-  if (importing && result_control[3] == 0) {
-    bool ok = false;
-    const uint32_t sum = device_import_checksum(*e, import_mask, ok);
-    if (!ok) return 31;
-    result_control[5] = static_cast<int32_t>(sum);
-  }
   *output_device_status = result_control[3];
   *output_model_calls = result_control[4];
   *output_kv_import_checksum = result_control[5];
@@ -943,13 +900,6 @@ extern "C" int32_t resident_epoch_proc(void* engine, const void* feed, int64_t f
   if (!run_graph(*e, graph_k, importing)) return -2;
   if (hipStreamSynchronize(e->stream) != hipSuccess) return -2;
   collect_timing(*e, graph_k);
-  int32_t* control = reinterpret_cast<int32_t*>(e->h_fetch + 8 * kMaxEpochSteps * B);
-  if (importing && control[3] == 0) {
-    bool ok = false;
-    const int32_t variant = *reinterpret_cast<const int32_t*>(e->h_feed + ctl_off + 4 * (2 + B));
-    control[5] = static_cast<int32_t>(device_import_checksum(*e, variant & (kImportGraphFlag - 1), ok));
-    if (!ok) return -2;
-  }
   std::memcpy(fetch, e->h_fetch, e->fetch_bytes);
   return 0;
 }

@@ -91,6 +91,8 @@ struct StatePtrs {
   int32_t* res_valid;
   // fetch (D2H once per epoch): history i64[8,B] then control i32[6+4B+2+B]
   uint8_t* fetch;
+  // import mode: Adler-32 partial sums (sum of bytes, sum of weighted bytes)
+  unsigned long long* import_sum;
 };
 
 // Inputs of one decoder step (the 9-input decoder ABI, resolved to device
@@ -182,6 +184,9 @@ hipError_t launch_clear_rows(const KernelEnv& env, const StatePtrs& st, void* ke
                              void* value_cache, hipStream_t stream);
 hipError_t launch_ctrl_step(const KernelEnv& env, const StatePtrs& st, hipStream_t stream);
 hipError_t launch_ctrl_finish(const KernelEnv& env, const StatePtrs& st, hipStream_t stream);
+// Import mode: Adler-32 of the imported blocks as they sit in the caches.
+hipError_t launch_import_checksum(const KernelEnv& env, const StatePtrs& st, const void* key_cache,
+                                  const void* value_cache, hipStream_t stream);
 // Helpers for prefill / state management.
 hipError_t launch_clear_blocks(const KernelEnv& env, void* key_cache, void* value_cache,
                                const int32_t* blocks, int nblocks, hipStream_t stream);

@@ -323,6 +323,27 @@ __device__ __forceinline__ void proj_rows(const ProjArgs& a, int u, const T* W0,
 // Waves per SIMD a projection is compiled for.  qkv runs one row pair per
 // wave (2,304 pairs fit the chip at once), so it trades the fourth wave for
 // registers: its RoPE epilogue would spill at 128.
+// Epilogue inputs of one qkv row pair for batch row b = b0 + lane (lanes <
+// MB): the two biases and the row's RoPE cos/sin.  Requested together with the
+// pair's weights so the epilogue needs no further memory round trip.
+struct QkvEpi {
+  float bias0, bias1, cos, sin;
+};
+
+template <typename T>
+__device__ __forceinline__ QkvEpi qkv_epilogue_inputs(const ProjArgs& a, int u, int row0, int row1, int b) {
+  QkvEpi e{0.f, 0.f, 1.f, 0.f};
+  const T* bias = static_cast<const T*>(a.w1);
+  e.bias0 = Elt<T>::f(bias[row0]);
+  e.bias1 = Elt<T>::f(bias[row1]);
+  const int half = a.head_dim >> 1;
+  const int j = u % half;
+  const int bc = min(b, a.B - 1);
+  e.cos = a.rope[((size_t)bc * half + j) * 2];
+  e.sin = a.rope[((size_t)bc * half + j) * 2 + 1];
+  return e;
+}
+
 template <typename T, int MB, int KIND>
 constexpr int proj_min_waves() {
   return (sizeof(T) == 2 && MB == 4) ? (KIND == 0 ? 3 : NORMED_MIN_WAVES) : 2;
@@ -357,6 +378,8 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   int row0 = 0, row1 = 0;
   proj_rows<KIND, T>(a, min(u, a.units - 1), W0, W1, wr, row0, row1);
   load_rows<T, kRowsPerWave, FULL>(w, wr, 0, H, lane);
+  QkvEpi epi{};
+  if constexpr (KIND == kQkv) epi = qkv_epilogue_inputs<T>(a, min(u, a.units - 1), row0, row1, b0 + lane);
   __builtin_amdgcn_sched_barrier(0);
   store_rows_block<T, MB>(xv, H, xs, H);
   if (stop != 0) return;
@@ -388,16 +411,14 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
         // F.linear with bias (g4a_linear_t_bias.py:18-21): fp32 sum + bias, one
         // rounding to T.  RoPE (batched_decoder_step.py:231-240, 323-324):
         // q' = q*cos + rotate_half(q)*sin, each product and the sum rounded to T.
-        const T* bias = W1;
-        const float qa = Elt<T>::r(y0 + Elt<T>::f(bias[c0]));
-        const float qb = Elt<T>::r(y1 + Elt<T>::f(bias[c1]));
+        const float qa = Elt<T>::r(y0 + epi.bias0);
+        const float qb = Elt<T>::r(y1 + epi.bias1);
         const int half = a.head_dim >> 1;
         const int hg = cu / half, j = cu - hg * half;
         const int nq = a.heads, nkv = a.kv_heads;
         float oa = qa, ob = qb;
         if (hg < nq + nkv) {
-          const float c = a.rope[((size_t)b * half + j) * 2];
-          const float s = a.rope[((size_t)b * half + j) * 2 + 1];
+          const float c = epi.cos, s = epi.sin;
           oa = Elt<T>::r(Elt<T>::r(qa * c) + Elt<T>::r(-qb * s));
           ob = Elt<T>::r(Elt<T>::r(qb * c) + Elt<T>::r(qa * s));
         }
@@ -447,6 +468,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
     if (u < u_end) {
       proj_rows<KIND, T>(a, u, W0, W1, wr, row0, row1);
       load_rows<T, kRowsPerWave, FULL>(w, wr, 0, H, lane);
+      if constexpr (KIND == kQkv) epi = qkv_epilogue_inputs<T>(a, u, row0, row1, b0 + lane);
     }
   }
   if constexpr (KIND == kLmHead) {
