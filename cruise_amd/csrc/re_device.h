@@ -11,16 +11,31 @@ typedef float re_f32x4 __attribute__((ext_vector_type(4)));
 
 // bf16 <-> fp32.  The fp32 -> bf16 rounding is round-to-nearest-even with
 // NaN mapped to 0x7FC0, the conversion torch applies on ``.to(bfloat16)``.
+// gfx950's v_cvt_pk_bf16_f32 rounds to nearest even; it agrees with the
+// bit-level RNE on every non-NaN fp32 input (all 2^32 patterns checked on
+// the device), so only NaN needs the canonical value.
 __device__ __forceinline__ float bf16_to_f(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
 __device__ __forceinline__ bf16_t f_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>(0x7fc0);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
+  const bf16_t h = __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
+  return f != f ? static_cast<bf16_t>(0x7fc0) : h;
 }
-__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
+// Two values rounded and packed (lo, hi) with one conversion instruction.
+__device__ __forceinline__ uint32_t f2_to_bf16x2(float lo, float hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {lo, hi};
+  uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, re_bf16x2));
+  if (lo != lo) p = (p & 0xffff0000u) | 0x7fc0u;
+  if (hi != hi) p = (p & 0x0000ffffu) | 0x7fc00000u;
+  return p;
+}
+// Rounding to bf16 inside a computation: a NaN stays a NaN (its payload does
+// not matter until a value is stored, and stores canonicalize), so the
+// hardware conversion is used as is.
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f(__builtin_bit_cast(bf16_t, static_cast<__bf16>(f)));
+}
 
 // Element traits: the compute dtype T of a model is bf16 or fp32.
 template <typename T>
@@ -67,8 +82,7 @@ struct Vec8<bf16_t> {
   __device__ __forceinline__ static Vec8 from_floats(const float (&f)[8]) {
     Vec8 r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      r.v[i] = static_cast<uint32_t>(f_to_bf16(f[2 * i])) | (static_cast<uint32_t>(f_to_bf16(f[2 * i + 1])) << 16);
+    for (int i = 0; i < 4; ++i) r.v[i] = f2_to_bf16x2(f[2 * i], f[2 * i + 1]);
     return r;
   }
 };

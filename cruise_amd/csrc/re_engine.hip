@@ -349,7 +349,6 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.am_idx), (size_t)p.lm_wg * B * sizeof(int32_t)},
       {reinterpret_cast<void**>(&e.scratch.am_bad), (size_t)p.lm_wg * B * sizeof(int32_t)},
       {reinterpret_cast<void**>(&e.scratch.inv_freq), (size_t)d.head_dim / 2 * sizeof(float)},
-      {&e.scratch.xn, (size_t)B * d.hidden * T},
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},

@@ -122,7 +122,6 @@ struct Scratch {
   int32_t* am_idx;    // argmax partial indices [nwg, B]
   int32_t* am_bad;    // non-finite flags [nwg, B]
   float* inv_freq;    // fp32 [d/2]
-  void* xn;           // T [B, H] normalized input of the next projection
   float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
 };
 

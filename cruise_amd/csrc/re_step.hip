@@ -1,25 +1,30 @@
 // Decoder-step kernels of the resident decode epoch (gfx950).
 //
 // A decoder step (batched_decoder_step.py:277-417) runs as
-//   embed+norm -> L x [qkv | attention | o-proj | reduce+norm | gate/up |
-//   down | reduce+norm] -> LM head.
+//   embed -> L x [qkv | attention | o-proj | gate/up | down | down-reduce]
+//   -> LM head,
+// six launches per layer at Qwen2.5-7B's shape (o-proj and down add a reduce
+// launch each when their K spans more than one 3584-element segment).
 //
 // Every projection is a weight-streaming skinny GEMM: M = batch rows (4 at the
 // reference geometry) against an [N, K] weight read exactly once.  A wave owns
 // two weight rows over one K-segment of up to 7 x 512 elements (3584: all of
 // Qwen2.5-7B's hidden size) and issues all 14 of its 16-byte non-temporal loads
-// before touching them, so one HBM round trip covers a whole row pair; the
-// first pair is requested before the workgroup stages its activations.
+// before touching them, so one HBM round trip covers a whole row pair.
 // Activations sit in LDS; bf16 pairs go through v_dot2 into fp32
 // accumulators; the 64 lanes are combined by a halving exchange.
 //
-// RMSNorm needs a whole hidden row, so it runs once per row in the small
-// row kernels (embedding gather, residual reduce) that precede each normed
-// projection; they write the normalized activations ``xn`` the projections
-// read.  RoPE cos/sin are tabulated once per step.  RoPE, the paged slot
-// write, SwiGLU and the argmax partials are fused into the projection
-// epilogues; rounding points follow the reference decoder (see the
-// per-kernel comments).
+// The projections that consume a norm (qkv, gate/up, LM head) compute it in
+// their prologue from the residual stream: the hidden rows and the norm
+// weight are requested first, then the first row pair's weights, so the norm
+// is computed while the weights are in flight.  The residual adds happen in
+// the epilogue of a single-segment projection (o-proj), or in the reduce
+// launch that sums a split-K projection's segment partials in order (down:
+// 18944 = five full segments and a tail, one workgroup column each, so every
+// segment's loads are in flight at once).
+// RoPE cos/sin are tabulated once per step.  RoPE, the paged slot write,
+// SwiGLU and the argmax partials are fused into the epilogues; rounding
+// points follow the reference decoder (see the per-kernel comments).
 #include "re_device.h"
 #include "re_layout.h"
 
@@ -37,14 +42,14 @@ constexpr int kRowsPerWave = 2;
 constexpr int kChunk = 512;     // elements covered by one wave-wide 16-byte load
 constexpr int kSegChunks = 7;   // chunks per K-segment
 constexpr int kSeg = kChunk * kSegChunks;
-constexpr int kRowThreads = 512;  // row kernels: one Vec8 of a 3584 row per thread
 
 __device__ __forceinline__ bool skip_step(const int32_t* done) {
   return done != nullptr && __builtin_nontemporal_load(done) != 0;
 }
 
 // Issue the loads of RPW weight rows over the segment [k0, k0 + len): chunk c
-// of lane l covers elements k0 + c*512 + l*8 .. +8.  Chunks past len are zero.
+// of lane l covers elements k0 + c*512 + l*8 .. +8.  Chunks past len are left
+// unset (dot_rows skips them), so no value merge forces an early wait.
 // FULL: the segment holds all kSegChunks chunks (len == kSeg), no guards.
 template <typename T, int RPW, bool FULL = false>
 __device__ __forceinline__ void load_rows(Vec8<T> (&w)[kSegChunks][RPW], const T* const (&wr)[RPW], int k0,
@@ -53,18 +58,15 @@ __device__ __forceinline__ void load_rows(Vec8<T> (&w)[kSegChunks][RPW], const T
   for (int c = 0; c < kSegChunks; ++c) {
     const int k = c * kChunk + lane * 8;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      if (FULL || k < len)
-        w[c][r] = Vec8<T>::load(wr[r] + k0 + k);
-      else
-        w[c][r] = Vec8<T>{};
-    }
+    for (int r = 0; r < RPW; ++r)
+      if (FULL || k < len) w[c][r] = Vec8<T>::load(wr[r] + k0 + k);
   }
 }
 
-// acc[r][m] += sum over the segment of W_r[k] * xs[m][k] (xs: LDS, row stride ldx).
+// acc[r][m] += sum over the segment of W_r[k] * xs[m][k0 + k] (xs: LDS, row
+// stride ldx).
 template <typename T, int MB, int RPW, bool FULL = false>
-__device__ __forceinline__ void dot_rows(const Vec8<T> (&w)[kSegChunks][RPW], const T* xs, int ldx, int len,
+__device__ __forceinline__ void dot_rows(const Vec8<T> (&w)[kSegChunks][RPW], const T* xs, int ldx, int k0, int len,
                                          int lane, float (&acc)[RPW][MB]) {
 #pragma unroll
   for (int c = 0; c < kSegChunks; ++c) {
@@ -72,7 +74,7 @@ __device__ __forceinline__ void dot_rows(const Vec8<T> (&w)[kSegChunks][RPW], co
     if (FULL || k < len) {
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
-        const Vec8<T> x = Vec8<T>::load_cached(xs + m * ldx + k);
+        const Vec8<T> x = Vec8<T>::load_cached(xs + m * ldx + k0 + k);
 #pragma unroll
         for (int r = 0; r < RPW; ++r) acc[r][m] = dot8(w[c][r], x, acc[r][m]);
       }
@@ -103,25 +105,26 @@ constexpr int seg_vecs_per_thread() {
 
 // Load rows b0..b0+MB-1, columns [k0, k0+len), of X [B, ldg] into registers:
 // slot i of thread t holds Vec8 number t + 256*i of the row-major [MB, len]
-// block (zero for rows >= B).  All loads are issued before any is used.
+// block.  The loads are unconditional (addresses clamped into the block), so
+// no branch separates them from later loads and every wait counts exactly;
+// store_rows_block zeroes what lies outside.
 template <typename T, int MB>
 __device__ __forceinline__ void load_rows_block(Vec8<T> (&v)[seg_vecs_per_thread<MB>()], const T* __restrict__ X,
                                                 int ldg, int b0, int B, int k0, int len) {
-  const int per_row = len / 8;
+  const int per_row = max(len / 8, 1);
 #pragma unroll
   for (int i = 0; i < seg_vecs_per_thread<MB>(); ++i) {
-    const int idx = threadIdx.x + 256 * i;
-    const int m = idx / max(per_row, 1), k = (idx - m * per_row) * 8;
-    v[i] = Vec8<T>{};
-    if (idx < MB * per_row && b0 + m < B) v[i] = Vec8<T>::load_cached(X + (size_t)(b0 + m) * ldg + k0 + k);
+    const int idx = min((int)threadIdx.x + 256 * i, MB * per_row - 1);
+    const int m = idx / per_row, k = (idx - m * per_row) * 8;
+    v[i] = Vec8<T>::load_cached(X + (size_t)min(b0 + m, B - 1) * ldg + k0 + k);
   }
 }
 
-// Store the block loaded by load_rows_block into LDS xs [MB, ldx], then a
-// workgroup barrier.
+// Store the block loaded by load_rows_block into LDS xs [MB, ldx] (rows >= B
+// as zero), then a workgroup barrier.
 template <typename T, int MB>
-__device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per_thread<MB>()], int len, T* xs,
-                                                 int ldx) {
+__device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per_thread<MB>()], int b0, int B, int len,
+                                                 T* xs, int ldx) {
   constexpr int NV = seg_vecs_per_thread<MB>();
   const int per_row = len / 8;
 #pragma unroll
@@ -129,148 +132,133 @@ __device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per
     const int idx = threadIdx.x + 256 * i;
     if (idx < MB * per_row) {
       const int m = idx / per_row, k = (idx - m * per_row) * 8;
-      *reinterpret_cast<Vec8<T>*>(xs + m * ldx + k) = v[i];
+      *reinterpret_cast<Vec8<T>*>(xs + m * ldx + k) = b0 + m < B ? v[i] : Vec8<T>{};
     }
   }
   lds_barrier();  // weight loads issued before the staging stay in flight
 }
 
 // ---------------------------------------------------------------------------
-// Row kernels: one workgroup of kRowThreads per batch row, thread t owning
-// elements 8t .. 8t+7 of the hidden row (H <= 8 * kRowThreads).
-// ---------------------------------------------------------------------------
-
-// RMSNorm of one hidden row held as eight values per thread
+// Norm prologue: RMSNorm of rows b0..b0+MB-1 of the residual stream into LDS
 // (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
-// cast to T, then a T x T product with the weight.  Writes xn[8t .. 8t+7].
-template <typename T>
-__device__ __forceinline__ void row_rmsnorm(const float (&h)[8], bool has, const Vec8<T>& wv, T* xn, int H,
-                                            float eps, float* red) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float ss = 0.f;
+// cast to T, then a T x T product with the weight.  Thread t owns hidden
+// chunks t and t + 256 (8 elements each) of every row, so it needs the norm
+// weight of two chunks only.  Requires blockDim.x == 256, H <= 4096.
+// ---------------------------------------------------------------------------
+constexpr int kNormChunks = 2;
+
+template <typename T, int MB>
+struct NormIn {
+  Vec8<T> h[MB][kNormChunks];
+  Vec8<T> w[kNormChunks];
+};
+
+template <typename T, int MB>
+__device__ __forceinline__ void norm_load(NormIn<T, MB>& in, const T* __restrict__ hidden, const T* __restrict__ norm_w,
+                                          int b0, int B, int H) {
+  // unconditional (clamped) loads; norm_to_lds ignores what lies outside
+  const int per_row = H / 8;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss = fmaf(h[e], h[e], ss);
-  ss = wave_sum(ss);
-  if (lane == 0) red[wave] = ss;
-  __syncthreads();
-  float total = 0.f;
-  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) total += red[i];
-  const float rs = rsqrtf(total / static_cast<float>(H) + eps);
-  if (has) {
-    float out[8];
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = min((int)threadIdx.x + 256 * j, per_row - 1);
+    in.w[j] = Vec8<T>::load_cached(norm_w + c * 8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = Elt<T>::r(Elt<T>::r(h[e] * rs) * wv.get(e));
-    *reinterpret_cast<Vec8<T>*>(xn + tid * 8) = Vec8<T>::from_floats(out);
+    for (int m = 0; m < MB; ++m)
+      in.h[m][j] = Vec8<T>::load_cached(hidden + (size_t)min(b0 + m, B - 1) * H + c * 8);
   }
 }
 
-struct RowArgs {
+// The raw rows go to LDS as they arrive (the per-row sums of squares formed
+// on the way), so the hidden values are dead before the block reduction; after
+// it each thread normalizes its own chunks in place.  red: LDS scratch of at
+// least 4 * MB floats.
+template <typename T, int MB>
+__device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int B, int H, float eps, T* xs,
+                                            float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per_row = H / 8;
+  float ss[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) {
+      const int c = tid + 256 * j;
+      const bool ok = c < per_row && b0 + m < B;
+      const Vec8<T> h = ok ? in.h[m][j] : Vec8<T>{};
+      if (c < per_row) *reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8) = h;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = h.get(e);
+        s = fmaf(x, x, s);
+      }
+    }
+    ss[m] = s;
+  }
+  wave_reduce_transpose<MB>(ss, lane);
+  if ((lane & (64 / MB - 1)) == 0) red[wave * MB + lane / (64 / MB)] = ss[0];
+  lds_barrier();
+  float rs[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) total += red[w * MB + m];
+    rs[m] = rsqrtf(total / static_cast<float>(H) + eps);
+  }
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = tid + 256 * j;
+    if (c < per_row) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        Vec8<T>* p = reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8);
+        const Vec8<T> h = *p;
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = Elt<T>::r(Elt<T>::r(h.get(e) * rs[m]) * in.w[j].get(e));
+        *p = Vec8<T>::from_floats(out);
+      }
+    }
+  }
+  lds_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// Embedding gather (batched_decoder_step.py:289-291) and the step's RoPE table
+// (DEC:235-240: fp32 angle pos * inv_freq, cos/sin cast to T; one table for
+// every layer, as DEC computes it once per step).  One workgroup per row.
+// ---------------------------------------------------------------------------
+struct EmbedArgs {
   const int32_t* done;
-  // embed: token ids, embedding table; reduce: fp32 partials [segments, B, H]
   const int64_t* token;
   const void* embedding;
-  const float* partial;
-  int segments;
-  void* hidden;          // T [B, H] residual stream
-  const void* norm_w;    // T [H] weight of the norm that follows
-  void* xn;              // T [B, H] normalized activations
-  // embed only: the step's RoPE table
+  void* hidden;           // T [B, H]
   const int64_t* pos;
   const float* inv_freq;  // [d/2]
   float* rope;            // [B, d/2, 2] cos, sin (rounded to T)
   int B, H, V, half;
-  float eps;
 };
 
-// Embedding gather (batched_decoder_step.py:289-291), the step's RoPE table
-// (DEC:235-240: fp32 angle pos * inv_freq, cos/sin cast to T; one table for
-// every layer, as DEC computes it once per step) and layer 0's input norm.
 template <typename T>
-__global__ void __launch_bounds__(kRowThreads) k_embed_norm(RowArgs a) {
-  __shared__ float red[kRowThreads / 64];
+__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
   if (skip_step(a.done)) return;
   const int b = blockIdx.x, tid = threadIdx.x;
   long long t = a.token[b];
   if (t < 0 || t >= a.V) t = 0;  // the controller rejects such ids (CTRL:356); reads stay in bounds
-  const bool has = tid * 8 < a.H;
-  Vec8<T> ev = Vec8<T>{}, wv = Vec8<T>{};
-  if (has) {
-    ev = Vec8<T>::load_cached(static_cast<const T*>(a.embedding) + (size_t)t * a.H + tid * 8);
-    wv = Vec8<T>::load_cached(static_cast<const T*>(a.norm_w) + tid * 8);
-  }
   for (int j = tid; j < a.half; j += blockDim.x) {
     const float ang = static_cast<float>(a.pos[b]) * a.inv_freq[j];
     a.rope[((size_t)b * a.half + j) * 2] = Elt<T>::r(cosf(ang));
     a.rope[((size_t)b * a.half + j) * 2 + 1] = Elt<T>::r(sinf(ang));
   }
-  float h[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = ev.get(e);
-  T* hid = static_cast<T*>(a.hidden) + (size_t)b * a.H;
-  if (has) *reinterpret_cast<Vec8<T>*>(hid + tid * 8) = ev;
-  row_rmsnorm<T>(h, has, wv, static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps, red);
-}
-
-// Residual add of a projection and the norm of the next one: the segment
-// partials are summed in segment order (deterministic), rounded to T (the
-// projection output; Bf16Materialize is the identity), added to the residual
-// in T (batched_decoder_step.py:380-386, 399-403), then normalized.
-template <typename T>
-__global__ void __launch_bounds__(kRowThreads) k_resid_norm(RowArgs a) {
-  __shared__ float red[kRowThreads / 64];
-  if (skip_step(a.done)) return;
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const bool has = tid * 8 < a.H;
-  T* hid = static_cast<T*>(a.hidden) + (size_t)b * a.H;
-  float h[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = 0.f;
-  // every load of the kernel (hidden, norm weight, partials) in one round trip
-  Vec8<T> wv = Vec8<T>{};
-  if (has) {
-    const Vec8<T> hv = Vec8<T>::load_cached(hid + tid * 8);
-    wv = Vec8<T>::load_cached(static_cast<const T*>(a.norm_w) + tid * 8);
-    float s[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s[e] = 0.f;
-    // The first kUnrolledSegments partials are requested at once (clamped to
-    // a valid segment, added only below the count); more are summed after.
-    constexpr int kUnrolledSegments = 8;
-    re_f32x4 lo[kUnrolledSegments], hi[kUnrolledSegments];
-#pragma unroll
-    for (int sp = 0; sp < kUnrolledSegments; ++sp) {
-      const int spc = min(sp, a.segments - 1);
-      const re_f32x4* p = reinterpret_cast<const re_f32x4*>(a.partial + ((size_t)spc * a.B + b) * a.H + tid * 8);
-      lo[sp] = p[0];
-      hi[sp] = p[1];
-    }
-#pragma unroll
-    for (int sp = 0; sp < kUnrolledSegments; ++sp) {
-      const bool use = sp < a.segments;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[e] += use ? lo[sp][e] : 0.f;
-        s[e + 4] += use ? hi[sp][e] : 0.f;
-      }
-    }
-    for (int sp = kUnrolledSegments; sp < a.segments; ++sp) {
-      const re_f32x4* p = reinterpret_cast<const re_f32x4*>(a.partial + ((size_t)sp * a.B + b) * a.H + tid * 8);
-      const re_f32x4 l = p[0], u = p[1];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[e] += l[e];
-        s[e + 4] += u[e];
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = Elt<T>::r(hv.get(e) + Elt<T>::r(s[e]));
-    *reinterpret_cast<Vec8<T>*>(hid + tid * 8) = Vec8<T>::from_floats(h);
-  }
-  row_rmsnorm<T>(h, has, wv, static_cast<T*>(a.xn) + (size_t)b * a.H, a.H, a.eps, red);
+  const T* src = static_cast<const T*>(a.embedding) + (size_t)t * a.H;
+  T* dst = static_cast<T*>(a.hidden) + (size_t)b * a.H;
+  for (int c = tid; c < a.H / 8; c += blockDim.x)
+    *reinterpret_cast<Vec8<T>*>(dst + c * 8) = Vec8<T>::load_cached(src + c * 8);
 }
 
 // ---------------------------------------------------------------------------
-// Projections of the normalized activations: skinny GEMM + fused epilogue.
+// Normed projections: norm prologue + skinny GEMM + fused epilogue.
 // Workgroup g owns the contiguous unit range [g*per, (g+1)*per) (per = iters
 // x waves), so each workgroup's outputs (logits, mlp) form whole lines.
 // ---------------------------------------------------------------------------
@@ -278,7 +266,8 @@ enum ProjKind { kQkv = 0, kGateUp = 1, kLmHead = 2 };
 
 struct ProjArgs {
   const int32_t* done;
-  const void* xn;         // T [B, H]
+  const void* hidden;     // T [B, H] residual stream
+  const void* norm_w;     // T [H]
   const void* w0;         // qkv: stacked [qkv_rows, H]; gate/up: gate [I, H]; lm: [V, H]
   const void* w1;         // gate/up: up [I, H]; qkv: bias [qkv_rows]
   void* out;              // qkv: q [B, NH*d]; gate/up: mlp [B, I]
@@ -294,6 +283,7 @@ struct ProjArgs {
   void* value_cache;
   long long slots;
   int B, H, units, heads, kv_heads, head_dim;
+  float eps;
 };
 
 template <int KIND, typename T>
@@ -320,9 +310,6 @@ __device__ __forceinline__ void proj_rows(const ProjArgs& a, int u, const T* W0,
   }
 }
 
-// Waves per SIMD a projection is compiled for.  qkv runs one row pair per
-// wave (2,304 pairs fit the chip at once), so it trades the fourth wave for
-// registers: its RoPE epilogue would spill at 128.
 // Epilogue inputs of one qkv row pair for batch row b = b0 + lane (lanes <
 // MB): the two biases and the row's RoPE cos/sin.  Requested together with the
 // pair's weights so the epilogue needs no further memory round trip.
@@ -344,6 +331,9 @@ __device__ __forceinline__ QkvEpi qkv_epilogue_inputs(const ProjArgs& a, int u, 
   return e;
 }
 
+// Waves per SIMD a projection is compiled for.  qkv runs one row pair per
+// wave (2,304 pairs fit the chip at once), so it trades the fourth wave for
+// registers: its RoPE epilogue would spill at 128.
 template <typename T, int MB, int KIND>
 constexpr int proj_min_waves() {
   return (sizeof(T) == 2 && MB == 4) ? (KIND == 0 ? 3 : NORMED_MIN_WAVES) : 2;
@@ -364,13 +354,13 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   const int u_end = min((int)(blockIdx.x + 1) * iters * WAVES, a.units);
   int u = blockIdx.x * iters * WAVES + wave;
 
-  // The early-exit flag, the activations and the first row pair are
-  // requested together, in that order (loads complete in issue order, so
-  // the activations can be staged while the weights are still in flight).
-  // The flag is uniform: the workgroup leaves together, after the barrier.
+  // Issue order (loads complete in issue order): the early-exit flag, the
+  // hidden rows and norm weight, then the first row pair's weights, so the
+  // norm is computed while the weights are in flight.  The flag is uniform:
+  // the workgroup leaves together, after the barriers.
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
-  Vec8<T> xv[seg_vecs_per_thread<MB>()];
-  load_rows_block<T, MB>(xv, static_cast<const T*>(a.xn), H, b0, a.B, 0, H);
+  NormIn<T, MB> nin;
+  norm_load<T, MB>(nin, static_cast<const T*>(a.hidden), static_cast<const T*>(a.norm_w), b0, a.B, H);
   // Unconditional (a wave past its range loads a valid pair it never uses):
   // with no branch around them the waits below count exactly these 14 loads.
   Vec8<T> w[kSegChunks][kRowsPerWave];
@@ -381,7 +371,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   QkvEpi epi{};
   if constexpr (KIND == kQkv) epi = qkv_epilogue_inputs<T>(a, min(u, a.units - 1), row0, row1, b0 + lane);
   __builtin_amdgcn_sched_barrier(0);
-  store_rows_block<T, MB>(xv, H, xs, H);
+  norm_to_lds<T, MB>(nin, b0, a.B, H, a.eps, xs, red + 3 * WAVES * kRowsPerWave * MB);
   if (stop != 0) return;
   // argmax running state of lane m < MB (batch row b0+m), LM head only
   float best_v = 0.f;
@@ -399,7 +389,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
     for (int r = 0; r < kRowsPerWave; ++r)
 #pragma unroll
       for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
-    dot_rows<T, MB, kRowsPerWave, FULL>(w, xs, H, H, lane, acc);
+    dot_rows<T, MB, kRowsPerWave, FULL>(w, xs, H, 0, H, lane, acc);
     const int cu = u, c0 = row0, c1 = row1;
     wave_totals<MB, kRowsPerWave>(acc, lane, wred);
     const int m = lane;
@@ -505,16 +495,19 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
 }
 
 // ---------------------------------------------------------------------------
-// Residual projections (o-proj, down-proj): fp32 partials x W^T per K-segment.
-// Grid: (row groups, K-segments, row tiles); k_resid_norm adds them to the
-// residual.
+// Residual projections, split-K form (o-proj; down when its activations do
+// not fit one workgroup's LDS): x W^T per K-segment.  Grid: (row groups,
+// K-segments, row tiles).  One segment: the residual add happens here
+// (h = T(h + T(x W^T)), batched_decoder_step.py:380-386, 399-403).  Several:
+// fp32 partials, added by k_resid_reduce in segment order (deterministic).
 // ---------------------------------------------------------------------------
 struct ResidArgs {
   const int32_t* done;
   const void* x;      // T [B, K]
   const void* w;      // T [N, K]
+  void* hidden;       // T [B, N]
   float* partial;     // [segments, B, N]
-  int B, N, K;
+  int B, N, K, segments;
 };
 
 // The body for one segment kind: FULL segments (len == kSeg) need no guards.
@@ -527,32 +520,41 @@ __device__ __forceinline__ void resid_segment(const ResidArgs& a, T* xs, float* 
   const int k0 = seg * kSeg;
   const int u = blockIdx.x * WAVES + wave;  // rows 2u, 2u+1
   const int units = a.N / 2;
+  const int uc = min(u, units - 1);
   const T* W = static_cast<const T*>(a.w);
-  // Flag, activations, then weights, as in k_proj; the weight loads are
-  // unconditional (clamped to a valid pair).
+  T* Hd = static_cast<T*>(a.hidden);
+  // Flag, residual values (single segment), activations, then weights; the
+  // weight loads are unconditional (clamped to a valid pair).
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  // (unconditional, clamped: used by lanes < MB of single-segment launches)
+  const size_t hrow = (size_t)min(b0 + lane, a.B - 1) * a.N;
+  const T h0 = Hd[hrow + 2 * uc], h1 = Hd[hrow + 2 * uc + 1];
   Vec8<T> xv[seg_vecs_per_thread<MB>()];
   load_rows_block<T, MB>(xv, static_cast<const T*>(a.x), a.K, b0, a.B, k0, len);
   Vec8<T> w[kSegChunks][kRowsPerWave];
-  const int uc = min(u, units - 1);
   const T* wr[kRowsPerWave] = {W + (size_t)(2 * uc) * a.K, W + (size_t)(2 * uc + 1) * a.K};
   load_rows<T, kRowsPerWave, FULL>(w, wr, k0, len, lane);
   __builtin_amdgcn_sched_barrier(0);
-  store_rows_block<T, MB>(xv, len, xs, kSeg);
+  store_rows_block<T, MB>(xv, b0, a.B, len, xs, kSeg);
   if (stop != 0 || u >= units) return;
   float acc[kRowsPerWave][MB];
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; ++r)
 #pragma unroll
     for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
-  dot_rows<T, MB, kRowsPerWave, FULL>(w, xs, kSeg, len, lane, acc);
+  dot_rows<T, MB, kRowsPerWave, FULL>(w, xs, kSeg, 0, len, lane, acc);
   float* wred = red + wave * (kRowsPerWave * MB);
   wave_totals<MB, kRowsPerWave>(acc, lane, wred);
   if (lane >= MB || b0 + lane >= a.B) return;
   const int b = b0 + lane;
+  if (a.segments == 1) {
+    Hd[(size_t)b * a.N + 2 * u] = Elt<T>::t(Elt<T>::f(h0) + Elt<T>::r(wred[0 * MB + lane]));
+    Hd[(size_t)b * a.N + 2 * u + 1] = Elt<T>::t(Elt<T>::f(h1) + Elt<T>::r(wred[1 * MB + lane]));
+  } else {
 #pragma unroll
-  for (int r = 0; r < kRowsPerWave; ++r)
-    a.partial[((size_t)seg * a.B + b) * a.N + 2 * u + r] = wred[r * MB + lane];
+    for (int r = 0; r < kRowsPerWave; ++r)
+      a.partial[((size_t)seg * a.B + b) * a.N + 2 * u + r] = wred[r * MB + lane];
+  }
 }
 
 template <typename T, int MB, int WAVES>
@@ -568,23 +570,37 @@ __global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
     resid_segment<T, MB, WAVES, false>(a, xs, red, seg, len);
 }
 
+// Sum of the segment partials in segment order, rounded to T, residual add.
+template <typename T>
+__global__ void k_resid_reduce(const int32_t* done, const float* partial, void* hidden, int B, int N,
+                               int segments) {
+  if (skip_step(done)) return;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * N) return;
+  float s = 0.f;
+  for (int sp = 0; sp < segments; ++sp) s += partial[(size_t)sp * B * N + i];
+  T* Hd = static_cast<T*>(hidden);
+  Hd[i] = Elt<T>::t(Elt<T>::f(Hd[i]) + Elt<T>::r(s));
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // Launcher
 // ---------------------------------------------------------------------------
 size_t normed_lds_bytes(int mb, int hidden, int dtype_bytes, int waves) {
-  return (size_t)mb * hidden * dtype_bytes + 3 * (size_t)waves * mb * kRowsPerWave * sizeof(float);
+  return (size_t)mb * hidden * dtype_bytes + (3 * (size_t)waves * kRowsPerWave + 4) * mb * sizeof(float);
 }
 size_t resid_lds_bytes(int mb, int dtype_bytes, int waves) {
   return (size_t)mb * kSeg * dtype_bytes + (size_t)waves * mb * kRowsPerWave * sizeof(float);
 }
 int k_segment_elems() { return kSeg; }
-int row_kernel_max_hidden() { return 8 * kRowThreads; }
+int row_kernel_max_hidden() { return 8 * 256 * kNormChunks; }
 
-// The step is a fixed list of launches: embed+norm, then per layer
-// [qkv, attention, o-proj, o-reduce+norm, gate/up, down, down-reduce+norm],
-// then the LM head.  [begin, end) selects a contiguous range of the list.
+// The step is a fixed list of launches: embed, then per layer [qkv,
+// attention, o-proj, o-reduce, gate/up, down, down-reduce], then the LM head.
+// The reduce entries launch nothing unless their projection runs split-K.
+// [begin, end) selects a contiguous range of the list.
 constexpr int kOpsPerLayer = 7;
 constexpr int kGateUpOp = 4;
 
@@ -612,34 +628,32 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     ++op;
     return w;
   };
-  RowArgs row{};
-  row.done = st.done;
-  row.hidden = sc.hidden;
-  row.xn = sc.xn;
-  row.B = B;
-  row.H = d.hidden;
-  row.V = d.vocab;
-  row.half = d.head_dim / 2;
-  row.eps = d.rms_eps;
   if (want()) {
-    RowArgs e = row;
+    EmbedArgs e{};
+    e.done = st.done;
     e.token = st.token;
     e.embedding = env.weights + env.embedding_off;
-    e.norm_w = env.weights + env.layer_off[0].input_norm;
+    e.hidden = sc.hidden;
     e.pos = st.pos;
     e.inv_freq = sc.inv_freq;
     e.rope = sc.rope;
-    k_embed_norm<T><<<B, kRowThreads, 0, stream>>>(e);
+    e.B = B;
+    e.H = d.hidden;
+    e.V = d.vocab;
+    e.half = d.head_dim / 2;
+    k_embed<T><<<B, 256, 0, stream>>>(e);
   }
   const size_t proj_smem = normed_lds_bytes(MB, d.hidden, sizeof(T), WAVES);
   const size_t resid_smem = resid_lds_bytes(MB, sizeof(T), WAVES);
+  const int reduce_blocks = (B * d.hidden + 255) / 256;
   for (int l = 0; l < d.layers; ++l) {
     const LayerOffsets& lo = env.layer_off[l];
     T* kc = static_cast<T*>(st.key_cache) + l * cache_layer_elems;
     T* vc = static_cast<T*>(st.value_cache) + l * cache_layer_elems;
     ProjArgs q{};
     q.done = st.done;
-    q.xn = sc.xn;
+    q.hidden = sc.hidden;
+    q.norm_w = env.weights + lo.input_norm;
     q.w0 = env.weights + lo.qkv_w;
     q.w1 = env.weights + lo.qkv_b;
     q.out = sc.q;
@@ -655,6 +669,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     q.heads = d.heads;
     q.kv_heads = d.kv_heads;
     q.head_dim = d.head_dim;
+    q.eps = d.rms_eps;
     if (want()) launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
 
     AttnArgs at{};
@@ -682,53 +697,51 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     o.done = st.done;
     o.x = sc.attn;
     o.w = env.weights + lo.o_w;
+    o.hidden = sc.hidden;
     o.partial = sc.partial;
     o.B = B;
     o.N = d.hidden;
     o.K = d.q_dim();
+    o.segments = p.o_segments;
     if (want())
       k_resid<T, MB, WAVES><<<dim3(p.o_grid, p.o_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(o);
-    if (want()) {
-      RowArgs r = row;
-      r.partial = sc.partial;
-      r.segments = p.o_segments;
-      r.norm_w = env.weights + lo.post_norm;
-      k_resid_norm<T><<<B, kRowThreads, 0, stream>>>(r);
-    }
+    if (want() && p.o_segments > 1)
+      k_resid_reduce<T><<<reduce_blocks, 256, 0, stream>>>(st.done, sc.partial, sc.hidden, B, d.hidden,
+                                                            p.o_segments);
 
     ProjArgs gu{};
     gu.done = st.done;
-    gu.xn = sc.xn;
+    gu.hidden = sc.hidden;
+    gu.norm_w = env.weights + lo.post_norm;
     gu.w0 = env.weights + lo.gate_w;
     gu.w1 = env.weights + lo.up_w;
     gu.out = sc.mlp;
     gu.B = B;
     gu.H = d.hidden;
     gu.units = d.intermediate;
+    gu.eps = d.rms_eps;
     if (want()) launch_proj<T, MB, WAVES, kGateUp>(gu, dim3(p.gu_grid, p.row_tiles), proj_smem, stream);
 
     ResidArgs dn{};
     dn.done = st.done;
     dn.x = sc.mlp;
     dn.w = env.weights + lo.down_w;
+    dn.hidden = sc.hidden;
     dn.partial = sc.partial;
     dn.B = B;
     dn.N = d.hidden;
     dn.K = d.intermediate;
+    dn.segments = p.down_segments;
     if (want())
       k_resid<T, MB, WAVES><<<dim3(p.down_grid, p.down_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(dn);
-    if (want()) {
-      // The next norm: layer l+1's input norm, or the final norm before the LM head.
-      RowArgs r = row;
-      r.partial = sc.partial;
-      r.segments = p.down_segments;
-      r.norm_w = env.weights + (l + 1 < d.layers ? env.layer_off[l + 1].input_norm : env.final_norm_off);
-      k_resid_norm<T><<<B, kRowThreads, 0, stream>>>(r);
-    }
+    if (want() && p.down_segments > 1)
+      k_resid_reduce<T><<<reduce_blocks, 256, 0, stream>>>(st.done, sc.partial, sc.hidden, B, d.hidden,
+                                                            p.down_segments);
   }
   ProjArgs lm{};
   lm.done = st.done;
-  lm.xn = sc.xn;
+  lm.hidden = sc.hidden;
+  lm.norm_w = env.weights + env.final_norm_off;
   lm.w0 = env.weights + env.lm_head_off;
   lm.logits = st.logits;
   lm.am_val = sc.am_val;
@@ -737,6 +750,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
   lm.B = B;
   lm.H = d.hidden;
   lm.units = d.vocab / 2;
+  lm.eps = d.rms_eps;
   if (want()) launch_proj<T, MB, WAVES, kLmHead>(lm, dim3(p.lm_grid, p.row_tiles), proj_smem, stream);
   return hipGetLastError();
 }

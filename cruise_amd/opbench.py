@@ -20,6 +20,7 @@ Examples::
 from __future__ import annotations
 
 import argparse
+import json
 import sys
 
 import numpy as np
@@ -73,6 +74,7 @@ def main() -> int:
     p.add_argument("--iters", type=int, default=20)
     p.add_argument("--context", type=int, default=128, help="tokens per row already in the KV cache")
     p.add_argument("--copy-bytes", type=int, default=0)
+    p.add_argument("--tuning", default="", help="JSON object of launch-plan overrides")
     args = p.parse_args()
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.iters)
@@ -89,6 +91,7 @@ def main() -> int:
         model=ModelSpec(),
         engine=EngineSpec(batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=capacity),
         weights=WeightSpec("synthetic", 1, 0.02),
+        tuning=json.loads(args.tuning) if args.tuning else {},
     )
     rt = ResidentEpochRuntime(cfg)
     try:

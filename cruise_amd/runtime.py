@@ -74,9 +74,15 @@ class EngineConfig:
     model: ModelSpec = field(default_factory=ModelSpec)
     engine: EngineSpec = field(default_factory=EngineSpec)
     weights: WeightSpec = field(default_factory=WeightSpec)
+    # Launch-plan overrides for tuning sweeps: qkv_grid, gu_grid, lm_grid
+    # (workgroup counts of the projections).
+    tuning: dict = field(default_factory=dict)
 
     def to_json(self) -> str:
-        return json.dumps({"model": asdict(self.model), "engine": asdict(self.engine), "weights": asdict(self.weights)})
+        doc = {"model": asdict(self.model), "engine": asdict(self.engine), "weights": asdict(self.weights)}
+        if self.tuning:
+            doc["tuning"] = dict(self.tuning)
+        return json.dumps(doc)
 
 
 def _ptr(value: Any) -> tuple[int, Any]:
