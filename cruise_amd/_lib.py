@@ -90,11 +90,19 @@ def library_path() -> Path:
     return Path(override) if override else LIBRARY_PATH
 
 
-def load() -> ctypes.CDLL:
-    """Load the HIP library (once) and bind every declared symbol."""
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load the HIP library (once per path) and bind every declared symbol.
+    ``path`` defaults to the in-tree build (or CRUISE_RESIDENT_EPOCH_LIBRARY)."""
     global _LIB
+    if path is not None and Path(path).resolve() != library_path().resolve():
+        return _bind(Path(path))
     if _LIB is not None:
         return _LIB
+    _LIB = _bind(library_path())
+    return _LIB
+
+
+def _bind(path: Path) -> ctypes.CDLL:
     # PyTorch-ROCm ships its own libamdhip64.so.7.  Importing it first makes
     # the library bind that same HIP runtime (same soname), so torch tensors
     # and the engine share one runtime and one device context per process.
@@ -102,7 +110,6 @@ def load() -> ctypes.CDLL:
         import torch  # noqa: F401
     except ImportError:  # pragma: no cover - torch is part of this image
         pass
-    path = library_path()
     if not path.is_file():
         raise RuntimeError(
             f"libresident_epoch.so is not built ({path}); run `python -m cruise_amd.build` "
@@ -113,5 +120,4 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
-    _LIB = lib
     return lib

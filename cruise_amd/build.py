@@ -17,6 +17,8 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 LIBDIR = PACKAGE / "lib"
 LIBRARY = LIBDIR / "libresident_epoch.so"
+SERVER = LIBDIR / "resident_epoch_server"
+SERVER_SOURCE = "re_server.cpp"
 INCLUDE = PACKAGE.parent / "include"
 SOURCES = ("re_step.hip", "re_attn.hip", "re_ctrl.hip", "re_engine.hip")
 
@@ -72,7 +74,26 @@ def build(verbose: bool = False, defines: tuple[str, ...] = (), output: Path | N
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
     os.replace(tmp, library)
+    if output is None:
+        build_server(library, SERVER)
     return library
+
+
+def build_server(library: Path = LIBRARY, output: Path = SERVER) -> Path:
+    """Compile the sidecar server (host C++ only) against ``library``; it
+    finds the library next to itself at run time (rpath $ORIGIN)."""
+    compiler = shutil.which("g++") or "g++"
+    tmp = output.with_name(output.name + ".tmp")
+    cmd = [
+        compiler, "-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{INCLUDE}", str(CSRC / SERVER_SOURCE),
+        f"-L{library.parent}", f"-l:{library.name}", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib",
+        "-o", str(tmp),
+    ]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"server build failed:\n{res.stderr[-4000:]}")
+    os.replace(tmp, output)
+    return output
 
 
 if __name__ == "__main__":

@@ -400,3 +400,25 @@ class ResidentEpochRuntime:
 
 def default_workdir_env() -> str | None:
     return os.getenv("CRUISE_ENGINE_WORKDIR")
+
+
+def write_weight_bundle(directory: str | Path, weights: dict[str, Any], inv_freq: Any | None = None) -> Path:
+    """Write a weight bundle the engine loads with "weights.source" =
+    "bundle": one raw little-endian file per tensor, named as the reference's
+    bundle (materialize_runtime_weights.py:53-80), plus the optional fp32
+    RoPE table ``inv_freq`` (materialize_runtime_weights.py:341-353)."""
+    out = Path(directory)
+    out.mkdir(parents=True, exist_ok=True)
+    items = dict(weights)
+    if inv_freq is not None:
+        items["inv_freq"] = inv_freq
+    for name, value in items.items():
+        if hasattr(value, "detach"):
+            value = value.detach().to("cpu").contiguous()
+            import torch
+
+            raw = value.view(-1).view(torch.uint8).numpy().tobytes()
+        else:
+            raw = np.ascontiguousarray(value).tobytes()
+        (out / name).write_bytes(raw)
+    return out
