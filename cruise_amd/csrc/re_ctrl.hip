@@ -2,6 +2,8 @@
 // generation continuity, row clear / KV import, per-step argmax and row update,
 // finish and emit (controller/g4c_b4_resident_epoch.cpp:177-622), plus the
 // synthetic weight fill.  Integer state, bit-exact with the reference.
+#include <algorithm>
+
 #include "re_device.h"
 #include "re_layout.h"
 
@@ -569,6 +571,29 @@ hipError_t launch_import_checksum(const KernelEnv& env, const StatePtrs& st, con
   c.block_bytes = (long long)d.block_size * d.kv_dim() * d.dtype_bytes;
   c.layer_bytes = (long long)d.slots() * d.kv_dim() * d.dtype_bytes;
   k_import_checksum<<<256, 256, 0, stream>>>(c);
+  return hipGetLastError();
+}
+
+// One workgroup column per (imported row, cache); 16-byte copies, coalesced.
+// The host has checked every source range against the mapped allocation.
+__global__ void __launch_bounds__(256) k_import_gather(ImportGatherArgs a) {
+  const int cache = blockIdx.z;  // 2 * layer + (0 for K, 1 for V)
+  const int layer = cache >> 1, kv = cache & 1;
+  const int row = a.rows[blockIdx.y];
+  const re_u32x4* src = reinterpret_cast<const re_u32x4*>(a.src[cache] + a.block_ids[row] * a.block_bytes);
+  re_u32x4* dst = reinterpret_cast<re_u32x4*>(
+      a.dst + (((long long)kv * a.layers + layer) * a.batch + row) * a.block_bytes);
+  const long long n = a.block_bytes / 16;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+    dst[i] = __builtin_nontemporal_load(src + i);
+}
+
+hipError_t launch_import_gather(const ImportGatherArgs& a, hipStream_t stream) {
+  if (a.nrows < 1 || a.nrows > 4 || a.layers < 1 || 2 * a.layers > kImportMaxCaches || a.block_bytes % 16 != 0)
+    return hipErrorInvalidValue;
+  const long long words = a.block_bytes / 16;
+  const int chunks = static_cast<int>(std::min<long long>((words + 255) / 256, 64));
+  k_import_gather<<<dim3(chunks, a.nrows, 2 * a.layers), 256, 0, stream>>>(a);
   return hipGetLastError();
 }
 

@@ -95,11 +95,17 @@ struct Engine {
   uint8_t* h_feed = nullptr;
   uint8_t* h_fetch = nullptr;
   size_t feed_bytes = 0, import_feed_bytes = 0, fetch_bytes = 0, payload_bytes = 0;
-  uint8_t* import_payload_scratch = nullptr;  // device, for checksum of the imported blocks
+  // Device-IPC import: mapped source allocations, keyed by the 64-byte
+  // handle, with their mapped sizes; closed when the engine is destroyed.
+  struct IpcMapping {
+    void* ptr;
+    size_t bytes;
+  };
+  std::map<std::string, IpcMapping> ipc_maps;
   unsigned long long* checksum_dev = nullptr;  // import Adler-32 partial sums [2]
 
-  // graphs keyed by (K * 2 + import) * 4 + part (0 whole epoch; 1 and 2 the
-  // halves around the timed launch)
+  // graphs keyed by (K * 3 + feed mode) * 4 + part (0 whole epoch; 1 and 2
+  // the halves around the timed launch)
   std::map<int, hipGraphExec_t> graphs;
   std::map<int, hipGraph_t> graph_defs;
   // Kernel timing: the gate/up launch of layer timing_layer in an epoch's last
@@ -478,14 +484,24 @@ StepPtrs epoch_step_ptrs(const Engine& e) {
 // finish, fetch copy.  part 1: everything before the timed launch (the
 // gate/up projection of timing_layer in the last step); part 2: everything
 // after it.
-hipError_t record_epoch(Engine& e, int K, bool importing, int part) {
+// How the epoch's inputs reach the device feed: the plain feed, an import
+// feed with its payload copied from the host (transfer file or the 8-input
+// ABI), or an import feed whose payload the device-IPC gather has already
+// written (only the part after the payload is copied).
+enum FeedMode : int { kFeedPlain = 0, kFeedHostImport = 1, kFeedDeviceImport = 2 };
+
+hipError_t record_epoch(Engine& e, int K, FeedMode mode, int part) {
+  const bool importing = mode != kFeedPlain;
   const KernelEnv env = e.env();
   const int nops = step_op_count(env);
   const int split = gateup_op_index(e.timing_layer);
   hipError_t err = hipSuccess;
   if (part != 2) {
-    const size_t feed = importing ? e.import_feed_bytes : e.feed_bytes;
-    if ((err = hipMemcpyAsync(e.st.feed, e.h_feed, feed, hipMemcpyHostToDevice, e.stream)) != hipSuccess) return err;
+    const size_t skip = mode == kFeedDeviceImport ? e.payload_bytes : 0;
+    const size_t feed = (importing ? e.import_feed_bytes : e.feed_bytes) - skip;
+    if ((err = hipMemcpyAsync(e.st.feed + skip, e.h_feed + skip, feed, hipMemcpyHostToDevice, e.stream)) !=
+        hipSuccess)
+      return err;
     if ((err = launch_ctrl_init(env, e.st, importing ? 1 : 0, e.stream)) != hipSuccess) return err;
     if ((err = launch_clear_rows(env, e.st, e.key_cache, e.value_cache, e.stream)) != hipSuccess) return err;
     if (importing &&
@@ -507,13 +523,13 @@ hipError_t record_epoch(Engine& e, int K, bool importing, int part) {
   return hipMemcpyAsync(e.h_fetch, e.st.fetch, e.fetch_bytes, hipMemcpyDeviceToHost, e.stream);
 }
 
-hipGraphExec_t epoch_graph(Engine& e, int K, bool importing, int part) {
-  const int key = (K * 2 + (importing ? 1 : 0)) * 4 + part;
+hipGraphExec_t epoch_graph(Engine& e, int K, FeedMode mode, int part) {
+  const int key = (K * 3 + mode) * 4 + part;
   auto it = e.graphs.find(key);
   if (it != e.graphs.end()) return it->second;
   hipGraph_t graph = nullptr;
   if (hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return nullptr;
-  hipError_t rec = record_epoch(e, K, importing, part);
+  hipError_t rec = record_epoch(e, K, mode, part);
   hipError_t end = hipStreamEndCapture(e.stream, &graph);
   if (rec != hipSuccess || end != hipSuccess || graph == nullptr) {
     if (graph) hipGraphDestroy(graph);
@@ -551,6 +567,7 @@ void free_engine(Engine* e) {
   if (e->dec_value) hipFree(e->dec_value);
   if (e->h_feed) hipHostFree(e->h_feed);
   if (e->h_fetch) hipHostFree(e->h_fetch);
+  for (auto& kv : e->ipc_maps) (void)hipIpcCloseMemHandle(kv.second.ptr);
   if (e->stream) hipStreamDestroy(e->stream);
   delete e;
 }
@@ -622,16 +639,102 @@ bool read_transfer(Engine& e, const char* path, uint64_t transfer_id, const int3
   return true;
 }
 
+// Exported allocations of 2 GiB or more are refused: opening such a handle
+// has been seen not to return on the ROCm 7 dmabuf IPC path.
+constexpr uint64_t kIpcMaxSourceBytes = 2ULL << 30;
+
+// The mapping of one exported allocation, opened once per engine.
+const Engine::IpcMapping* ipc_mapping(Engine& e, const char (&key)[CRUISE_RESIDENT_IPC_KEY_BYTES],
+                                      uint64_t source_bytes) {
+  const std::string id(key, CRUISE_RESIDENT_IPC_KEY_BYTES);
+  auto it = e.ipc_maps.find(id);
+  if (it == e.ipc_maps.end()) {
+    hipIpcMemHandle_t handle;
+    static_assert(sizeof(handle) == CRUISE_RESIDENT_IPC_KEY_BYTES, "HIP IPC handle size");
+    std::memcpy(&handle, key, sizeof(handle));
+    void* ptr = nullptr;
+    if (hipIpcOpenMemHandle(&ptr, handle, hipIpcMemLazyEnablePeerAccess) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t bytes = 0;
+    if (hipMemGetAddressRange(&base, &bytes, ptr) != hipSuccess || base != ptr) {
+      (void)hipGetLastError();
+      (void)hipIpcCloseMemHandle(ptr);
+      return nullptr;
+    }
+    it = e.ipc_maps.emplace(id, Engine::IpcMapping{ptr, bytes}).first;
+  }
+  // every source range was checked against source_bytes; the mapping must hold them
+  return it->second.bytes >= source_bytes ? &it->second : nullptr;
+}
+
+// ValidateIpcMetadata + PrepareDeviceIpcPayload (resident_epoch_bridge.cpp:
+// 156-243): check the record against the engine's geometry and the rows'
+// generations, map the exported allocations, and gather the imported blocks
+// into the device feed's payload region on the engine stream.  Cache slots
+// past 2 x layers (models with fewer than 28 layers) must be all zero.
+bool prepare_device_import(Engine& e, const ResidentEpochIpcMetadata* m, const int32_t* gens, int32_t& import_mask) {
+  const Dims& d = e.dims;
+  constexpr int kRows = 4;
+  const int caches = 2 * d.layers;
+  const uint64_t block_bytes = (uint64_t)d.block_size * d.kv_dim() * d.dtype_bytes;
+  if (d.batch != kRows || caches > CRUISE_RESIDENT_IPC_KEY_COUNT || caches > kImportMaxCaches || block_bytes % 16 != 0)
+    return false;
+  if (m->magic != CRUISE_RESIDENT_IPC_METADATA_MAGIC || m->version != CRUISE_RESIDENT_IPC_METADATA_VERSION ||
+      m->import_mask == 0 || m->import_mask >= (1u << kRows) || m->source_bytes >= kIpcMaxSourceBytes ||
+      m->source_bytes < (uint64_t)d.physical_blocks * block_bytes)
+    return false;
+  ImportGatherArgs g{};
+  for (int r = 0; r < kRows; ++r) {
+    const bool selected = (m->import_mask >> r) & 1u;
+    if (selected) {
+      if (m->row_generations[r] <= 0 || m->row_generations[r] != gens[r] || m->block_ids[r] < 0) return false;
+      g.rows[g.nrows++] = r;
+    } else if (m->row_generations[r] != 0 || m->block_ids[r] != 0) {
+      return false;
+    }
+    g.block_ids[r] = m->block_ids[r];
+  }
+  for (int c = 0; c < CRUISE_RESIDENT_IPC_KEY_COUNT; ++c) {
+    const char* key = m->keys[c];
+    const bool key_set = std::any_of(key, key + CRUISE_RESIDENT_IPC_KEY_BYTES, [](char v) { return v != 0; });
+    const uint64_t off = m->source_offsets[c];
+    if (c >= caches) {
+      if (key_set || off != 0) return false;
+      continue;
+    }
+    if (!key_set || off % 16 != 0 || off > m->source_bytes) return false;
+    for (int k = 0; k < g.nrows; ++k) {
+      const uint64_t end = ((uint64_t)m->block_ids[g.rows[k]] + 1) * block_bytes;
+      if (end > m->source_bytes - off) return false;
+    }
+  }
+  for (int c = 0; c < caches; ++c) {
+    const Engine::IpcMapping* map = ipc_mapping(e, m->keys[c], m->source_bytes);
+    if (map == nullptr) return false;
+    g.src[c] = static_cast<const uint8_t*>(map->ptr) + m->source_offsets[c];
+  }
+  g.dst = e.st.feed;
+  g.layers = d.layers;
+  g.batch = d.batch;
+  g.block_bytes = static_cast<long long>(block_bytes);
+  if (launch_import_gather(g, e.stream) != hipSuccess) return false;
+  import_mask = static_cast<int32_t>(m->import_mask);
+  return true;
+}
+
 // Launch one epoch.  Without timing it is one graph; with timing it is graph
 // part 1, the timed gate/up launch between two events, graph part 2 -- all on
 // the engine stream, still one feed copy and one fetch copy.
-bool run_graph(Engine& e, int K, bool importing) {
+bool run_graph(Engine& e, int K, FeedMode mode) {
   if (!e.timing) {
-    hipGraphExec_t g = epoch_graph(e, K, importing, 0);
+    hipGraphExec_t g = epoch_graph(e, K, mode, 0);
     return g != nullptr && hipGraphLaunch(g, e.stream) == hipSuccess;
   }
-  hipGraphExec_t pre = epoch_graph(e, K, importing, 1);
-  hipGraphExec_t post = epoch_graph(e, K, importing, 2);
+  hipGraphExec_t pre = epoch_graph(e, K, mode, 1);
+  hipGraphExec_t post = epoch_graph(e, K, mode, 2);
   if (pre == nullptr || post == nullptr) return false;
   const int op = gateup_op_index(e.timing_layer);
   return hipGraphLaunch(pre, e.stream) == hipSuccess && hipEventRecord(e.ev_start, e.stream) == hipSuccess &&
@@ -735,7 +838,7 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     *status = kCreateRuntime;
     return nullptr;
   }
-  if (re::epoch_graph(*e, 1, false, 0) == nullptr) {
+  if (re::epoch_graph(*e, 1, re::kFeedPlain, 0) == nullptr) {
     *status = kCreateGraph;
     return nullptr;
   }
@@ -779,7 +882,7 @@ extern "C" int32_t resident_epoch_execute(
       !read_transfer(*e, transfer_path, transfer_id, input_row_generations, import_mask, expected_checksum)) {
     return 13;
   }
-  if (direct_device_import) return 35;  // device IPC import is not available in this library
+  if (direct_device_import && !prepare_device_import(*e, ipc_metadata, input_row_generations, import_mask)) return 35;
   *output_model_calls = 0;
   *output_device_status = -1;
   *output_feed_calls = 0;
@@ -787,8 +890,12 @@ extern "C" int32_t resident_epoch_execute(
   *output_kv_import_checksum = 0;
   *output_wall_us = 0;
   *output_native_cpu_us = 0;
-  *output_declared_input_bytes = importing ? static_cast<int64_t>(e->import_feed_bytes)
-                                           : static_cast<int64_t>(e->feed_bytes);
+  // a device-IPC epoch declares what crossed the host boundary: the request
+  // and the metadata record (resident_epoch_bridge.cpp:42-43)
+  *output_declared_input_bytes =
+      direct_device_import ? static_cast<int64_t>(CRUISE_SIDECAR_REQUEST_BYTES + CRUISE_RESIDENT_IPC_METADATA_BYTES)
+      : importing          ? static_cast<int64_t>(e->import_feed_bytes)
+                           : static_cast<int64_t>(e->feed_bytes);
   *output_declared_output_bytes = static_cast<int64_t>(e->fetch_bytes);
   const int64_t cpu_start = process_cpu_us();
   std::fill(output_token_ids, output_token_ids + B * kMaxEpochSteps, -1);
@@ -837,7 +944,8 @@ extern "C" int32_t resident_epoch_execute(
 
   const auto wall_start = std::chrono::steady_clock::now();
   *output_commit_state = CRUISE_EPOCH_EXECUTING;
-  const bool launched = run_graph(*e, max_steps, importing);
+  const bool launched =
+      run_graph(*e, max_steps, direct_device_import ? kFeedDeviceImport : importing ? kFeedHostImport : kFeedPlain);
   *output_feed_calls = 1;
   if (!launched) return 30;
   const hipError_t synced = hipStreamSynchronize(e->stream);
@@ -851,8 +959,13 @@ extern "C" int32_t resident_epoch_execute(
   *output_device_status = result_control[3];
   *output_model_calls = result_control[4];
   *output_kv_import_checksum = result_control[5];
-  if (*output_device_status == 0 && importing && static_cast<uint32_t>(*output_kv_import_checksum) != expected_checksum)
-    return 34;
+  if (*output_device_status == 0) {
+    // a device-IPC import must prove itself with a checksum; a file import
+    // with the one its header carries
+    if (direct_device_import && *output_kv_import_checksum == 0) return 34;
+    if (importing && !direct_device_import && static_cast<uint32_t>(*output_kv_import_checksum) != expected_checksum)
+      return 34;
+  }
   for (int r = 0; r < B; ++r) {  // bridge.cpp:632-642
     const int32_t executed = result_control[6 + 2 * B + r];
     if (executed < 0 || executed > max_steps) return 33;
@@ -896,7 +1009,7 @@ extern "C" int32_t resident_epoch_proc(void* engine, const void* feed, int64_t f
   std::memcpy(&K, e->h_feed + ctl_off, 4);
   // An out-of-range K still runs a one-step graph: the device rejects it (201).
   const int graph_k = (K >= 1 && K <= kMaxEpochSteps) ? K : 1;
-  if (!run_graph(*e, graph_k, importing)) return -2;
+  if (!run_graph(*e, graph_k, importing ? kFeedHostImport : kFeedPlain)) return -2;
   if (hipStreamSynchronize(e->stream) != hipSuccess) return -2;
   collect_timing(*e, graph_k);
   std::memcpy(fetch, e->h_fetch, e->fetch_bytes);

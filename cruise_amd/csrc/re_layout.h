@@ -186,6 +186,20 @@ hipError_t launch_ctrl_finish(const KernelEnv& env, const StatePtrs& st, hipStre
 // Import mode: Adler-32 of the imported blocks as they sit in the caches.
 hipError_t launch_import_checksum(const KernelEnv& env, const StatePtrs& st, const void* key_cache,
                                   const void* value_cache, hipStream_t stream);
+// Device-IPC import: gather each imported row's source block of every cache
+// (2 x layers caches, mapped from another process) into the payload region
+// [K|V][layer][row][block] of the device feed, so the import epoch runs as a
+// host-file import would without the payload crossing the host.
+constexpr int kImportMaxCaches = 56;  // 2 x 28 layers: the IPC record's slots
+struct ImportGatherArgs {
+  const uint8_t* src[kImportMaxCaches];  // cache c's first byte (allocation base + offset)
+  uint8_t* dst;                          // the payload region of the device feed
+  long long block_ids[4];                // source block of each row
+  int rows[4];                           // imported rows, ascending
+  int nrows, layers, batch;
+  long long block_bytes;                 // a multiple of 16
+};
+hipError_t launch_import_gather(const ImportGatherArgs& a, hipStream_t stream);
 // Helpers for prefill / state management.
 hipError_t launch_clear_blocks(const KernelEnv& env, void* key_cache, void* value_cache,
                                const int32_t* blocks, int nblocks, hipStream_t stream);

@@ -23,7 +23,12 @@ extern "C" {
 #endif
 
 /* Device-IPC KV metadata, 4,088 bytes packed.
- * Same layout as native/resident_epoch_bridge.h:7-22. */
+ * Same layout as native/resident_epoch_bridge.h:7-22.  On MI355X each key
+ * slot holds the 64-byte hipIpcMemHandle_t of the allocation containing
+ * cache c (c = 2 * layer + 0 for K, 1 for V); source_offsets[c] is that
+ * cache's byte offset in the allocation (a multiple of 16), source_bytes the
+ * common allocation size (below 2 GiB), block_ids[r] the source block of
+ * imported row r.  Slots past 2 x layers are all zero. */
 #pragma pack(push, 1)
 typedef struct ResidentEpochIpcMetadata {
   uint64_t magic;
@@ -64,7 +69,10 @@ void *resident_epoch_create(const char *air_path, const char *graph_config,
  * row-major [row * 8 + step].  Return: 0 ok; 10 arguments; 11 row metadata;
  * 12 active rows != request_count; 13 transfer file; 30 epoch launch failed;
  * 31 epoch completion failed; 33 executed count out of range; 34 import
- * checksum mismatch; 35 IPC metadata.  A device fallback (201-212) returns 0
+ * checksum mismatch; 35 IPC metadata invalid or not mappable (the engine maps
+ * each exported allocation once and gathers the imported blocks device to
+ * device; handles from the calling process itself cannot be opened).
+ * A device fallback (201-212) returns 0
  * with *output_device_status set.  *output_commit_state goes PREPARED ->
  * EXECUTING (just before the one host-to-device copy) -> COMMITTED (after the
  * one device-to-host copy and the unpacking). */

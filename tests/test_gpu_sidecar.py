@@ -5,8 +5,9 @@ sidecar (sidecar_backend.py:67-462, backend.py:90-208).
 
 Tiny fp32 model from a weight bundle in /dev/shm.  Epochs are checked
 against the oracle controller fed what the bridge feeds (identity block
-table, BRIDGE:524-569): new generations, a continuation, and a host-snapshot
-KV import whose device checksum must equal the snapshot's.
+table, BRIDGE:524-569): new generations, a continuation, a host-snapshot
+KV import whose device checksum must equal the snapshot's, and a device-IPC
+import of KV blocks that never leave the GPU.
 """
 from __future__ import annotations
 
@@ -186,3 +187,43 @@ def test_snapshot_import_through_the_server(sidecar, oracle):
     assert not sidecar.transfer_path.exists()
     ref = oracle_epoch(oracle, plan, history_of(out, plan), payload=payload, mask=mask)
     check_against_oracle(out, plan, ref)
+
+
+def test_device_ipc_import_through_the_server(sidecar, oracle):
+    """The KV blocks stay on the GPU: this process holds the stock caches
+    (one [blocks, block_size, kv_heads, head] tensor per layer and cache),
+    exports their allocations with HIP IPC, and the server's engine maps them
+    and gathers the imported rows' blocks device to device."""
+    from types import SimpleNamespace
+
+    from cruise_amd.kv_transfer import capture_kv_device_transfer, release_kv_device_exports
+
+    backend = ResidentEpochBackend(sidecar)
+    g = torch.Generator().manual_seed(91)
+    shape = (W.geometry.physical_blocks, BS, W.dims.num_kv_heads, W.dims.head_dim)
+    caches = [tuple((torch.randn(shape, generator=g) * 0.25).cuda() for _ in range(2)) for _ in range(W.dims.num_layers)]
+    torch.cuda.synchronize()
+    worker = SimpleNamespace(model_runner=SimpleNamespace(kv_caches=caches))
+    blocks = {0: 5, 2: 2}
+    reqs = [
+        ResidentEpochRequest("ipc-0", 0, 31, 40, 4, 5, W.eos, (blocks[0],), (0, 1), kv_import_required=True),
+        ResidentEpochRequest("ipc-2", 2, 32, 41, 2, 3, W.eos, (blocks[2],), (4, 5), kv_import_required=True),
+    ]
+    plan = plan_of(reqs, steps=2)
+    transfer = capture_kv_device_transfer(worker, plan)
+    assert transfer.geometry == GEOMETRY and transfer.import_mask == 0b0101
+    # the payload the host path would have carried, for the checksum and the oracle
+    zero = torch.zeros(shape[1:])
+    parts = [[caches[l][kv][blocks[r]].cpu() if r in blocks else zero for l in range(W.dims.num_layers) for r in range(B)]
+             for kv in range(2)]
+    payload = b"".join(torch.stack(p).numpy().astype(np.float32).tobytes() for p in parts)
+    print("sidecar: device-IPC import K=2", flush=True)
+    out = backend.execute(plan, device_transfer=transfer)
+    result = get_result(out)
+    assert result.kv_transfer_mode == "device_ipc"
+    assert result.declared_input_bytes == 136 + 4088
+    assert result.kv_import_checksum == kv_payload_checksum(payload, 0b0101, GEOMETRY)
+    ref = oracle_epoch(oracle, plan, history_of(out, plan), payload=payload, mask=0b0101)
+    check_against_oracle(out, plan, ref)
+    release_kv_device_exports(worker)
+    del caches
