@@ -95,6 +95,10 @@ struct Engine {
   uint8_t* h_feed = nullptr;
   uint8_t* h_fetch = nullptr;
   size_t feed_bytes = 0, import_feed_bytes = 0, fetch_bytes = 0, payload_bytes = 0;
+  // Batched prefill scratch (grown on demand, freed with the engine).
+  uint8_t* pf_mem = nullptr;
+  size_t pf_bytes = 0;
+  bool pf_ready = false;
   // Device-IPC import: mapped source allocations, keyed by the 64-byte
   // handle, with their mapped sizes; closed when the engine is destroyed.
   struct IpcMapping {
@@ -568,6 +572,7 @@ void free_engine(Engine* e) {
   if (e->h_feed) hipHostFree(e->h_feed);
   if (e->h_fetch) hipHostFree(e->h_fetch);
   for (auto& kv : e->ipc_maps) (void)hipIpcCloseMemHandle(kv.second.ptr);
+  if (e->pf_mem) hipFree(e->pf_mem);
   if (e->stream) hipStreamDestroy(e->stream);
   delete e;
 }
@@ -1127,6 +1132,196 @@ extern "C" int32_t resident_epoch_prefill(void* engine, int32_t row, int32_t gen
             hipMemcpy(e->st.res_valid + row, &valid, 4, hipMemcpyHostToDevice) == hipSuccess &&
             hipStreamSynchronize(s) == hipSuccess;
   return ok ? 0 : -2;
+}
+
+namespace {
+
+// One pass of the decoder over the prompt tokens of several rows (see
+// resident_epoch_prefill_batch).  Token i of the pass is (row, position);
+// a row's tokens are consecutive and start at position 0.
+int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector<int32_t>& gens,
+                      const std::vector<std::vector<int64_t>>& prompts, const std::vector<int32_t>& tables) {
+  using namespace re;
+  const Dims& d = e.dims;
+  const int nr = static_cast<int>(rows.size());
+  const int bpr = d.blocks_per_row;
+  hipStream_t s = e.stream;
+  if (!e.pf_ready) {
+    if (prepare_prefill(d) != hipSuccess) return -2;
+    e.pf_ready = true;
+  }
+  // token table and attention tiles
+  std::vector<int64_t> tok;
+  std::vector<int32_t> pos, slot;
+  std::vector<int4> tiles;
+  for (int i = 0; i < nr; ++i) {
+    const int base = static_cast<int>(tok.size());
+    const int n = static_cast<int>(prompts[i].size()) - 1;  // positions 0 .. len-2 are prefilled
+    for (int p = 0; p < n; ++p) {
+      tok.push_back(prompts[i][p]);
+      pos.push_back(p);
+      slot.push_back(tables[i * bpr + p / d.block_size] * d.block_size + p % d.block_size);
+    }
+    for (int q = 0; q < n; q += 64) tiles.push_back(make_int4(base + q, base, std::min(64, n - q), q));
+  }
+  const int M = static_cast<int>(tok.size());
+  const size_t T = d.dtype_bytes;
+  const size_t I = d.intermediate, H = d.hidden;
+  // scratch layout
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = align_up(off + bytes, 256);
+    return at;
+  };
+  const size_t o_hidden = take(M * H * T), o_xn = take(M * H * T), o_qkv = take((size_t)M * d.qkv_rows() * T);
+  const size_t o_attn = take((size_t)M * d.q_dim() * T), o_gate = take(M * I * T), o_up = take(M * I * T);
+  const size_t o_mlp = take(M * I * T), o_rope = take((size_t)M * d.head_dim * sizeof(float));
+  const size_t o_tok = take(8 * (size_t)M), o_pos = take(4 * (size_t)M), o_slot = take(4 * (size_t)M);
+  const size_t o_tiles = take(sizeof(int4) * tiles.size()), o_blocks = take(4 * tables.size());
+  if (off > e.pf_bytes) {
+    if (e.pf_mem) hipFree(e.pf_mem);
+    e.pf_mem = nullptr;
+    e.pf_bytes = 0;
+    if (hipMalloc(&e.pf_mem, off) != hipSuccess) return -2;
+    e.pf_bytes = off;
+  }
+  uint8_t* b = e.pf_mem;
+  const bool ok = (M == 0 || (hipMemcpy(b + o_tok, tok.data(), 8 * M, hipMemcpyHostToDevice) == hipSuccess &&
+                              hipMemcpy(b + o_pos, pos.data(), 4 * M, hipMemcpyHostToDevice) == hipSuccess &&
+                              hipMemcpy(b + o_slot, slot.data(), 4 * M, hipMemcpyHostToDevice) == hipSuccess &&
+                              hipMemcpy(b + o_tiles, tiles.data(), sizeof(int4) * tiles.size(),
+                                        hipMemcpyHostToDevice) == hipSuccess)) &&
+                  hipMemcpy(b + o_blocks, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice) == hipSuccess;
+  if (!ok) return -2;
+  const KernelEnv env = e.env();
+  if (launch_clear_blocks(env, e.key_cache, e.value_cache, reinterpret_cast<const int32_t*>(b + o_blocks),
+                          static_cast<int>(tables.size()), s) != hipSuccess)
+    return -2;
+  if (M > 0) {
+    hipError_t err = hipSuccess;
+    auto run = [&](hipError_t r) {
+      if (err == hipSuccess) err = r;
+    };
+    PrefillRows er{};
+    er.token = reinterpret_cast<const int64_t*>(b + o_tok);
+    er.pos = reinterpret_cast<const int32_t*>(b + o_pos);
+    er.embedding = e.weights + e.embedding_off;
+    er.inv_freq = e.scratch.inv_freq;
+    er.hidden = b + o_hidden;
+    er.rope = reinterpret_cast<float*>(b + o_rope);
+    er.M = M;
+    er.H = d.hidden;
+    er.V = d.vocab;
+    er.head_dim = d.head_dim;
+    run(launch_prefill_embed(er, d.dtype_bytes, s));
+    int max_keys = 1;
+    for (const auto& p : prompts) max_keys = std::max(max_keys, static_cast<int>(p.size()) - 1);
+    const long long cache_layer_elems = d.slots() * d.kv_dim();
+    for (int l = 0; l < d.layers && err == hipSuccess; ++l) {
+      const LayerOffsets& lo = e.layer_off[l];
+      auto gemm = [&](size_t a_off, long long lda, size_t w_off, size_t bias_off, size_t out_off, long long ldo, int N,
+                      int K, int epi) {
+        GemmArgs g{};
+        g.A = b + a_off;
+        g.W = e.weights + w_off;
+        g.bias = bias_off == SIZE_MAX ? nullptr : e.weights + bias_off;
+        g.out = b + out_off;
+        g.M = M;
+        g.N = N;
+        g.K = K;
+        g.lda = lda;
+        g.ldw = K;
+        g.ldo = ldo;
+        run(launch_gemm(g, epi, d.dtype_bytes, s));
+      };
+      run(launch_prefill_rmsnorm(b + o_hidden, e.weights + lo.input_norm, b + o_xn, M, d.hidden, d.rms_eps,
+                                 d.dtype_bytes, s));
+      gemm(o_xn, d.hidden, lo.qkv_w, lo.qkv_b, o_qkv, d.qkv_rows(), d.qkv_rows(), d.hidden, kGemmStore);
+      PrefillQkv qp{};
+      qp.qkv = b + o_qkv;
+      qp.rope = er.rope;
+      qp.slot = reinterpret_cast<const int32_t*>(b + o_slot);
+      qp.key_cache = static_cast<uint8_t*>(e.key_cache) + l * cache_layer_elems * T;
+      qp.value_cache = static_cast<uint8_t*>(e.value_cache) + l * cache_layer_elems * T;
+      qp.slots = d.slots();
+      qp.M = M;
+      qp.ld = d.qkv_rows();
+      qp.heads = d.heads;
+      qp.kv_heads = d.kv_heads;
+      qp.head_dim = d.head_dim;
+      run(launch_prefill_qkv_post(qp, d.dtype_bytes, s));
+      PrefillAttn at{};
+      at.qkv = b + o_qkv;
+      at.out = b + o_attn;
+      at.pos = er.pos;
+      at.tiles = reinterpret_cast<const int4*>(b + o_tiles);
+      at.M = M;
+      at.ld = d.qkv_rows();
+      at.heads = d.heads;
+      at.kv_heads = d.kv_heads;
+      at.head_dim = d.head_dim;
+      at.score_ld = (max_keys + 63) / 64 * 64 + 8;
+      run(launch_prefill_attention(at, d, static_cast<int>(tiles.size()), s));
+      gemm(o_attn, d.q_dim(), lo.o_w, SIZE_MAX, o_hidden, d.hidden, d.hidden, d.q_dim(), kGemmResidual);
+      run(launch_prefill_rmsnorm(b + o_hidden, e.weights + lo.post_norm, b + o_xn, M, d.hidden, d.rms_eps,
+                                 d.dtype_bytes, s));
+      gemm(o_xn, d.hidden, lo.gate_w, SIZE_MAX, o_gate, d.intermediate, d.intermediate, d.hidden, kGemmStore);
+      gemm(o_xn, d.hidden, lo.up_w, SIZE_MAX, o_up, d.intermediate, d.intermediate, d.hidden, kGemmStore);
+      run(launch_prefill_swiglu(b + o_gate, b + o_up, b + o_mlp, (long long)M * d.intermediate, d.dtype_bytes, s));
+      gemm(o_mlp, d.intermediate, lo.down_w, SIZE_MAX, o_hidden, d.hidden, d.hidden, d.intermediate, kGemmResidual);
+    }
+    if (err != hipSuccess) return -2;
+  }
+  if (hipStreamSynchronize(s) != hipSuccess) return -2;
+  for (int i = 0; i < nr; ++i) {
+    const int r = rows[i];
+    const int32_t len = static_cast<int32_t>(prompts[i].size()), valid = 1;
+    const int64_t last_tok = prompts[i].back(), last_pos = len - 1;
+    const bool stored = hipMemcpy(e.st.res_gen + r, &gens[i], 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(e.st.res_token + r, &last_tok, 8, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(e.st.res_pos + r, &last_pos, 8, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(e.st.res_len + r, &len, 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(e.st.res_valid + r, &valid, 4, hipMemcpyHostToDevice) == hipSuccess;
+    if (!stored) return -2;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int32_t resident_epoch_prefill_batch(void* engine, int32_t n_rows, const int32_t* rows,
+                                                const int32_t* generations, const int64_t* prompts,
+                                                const int32_t* prompt_lens, const int32_t* block_tables) {
+  using namespace re;
+  Engine* e = static_cast<Engine*>(engine);
+  if (e == nullptr || rows == nullptr || generations == nullptr || prompts == nullptr || prompt_lens == nullptr ||
+      block_tables == nullptr)
+    return -1;
+  const Dims& d = e->dims;
+  if (n_rows < 1 || n_rows > d.batch) return -1;
+  std::vector<int> row_list(n_rows);
+  std::vector<int32_t> gens(generations, generations + n_rows);
+  std::vector<std::vector<int64_t>> prompt_list(n_rows);
+  std::vector<int32_t> tables(block_tables, block_tables + (size_t)n_rows * d.blocks_per_row);
+  std::vector<bool> seen(d.batch, false);
+  size_t at = 0;
+  for (int i = 0; i < n_rows; ++i) {
+    const int r = rows[i];
+    if (r < 0 || r >= d.batch || seen[r] || gens[i] <= 0) return -1;
+    seen[r] = true;
+    row_list[i] = r;
+    const int len = prompt_lens[i];
+    if (len < 1 || len > d.capacity || (len > 1 && (len - 2) / d.block_size >= d.blocks_per_row)) return -1;
+    prompt_list[i].assign(prompts + at, prompts + at + len);
+    at += len;
+    for (int64_t t : prompt_list[i])
+      if (t < 0 || t >= d.vocab) return -1;
+  }
+  for (int32_t blk : tables)
+    if (blk < 0 || blk >= d.physical_blocks) return -1;
+  std::lock_guard<std::mutex> lock(e->execute_mutex);
+  return prefill_batch(*e, row_list, gens, prompt_list, tables);
 }
 
 namespace {

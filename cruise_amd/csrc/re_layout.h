@@ -200,6 +200,53 @@ struct ImportGatherArgs {
   long long block_bytes;                 // a multiple of 16
 };
 hipError_t launch_import_gather(const ImportGatherArgs& a, hipStream_t stream);
+// Batched prefill (re_prefill.hip): M prompt tokens of several rows at once.
+struct PrefillRows {           // embedding + per-token RoPE table
+  const int64_t* token;        // [M]
+  const int32_t* pos;          // [M] position of each token in its row
+  const void* embedding;
+  const float* inv_freq;       // [d/2]
+  void* hidden;                // T [M, H]
+  float* rope;                 // [M, d/2, 2] cos, sin (rounded to T)
+  int M, H, V, head_dim;
+};
+struct PrefillQkv {            // RoPE in place + paged KV write
+  void* qkv;                   // T [M, ld]: q | k | v rows, bias included
+  const float* rope;
+  const int32_t* slot;         // [M] paged slot of each token
+  void* key_cache;             // this layer [slots, KVH, d]
+  void* value_cache;
+  long long slots;
+  int M, ld, heads, kv_heads, head_dim;
+};
+struct PrefillAttn {           // causal attention within each row's prompt
+  const void* qkv;             // T [M, ld] after RoPE
+  void* out;                   // T [M, heads * d]
+  const int32_t* pos;          // [M]
+  const int4* tiles;           // MFMA path: {first query token, row's first token, queries, first position}
+  int M, ld, heads, kv_heads, head_dim, score_ld;
+};
+enum GemmEpilogue : int { kGemmStore = 0, kGemmResidual = 1 };
+struct GemmArgs {              // out[M,N] (epilogue) A[M,K] W[N,K]^T
+  const void* A;
+  const void* W;
+  void* out;
+  const void* bias;            // [N] or null (store epilogue)
+  int M, N, K;
+  long long lda, ldw, ldo;
+};
+hipError_t launch_prefill_embed(const PrefillRows& a, int dtype_bytes, hipStream_t stream);
+hipError_t launch_prefill_rmsnorm(const void* x, const void* w, void* y, int M, int H, float eps, int dtype_bytes,
+                                  hipStream_t stream);
+hipError_t launch_prefill_swiglu(const void* gate, const void* up, void* out, long long n, int dtype_bytes,
+                                 hipStream_t stream);
+hipError_t launch_prefill_qkv_post(const PrefillQkv& a, int dtype_bytes, hipStream_t stream);
+hipError_t launch_gemm(const GemmArgs& a, int epi, int dtype_bytes, hipStream_t stream);
+// The MFMA attention serves bf16 models with head_dim 128 (64-query tiles).
+bool prefill_attention_mfma(const Dims& d);
+size_t prefill_attention_lds(const Dims& d, int max_keys);
+hipError_t prepare_prefill(const Dims& d);
+hipError_t launch_prefill_attention(const PrefillAttn& a, const Dims& d, int ntiles, hipStream_t stream);
 // Helpers for prefill / state management.
 hipError_t launch_clear_blocks(const KernelEnv& env, void* key_cache, void* value_cache,
                                const int32_t* blocks, int nblocks, hipStream_t stream);

@@ -134,6 +134,24 @@ int32_t resident_epoch_prefill(void *engine, int32_t row, int32_t generation,
                                const int64_t *prompt, int32_t prompt_len,
                                const int32_t *block_table_row);
 
+/* Batched prefill of new generations (no reference counterpart: the
+ * reference prefills on the host with stock vLLM and imports the KV).  For
+ * each of n_rows rows: clear the row's blocks (block_tables row i, BPR
+ * entries), write the K/V of prompt positions 0..len-2 to their paged slots,
+ * and record the row as resident with token prompt[len-1], position len-1,
+ * length len -- the state resident_epoch_prefill leaves, computed in one pass
+ * over all the rows' tokens per layer: GEMMs with M = tokens (MFMA for bf16),
+ * causal attention within each prompt.
+ * rows[n_rows] distinct, generations[n_rows] > 0, prompt_lens[n_rows] in
+ * [1, capacity], prompts: the prompts back to back (sum of lengths).
+ * Return 0, -1 bad arguments, -2 HIP failure. */
+int32_t resident_epoch_prefill_batch(void *engine, int32_t n_rows,
+                                     const int32_t *rows,
+                                     const int32_t *generations,
+                                     const int64_t *prompts,
+                                     const int32_t *prompt_lens,
+                                     const int32_t *block_tables);
+
 /* Named state access (host or device buffers of exactly the named size).
  * Names: any weight of the bundle ("embedding", "layers_3_q_weight", ...),
  * "key_cache", "value_cache" (resident caches [L,P,bs,KVH,d]), "logits"
