@@ -128,8 +128,14 @@ __global__ void __launch_bounds__(256) k_pf_qkv_post(PrefillQkv a) {
 // ---------------------------------------------------------------------------
 // GEMMs
 // ---------------------------------------------------------------------------
-constexpr int kGbm = 128, kGbn = 128, kGbk = 32;
-constexpr int kGld = kGbk + 8;  // LDS row stride in elements (80 bytes)
+// Workgroup tile 128 x 256, K-steps of 32; wave (wm, wn) of the 2 x 2 waves
+// owns a 64 x 128 block: 2 x 4 MFMA tiles of 32 x 32, so each fragment read
+// from LDS feeds 2 (B) or 4 (A) products.
+constexpr int kGbm = 128, kGbn = 256, kGbk = 32;
+constexpr int kGld = kGbk + 8;                  // LDS row stride in elements (80 bytes)
+constexpr int kGtm = 2, kGtn = 4;               // MFMA tiles per wave
+constexpr int kGva = kGbm * kGbk / 8 / 256;     // 16-byte vectors per thread, A tile
+constexpr int kGvb = kGbn * kGbk / 8 / 256;     // 16-byte vectors per thread, W tile
 
 template <int EPI>
 __device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int n, float y) {
@@ -142,6 +148,11 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int n, floa
   }
 }
 
+// Software pipeline: while the waves multiply K-tile kt out of LDS, tile
+// kt + 1 is in flight into registers, then goes to the other LDS buffer.
+// The barrier orders LDS only (the next prefetch may already be in flight);
+// the loads are unconditional (the last tile's addresses are clamped), so
+// each wait counts exactly.
 template <int EPI>
 __global__ void __launch_bounds__(256, 2) k_gemm_bf16(GemmArgs a) {
   __shared__ __align__(16) bf16_t As[2][kGbm * kGld];
@@ -151,71 +162,88 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf16(GemmArgs a) {
   const int m0 = blockIdx.y * kGbm, n0 = blockIdx.x * kGbn;
   const bf16_t* A = static_cast<const bf16_t*>(a.A);
   const bf16_t* W = static_cast<const bf16_t*>(a.W);
+  const int nk = (a.K + kGbk - 1) / kGbk;
   const re_u32x4 zero = {0u, 0u, 0u, 0u};
-  re_u32x4 ra[2], rb[2];
-  // 16-byte vector v of a 128 x 32 tile: row v / 4, columns (v % 4) * 8 ..+8.
-  // Rows past M or N read a valid row (clamped) whose results are never
-  // stored; columns past K read zeros.
-  auto gload = [&](int k0) {
+  struct Stage {
+    re_u32x4 a[kGva], b[kGvb];
+  };
+  Stage st;
+  // 16-byte vector v of a tile with 32 columns: row v / 4, columns
+  // (v % 4) * 8 ..+8.  Rows past M or N read a valid row (clamped) whose
+  // results are never stored; columns past K read as zeros.
+  auto gload = [&](Stage& s, int kt) {
+    const int k0 = min(kt, nk - 1) * kGbk;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kGva; ++i) {
       const int v = tid + 256 * i, row = v >> 2, k = k0 + (v & 3) * 8;
       const bool kin = k < a.K;
-      const int kk = kin ? k : 0;
-      const re_u32x4 x = *reinterpret_cast<const re_u32x4*>(A + (size_t)min(m0 + row, a.M - 1) * a.lda + kk);
-      const re_u32x4 y = *reinterpret_cast<const re_u32x4*>(W + (size_t)min(n0 + row, a.N - 1) * a.ldw + kk);
-      ra[i] = kin ? x : zero;
-      rb[i] = kin ? y : zero;
+      const re_u32x4 x = *reinterpret_cast<const re_u32x4*>(A + (size_t)min(m0 + row, a.M - 1) * a.lda + (kin ? k : 0));
+      s.a[i] = kin ? x : zero;
+    }
+#pragma unroll
+    for (int i = 0; i < kGvb; ++i) {
+      const int v = tid + 256 * i, row = v >> 2, k = k0 + (v & 3) * 8;
+      const bool kin = k < a.K;
+      const re_u32x4 y = *reinterpret_cast<const re_u32x4*>(W + (size_t)min(n0 + row, a.N - 1) * a.ldw + (kin ? k : 0));
+      s.b[i] = kin ? y : zero;
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](const Stage& s, int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int v = tid + 256 * i, row = v >> 2, c = (v & 3) * 8;
-      *reinterpret_cast<re_u32x4*>(&As[buf][row * kGld + c]) = ra[i];
-      *reinterpret_cast<re_u32x4*>(&Bs[buf][row * kGld + c]) = rb[i];
+    for (int i = 0; i < kGva; ++i) {
+      const int v = tid + 256 * i;
+      *reinterpret_cast<re_u32x4*>(&As[buf][(v >> 2) * kGld + (v & 3) * 8]) = s.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kGvb; ++i) {
+      const int v = tid + 256 * i;
+      *reinterpret_cast<re_u32x4*>(&Bs[buf][(v >> 2) * kGld + (v & 3) * 8]) = s.b[i];
     }
   };
-  f32x16_t acc[2][2];
+  f32x16_t acc[kGtm][kGtn];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kGtm; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < kGtn; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  const int nk = (a.K + kGbk - 1) / kGbk;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * kGbk);
+  auto mma_tile = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < kGbk / 16; ++ks) {
       // lane l supplies row l % 32 of its operand, elements (l / 32) * 8 ..+8
       const int kof = ks * 16 + (lane >> 5) * 8;
-      bf16x8_t af[2], bf[2];
+      bf16x8_t af[kGtm], bf[kGtn];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = lds_frag(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * kGld + kof]);
+      for (int i = 0; i < kGtm; ++i) af[i] = lds_frag(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * kGld + kof]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = lds_frag(&Bs[buf][(wn * 64 + j * 32 + (lane & 31)) * kGld + kof]);
+      for (int j = 0; j < kGtn; ++j) bf[j] = lds_frag(&Bs[buf][(wn * 128 + j * 32 + (lane & 31)) * kGld + kof]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < kGtm; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < kGtn; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
-    __syncthreads();
+  };
+  gload(st, 0);
+  sstore(st, 0);
+  lds_barrier();
+  for (int kt = 0; kt < nk; ++kt) {
+    gload(st, kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_tile(kt & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    sstore(st, (kt + 1) & 1);
+    lds_barrier();
   }
   // accumulator v of lane l: row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kGtm; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < kGtn; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        const int n = n0 + wn * 128 + j * 32 + (lane & 31);
         if (m < a.M && n < a.N) gemm_store<EPI>(a, m, n, acc[i][j][v]);
       }
 }
@@ -371,16 +399,29 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
   const float scale_div = sqrtf(static_cast<float>(kAd));
   const bf16_t neg_inf = 0xFF80;
 
-  // Scores: S[q][j] = bf16(bf16(q.k_j) / sqrt(d)), causal mask as -inf.
+  // A 64-row tile of keys (or values) in registers: vector v = tid + 256 i is
+  // row v / 16, elements (v % 16) * 8 ..+8; rows past the keys read the last.
+  re_u32x4 pre[4];
+  auto tile_load = [&](int kt, size_t col) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + 256 * i;
+      const int tok = r0 + min(min(kt, nkt - 1) * kAk + (v >> 4), nkeys - 1);
+      pre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + col + (v & 15) * 8);
+    }
+  };
+
+  // Scores: S[q][j] = bf16(bf16(q.k_j) / sqrt(d)), causal mask as -inf.  The
+  // next key tile is in flight while this one is multiplied.
+  tile_load(0, koff);
   for (int kt = 0; kt < nkt; ++kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int v = tid + 256 * i, key = v >> 4, c = (v & 15) * 8;
-      const int tok = r0 + min(kt * kAk + key, nkeys - 1);
-      *reinterpret_cast<re_u32x4*>(&kv[key * kAkld + c]) =
-          *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + koff + c);
+      const int v = tid + 256 * i;
+      *reinterpret_cast<re_u32x4*>(&kv[(v >> 4) * kAkld + (v & 15) * 8]) = pre[i];
     }
-    __syncthreads();
+    tile_load(kt + 1, koff);
+    lds_barrier();
     f32x16_t acc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.f;
@@ -396,8 +437,9 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
       const float s = round_bf16(round_bf16(acc[v]) / scale_div);
       S[qi * sld + kj] = kj <= p0 + qi ? f_to_bf16(s) : neg_inf;
     }
-    __syncthreads();
+    lds_barrier();
   }
+  tile_load(0, voff);  // the first value tile travels during the softmax
   // Softmax of each query row: four threads per row.
   {
     const int qi = tid >> 2, part = tid & 3;
@@ -415,7 +457,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
     for (int j = part; j < nkt * kAk; j += 4)
       srow[j] = j < nvalid ? f_to_bf16(expf(bf16_to_f(srow[j]) - mx) * inv) : static_cast<bf16_t>(0);
   }
-  __syncthreads();
+  lds_barrier();
   // O = P V, fp32 accumulation.
   f32x16_t o[2];
 #pragma unroll
@@ -426,16 +468,15 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i, key = v >> 4, c = (v & 15) * 8;
-      const int tok = r0 + min(kt * kAk + key, nkeys - 1);
-      const Vec8<bf16_t> row = Vec8<bf16_t>::load_cached(qkv + (size_t)tok * a.ld + voff + c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t w = row.v[e];
+        const uint32_t w = pre[i][e];
         kv[(c + 2 * e) * kAvld + key] = static_cast<bf16_t>(w & 0xffffu);
         kv[(c + 2 * e + 1) * kAvld + key] = static_cast<bf16_t>(w >> 16);
       }
     }
-    __syncthreads();
+    tile_load(kt + 1, voff);
+    lds_barrier();
 #pragma unroll
     for (int ks = 0; ks < kAk / 16; ++ks) {
       const bf16x8_t af = lds_frag(&S[(sm * 32 + (lane & 31)) * sld + kt * kAk + ks * 16 + (lane >> 5) * 8]);
@@ -445,7 +486,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr, o[t], 0, 0, 0);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   bf16_t* out = static_cast<bf16_t*>(a.out);
 #pragma unroll
