@@ -10,12 +10,18 @@ one device-to-host fetch per epoch).
 
 A benchmark "step" is one K=8 epoch.  ``value`` is decoded tokens per second
 (sum of executed steps over all rows / wall time of the timed epochs, inputs
-resident in HBM; each epoch is one graph launch).  ``roofline`` reports the
-gate/up projection (the dominant kernel: 54% of the streamed bytes): right
-after the timed epochs, with the engine in their final state, HIP events on
-the engine's stream bracket ``--kernel-iters`` back-to-back launches of it, so
-the mean per launch excludes launch gaps.  ``cpu_baseline`` times the
-oracle's CPU decoder step on the host cores.
+resident in HBM; each epoch is one graph launch).
+
+``roofline`` reports the dominant kernel.  With the persistent step kernel
+(``--fused``) that is the kernel itself: one launch runs the 28
+layers and the LM head of a decoder step, so its algorithmic bytes are the
+step's streamed weights (14,141,238,272 B) and its launch duration is timed
+with HIP events on the engine's stream around the last step of each of
+``--kernel-epochs`` further epochs (the rest of each epoch runs as graphs
+before and after it).  With the per-op path (the default) it is the gate/up
+projection (54% of the streamed bytes), timed over ``--kernel-iters``
+back-to-back launches.  ``cpu_baseline`` times the oracle's CPU decoder step
+on the host cores.
 """
 from __future__ import annotations
 
@@ -43,6 +49,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-steps", type=int, default=48)
     p.add_argument("--kernel-iters", type=int, default=50)
+    p.add_argument("--kernel-epochs", type=int, default=10)
+    p.add_argument("--fused", action="store_true", help="run each decoder step as the persistent step kernel")
     return p.parse_args()
 
 
@@ -65,7 +73,9 @@ def main() -> int:
     K = args.epoch_steps
     cfg = EngineConfig(
         model=ModelSpec(),
-        engine=EngineSpec(batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=256),
+        engine=EngineSpec(
+            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=256, fused_step=args.fused
+        ),
         weights=WeightSpec(source="synthetic", seed=args.seed, std=0.02),
     )
     t0 = time.time()
@@ -131,22 +141,39 @@ def main() -> int:
         run_epoch(True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
-    # gate/up of the middle layer, timed on the engine's stream (HIP events)
-    gu_op = rt.op_index(rt.info("timing_layer"), "gate_up")
-    gu_avg_ms = rt.time_ops(gu_op, gu_op + 1, args.kernel_iters)
     tok_s = executed_total / elapsed
     ms_per_epoch = elapsed * 1e3 / args.steps
     streamed = rt.info("streamed_weight_bytes")
     decoder_steps = executed_total / B
     ms_per_decoder_step = elapsed * 1e3 / decoder_steps
     step_gbs = streamed / (ms_per_decoder_step * 1e-3) / 1e9
-    inter = rt.info("intermediate")
-    hidden = rt.info("hidden")
-    gu_bytes = 2 * inter * hidden * 2 + hidden * 2 + B * hidden * 2 + B * inter * 2
-    gu_gbs = gu_bytes / (gu_avg_ms * 1e-3) / 1e9
+    fused = rt.info("fused_step") == 1
+    if fused:
+        # The persistent step kernel of each epoch's last step, between HIP
+        # events on the engine's stream (untimed epochs after the timed ones).
+        rt.enable_kernel_timing(True)
+        for _ in range(args.kernel_epochs):
+            run_epoch(False)
+        torch.cuda.synchronize()
+        launches = rt.timed_launch_ms()
+        rt.enable_kernel_timing(False)
+        if not launches:
+            raise RuntimeError("no timed launch of the step kernel completed")
+        k_avg_ms = statistics.mean(launches)
+        k_bytes = streamed
+        k_name = f"persistent decoder-step kernel k_step_fused ({rt.info('fused_grid')} workgroups; 28 layers + LM head per launch)"
+    else:
+        # gate/up of the middle layer, timed on the engine's stream (HIP events)
+        gu_op = rt.op_index(rt.info("timing_layer"), "gate_up")
+        k_avg_ms = rt.time_ops(gu_op, gu_op + 1, args.kernel_iters)
+        inter = rt.info("intermediate")
+        hidden = rt.info("hidden")
+        k_bytes = 2 * inter * hidden * 2 + hidden * 2 + B * hidden * 2 + B * inter * 2
+        k_name = "gate/up projection (k_proj<bf16,4,4,GateUp>)"
+    k_gbs = k_bytes / (k_avg_ms * 1e-3) / 1e9
     log(
         f"{tok_s:.1f} tok/s, {ms_per_decoder_step:.3f} ms/decoder step, {step_gbs:.0f} GB/s step, "
-        f"gate/up {gu_avg_ms * 1e3:.1f} us ({gu_gbs:.0f} GB/s)"
+        f"{'step kernel' if fused else 'gate/up'} {k_avg_ms * 1e3:.1f} us ({k_gbs:.0f} GB/s)"
     )
 
     cpu = None
@@ -183,14 +210,14 @@ def main() -> int:
         "d2h_copies_per_epoch": 1,
         "roofline": {
             "bound": "hbm",
-            "kernel": "gate/up projection (k_proj<bf16,4,4,GateUp>)",
-            "achieved": round(gu_gbs, 1),
+            "kernel": k_name,
+            "achieved": round(k_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes(),
-            "avg_launch_us": round(gu_avg_ms * 1e3, 2),
-            "algorithmic_bytes_per_launch": gu_bytes,
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_bytes(fused),
+            "avg_launch_us": round(k_avg_ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": k_bytes,
         },
         "cpu_baseline": cpu,
     }
@@ -198,11 +225,12 @@ def main() -> int:
     return 0
 
 
-def traffic_bytes():
-    """HBM bytes per gate/up launch from the committed rocprofv3 PMC passes
-    (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a
-    plain copy of known size): profiles/gate_up_qwen7b_b4_traffic.md."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_qwen7b_b4_traffic.json")
+def traffic_bytes(fused: bool):
+    """HBM bytes per launch of the reported kernel from the committed
+    rocprofv3 PMC passes (FETCH_SIZE and WRITE_SIZE, each scaled by what the
+    counter reads for a plain copy of known size), or None without them."""
+    name = "step_kernel_qwen7b_b4_traffic.json" if fused else "gate_up_qwen7b_b4_traffic.json"
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])

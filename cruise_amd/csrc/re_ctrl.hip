@@ -21,6 +21,7 @@ struct CtrlArgs {
   const float* am_val;
   const int32_t* am_idx;
   const int32_t* am_bad;
+  const int32_t* model_abort;  // persistent step kernel's abort flag (nullptr: per-op path)
   int has_payload;
 };
 
@@ -313,6 +314,13 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   const int call = ++(*s.model_calls);
   int64_t* history = reinterpret_cast<int64_t*>(s.fetch);
   int32_t status = kStatusOk;
+  // A step kernel that could not complete is a failed model call (CTRL:494-497).
+  if (a.model_abort != nullptr && *a.model_abort != 0) {
+    for (int r = 0; r < B; ++r) s.reason[r] = kFinishFallback;
+    *s.status = kStatusModelError;
+    *s.done = 1;
+    return;
+  }
   // next_position = where(active, pos + 1, pos) (batched_decoder_step.py:409-411)
   for (int r = 0; r < B; ++r) {
     const int64_t next_pos = s.cur_active[r] != 0 ? s.cur_pos[r] + 1 : s.cur_pos[r];
@@ -524,6 +532,7 @@ static CtrlArgs ctrl_args(const KernelEnv& env, const StatePtrs& st) {
   a.am_val = env.scratch.am_val;
   a.am_idx = env.scratch.am_idx;
   a.am_bad = env.scratch.am_bad;
+  a.model_abort = env.plan.fused ? env.scratch.sync : nullptr;
   return a;
 }
 

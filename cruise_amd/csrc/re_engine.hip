@@ -120,6 +120,7 @@ struct Engine {
   std::vector<float> timing_ms;
 
   std::mutex execute_mutex;
+  bool trace_step = false;  // "engine": {"trace_step": true}: persistent kernel phase trace
 
   KernelEnv env() const {
     KernelEnv e{};
@@ -238,6 +239,18 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.gu_grid = std::max(1, static_cast<int>(t->number_or("gu_grid", p.gu_grid)));
     p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));
     p.lm_wg = p.lm_grid;
+  }
+  // The persistent step kernel serves the shapes it is written for when the
+  // configuration asks for it ("engine": {"fused_step": true}).
+  const Json* eng = cfg.get("engine");
+  e.trace_step = eng != nullptr && eng->bool_or("trace_step", false);
+  p.fused = 0;
+  p.fused_grid = 0;
+  if (eng != nullptr && eng->bool_or("fused_step", false) && fused_step_eligible(d)) {
+    p.fused_grid = fused_grid(d, e.cus);
+    if (const Json* t = cfg.get("tuning")) p.fused_grid = static_cast<int>(t->number_or("fused_grid", p.fused_grid));
+    p.fused = p.fused_grid >= 1 && p.fused_grid <= fused_grid(d, e.cus) ? 1 : 0;
+    if (p.fused) p.lm_wg = p.fused_grid;
   }
   p.o_grid = (d.hidden / 2 + p.waves - 1) / p.waves;
   p.down_grid = p.o_grid;
@@ -362,6 +375,10 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},
+      {reinterpret_cast<void**>(&e.scratch.sync), (size_t)fused_sync_ints(d) * sizeof(int32_t)},
+      {&e.scratch.fused_layers, fused_layer_table_bytes(d)},
+      {reinterpret_cast<void**>(&e.scratch.step_trace), e.trace_step ? fused_trace_bytes(d, p.fused_grid) : 0},
+      {&e.scratch.fused_act, p.fused ? fused_act_bytes(d) : 0},
   };
   off = 0;
   offs.clear();
@@ -372,6 +389,7 @@ bool alloc_state(Engine& e) {
   if (hipMalloc(&e.scratch_mem, off) != hipSuccess) return false;
   if (hipMemset(e.scratch_mem, 0, off) != hipSuccess) return false;
   for (size_t i = 0; i < sp.size(); ++i) *sp[i].p = e.scratch_mem + offs[i];
+  if (!e.trace_step) e.scratch.step_trace = nullptr;
   e.st.import_sum = e.checksum_dev;
 
   // decoder-step ABI inputs
@@ -498,7 +516,7 @@ hipError_t record_epoch(Engine& e, int K, FeedMode mode, int part) {
   const bool importing = mode != kFeedPlain;
   const KernelEnv env = e.env();
   const int nops = step_op_count(env);
-  const int split = gateup_op_index(e.timing_layer);
+  const int split = timed_op_index(env, e.timing_layer);
   hipError_t err = hipSuccess;
   if (part != 2) {
     const size_t skip = mode == kFeedDeviceImport ? e.payload_bytes : 0;
@@ -741,7 +759,7 @@ bool run_graph(Engine& e, int K, FeedMode mode) {
   hipGraphExec_t pre = epoch_graph(e, K, mode, 1);
   hipGraphExec_t post = epoch_graph(e, K, mode, 2);
   if (pre == nullptr || post == nullptr) return false;
-  const int op = gateup_op_index(e.timing_layer);
+  const int op = timed_op_index(e.env(), e.timing_layer);
   return hipGraphLaunch(pre, e.stream) == hipSuccess && hipEventRecord(e.ev_start, e.stream) == hipSuccess &&
          launch_step_ops(e.env(), epoch_step_ptrs(e), e.stream, op, op + 1) == hipSuccess &&
          hipEventRecord(e.ev_stop, e.stream) == hipSuccess && hipGraphLaunch(post, e.stream) == hipSuccess;
@@ -819,7 +837,8 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     *status = kCreateDevice;
     return nullptr;
   }
-  if (hipMemset(e->weights, 0, e->weight_bytes) != hipSuccess) {
+  if (hipMemset(e->weights, 0, e->weight_bytes) != hipSuccess ||
+      write_fused_layer_table(e->dims, e->weights, e->layer_off.data(), e->scratch.fused_layers) != hipSuccess) {
     *status = kCreateDevice;
     return nullptr;
   }
@@ -1344,6 +1363,10 @@ int32_t state_access(Engine* e, const char* name, void* buf, int64_t bytes, Acce
   } else if (n == "logits") {
     dev = e->logits;
     size = (size_t)d.batch * d.vocab * sizeof(float);
+  } else if (n == "step_trace") {
+    if (e->scratch.step_trace == nullptr) return -1;
+    dev = e->scratch.step_trace;
+    size = fused_trace_bytes(d, e->plan.fused_grid);
   } else if (n == "inv_freq") {
     dev = e->scratch.inv_freq;
     size = (size_t)d.head_dim / 2 * sizeof(float);
@@ -1432,7 +1455,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"streamed_weight_bytes", static_cast<int64_t>(e->streamed_weight_bytes)},
       {"configured_eos", d.configured_eos},
       {"step_ops", re::step_op_count(e->env())},
-      {"ops_per_layer", 7},
+      {"ops_per_layer", e->plan.fused ? 0 : 7},
       {"timing_layer", e->timing_layer},
       {"qkv_grid", e->plan.qkv_grid},
       {"o_segments", e->plan.o_segments},
@@ -1440,6 +1463,8 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"gateup_grid", e->plan.gu_grid},
       {"down_segments", e->plan.down_segments},
       {"lm_grid", e->plan.lm_grid},
+      {"fused_step", e->plan.fused},
+      {"fused_grid", e->plan.fused_grid},
       {"compute_units", e->cus},
   };
   auto it = facts.find(k);

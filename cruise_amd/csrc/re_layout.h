@@ -123,6 +123,10 @@ struct Scratch {
   int32_t* am_bad;    // non-finite flags [nwg, B]
   float* inv_freq;    // fp32 [d/2]
   float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
+  int32_t* sync;      // persistent step kernel: abort flag + phase counters
+  void* fused_layers; // persistent step kernel: per-layer weight pointers [L]
+  unsigned long long* step_trace;  // persistent step kernel phase trace (nullptr: off)
+  void* fused_act;    // persistent step kernel: per-layer activation blocks
 };
 
 struct LaunchPlan {
@@ -132,6 +136,8 @@ struct LaunchPlan {
   int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)
+  int fused;       // 1: a step is the persistent kernel (re_fused.hip)
+  int fused_grid;  // its workgroups: the chip's resident capacity
 };
 
 // Arguments of the paged decode attention (re_attn.hip).
@@ -173,7 +179,25 @@ struct KernelEnv {
 hipError_t launch_decoder_step(const KernelEnv& env, const StepPtrs& step, hipStream_t stream);
 hipError_t launch_step_ops(const KernelEnv& env, const StepPtrs& step, hipStream_t stream, int begin, int end);
 int step_op_count(const KernelEnv& env);
-int gateup_op_index(int layer);
+// The op whose launch the epoch timing brackets: layer's gate/up projection
+// (per-op path) or the persistent step kernel.
+int timed_op_index(const KernelEnv& env, int layer);
+// Persistent step kernel (re_fused.hip): bf16, B <= 4, hidden = q_dim = 3584,
+// head_dim 128.  Ops: 0 = embedding + counter reset, 1 = the kernel.
+bool fused_step_eligible(const Dims& d);
+size_t fused_lds_bytes(const Dims& d);
+size_t fused_layer_table_bytes(const Dims& d);
+int fused_sync_ints(const Dims& d);
+int fused_grid(const Dims& d, int cus);
+size_t fused_trace_bytes(const Dims& d, int grid);
+// Byte offsets inside one layer's activation block of the persistent kernel.
+struct FusedActLayout {
+  size_t q, attn, mlp, h_mid, h_out, stride;
+};
+FusedActLayout fused_act_layout(const Dims& d);
+size_t fused_act_bytes(const Dims& d);
+hipError_t write_fused_layer_table(const Dims& d, const uint8_t* weights, const LayerOffsets* lo, void* dst);
+hipError_t launch_fused_ops(const KernelEnv& env, const StepPtrs& st, hipStream_t stream, int begin, int end);
 // Grid sizes of the grid-stride projections from the kernels' occupancy.
 void plan_grids(LaunchPlan& p, const Dims& d, int cus);
 // Controller kernels.

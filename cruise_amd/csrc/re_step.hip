@@ -26,6 +26,7 @@
 // SwiGLU and the argmax partials are fused into the epilogues; rounding
 // points follow the reference decoder (see the per-kernel comments).
 #include "re_device.h"
+#include "re_gemv.h"
 #include "re_layout.h"
 
 namespace re {
@@ -37,192 +38,6 @@ namespace {
 #ifndef NORMED_MIN_WAVES
 #define NORMED_MIN_WAVES 4
 #endif
-
-constexpr int kRowsPerWave = 2;
-constexpr int kChunk = 512;     // elements covered by one wave-wide 16-byte load
-constexpr int kSegChunks = 7;   // chunks per K-segment
-constexpr int kSeg = kChunk * kSegChunks;
-
-__device__ __forceinline__ bool skip_step(const int32_t* done) {
-  return done != nullptr && __builtin_nontemporal_load(done) != 0;
-}
-
-// Issue the loads of RPW weight rows over the segment [k0, k0 + len): chunk c
-// of lane l covers elements k0 + c*512 + l*8 .. +8.  Chunks past len are left
-// unset (dot_rows skips them), so no value merge forces an early wait.
-// FULL: the segment holds all kSegChunks chunks (len == kSeg), no guards.
-template <typename T, int RPW, bool FULL = false>
-__device__ __forceinline__ void load_rows(Vec8<T> (&w)[kSegChunks][RPW], const T* const (&wr)[RPW], int k0,
-                                          int len, int lane) {
-#pragma unroll
-  for (int c = 0; c < kSegChunks; ++c) {
-    const int k = c * kChunk + lane * 8;
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
-      if (FULL || k < len) w[c][r] = Vec8<T>::load(wr[r] + k0 + k);
-  }
-}
-
-// acc[r][m] += sum over the segment of W_r[k] * xs[m][k0 + k] (xs: LDS, row
-// stride ldx).
-template <typename T, int MB, int RPW, bool FULL = false>
-__device__ __forceinline__ void dot_rows(const Vec8<T> (&w)[kSegChunks][RPW], const T* xs, int ldx, int k0, int len,
-                                         int lane, float (&acc)[RPW][MB]) {
-#pragma unroll
-  for (int c = 0; c < kSegChunks; ++c) {
-    const int k = c * kChunk + lane * 8;
-    if (FULL || k < len) {
-#pragma unroll
-      for (int m = 0; m < MB; ++m) {
-        const Vec8<T> x = Vec8<T>::load_cached(xs + m * ldx + k0 + k);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[r][m] = dot8(w[c][r], x, acc[r][m]);
-      }
-    }
-  }
-}
-
-// Reduce acc over the wave and leave the totals in red[r*MB + m] (LDS).
-template <int MB, int RPW>
-__device__ __forceinline__ void wave_totals(float (&acc)[RPW][MB], int lane, float* red) {
-  constexpr int N = MB * RPW;
-  float v[N];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r)
-#pragma unroll
-    for (int m = 0; m < MB; ++m) v[r * MB + m] = acc[r][m];
-  wave_reduce_transpose<N>(v, lane);
-  if ((lane & (64 / N - 1)) == 0) red[lane / (64 / N)] = v[0];
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-}
-
-// Vec8 slots a 256-thread workgroup needs to hold MB rows of one K-segment.
-template <int MB>
-constexpr int seg_vecs_per_thread() {
-  return (MB * kSeg / 8 + 255) / 256;
-}
-
-// Load rows b0..b0+MB-1, columns [k0, k0+len), of X [B, ldg] into registers:
-// slot i of thread t holds Vec8 number t + 256*i of the row-major [MB, len]
-// block.  The loads are unconditional (addresses clamped into the block), so
-// no branch separates them from later loads and every wait counts exactly;
-// store_rows_block zeroes what lies outside.
-template <typename T, int MB>
-__device__ __forceinline__ void load_rows_block(Vec8<T> (&v)[seg_vecs_per_thread<MB>()], const T* __restrict__ X,
-                                                int ldg, int b0, int B, int k0, int len) {
-  const int per_row = max(len / 8, 1);
-#pragma unroll
-  for (int i = 0; i < seg_vecs_per_thread<MB>(); ++i) {
-    const int idx = min((int)threadIdx.x + 256 * i, MB * per_row - 1);
-    const int m = idx / per_row, k = (idx - m * per_row) * 8;
-    v[i] = Vec8<T>::load_cached(X + (size_t)min(b0 + m, B - 1) * ldg + k0 + k);
-  }
-}
-
-// Store the block loaded by load_rows_block into LDS xs [MB, ldx] (rows >= B
-// as zero), then a workgroup barrier.
-template <typename T, int MB>
-__device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per_thread<MB>()], int b0, int B, int len,
-                                                 T* xs, int ldx) {
-  constexpr int NV = seg_vecs_per_thread<MB>();
-  const int per_row = len / 8;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = threadIdx.x + 256 * i;
-    if (idx < MB * per_row) {
-      const int m = idx / per_row, k = (idx - m * per_row) * 8;
-      *reinterpret_cast<Vec8<T>*>(xs + m * ldx + k) = b0 + m < B ? v[i] : Vec8<T>{};
-    }
-  }
-  lds_barrier();  // weight loads issued before the staging stay in flight
-}
-
-// ---------------------------------------------------------------------------
-// Norm prologue: RMSNorm of rows b0..b0+MB-1 of the residual stream into LDS
-// (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
-// cast to T, then a T x T product with the weight.  Thread t owns hidden
-// chunks t and t + 256 (8 elements each) of every row, so it needs the norm
-// weight of two chunks only.  Requires blockDim.x == 256, H <= 4096.
-// ---------------------------------------------------------------------------
-constexpr int kNormChunks = 2;
-
-template <typename T, int MB>
-struct NormIn {
-  Vec8<T> h[MB][kNormChunks];
-  Vec8<T> w[kNormChunks];
-};
-
-template <typename T, int MB>
-__device__ __forceinline__ void norm_load(NormIn<T, MB>& in, const T* __restrict__ hidden, const T* __restrict__ norm_w,
-                                          int b0, int B, int H) {
-  // unconditional (clamped) loads; norm_to_lds ignores what lies outside
-  const int per_row = H / 8;
-#pragma unroll
-  for (int j = 0; j < kNormChunks; ++j) {
-    const int c = min((int)threadIdx.x + 256 * j, per_row - 1);
-    in.w[j] = Vec8<T>::load_cached(norm_w + c * 8);
-#pragma unroll
-    for (int m = 0; m < MB; ++m)
-      in.h[m][j] = Vec8<T>::load_cached(hidden + (size_t)min(b0 + m, B - 1) * H + c * 8);
-  }
-}
-
-// The raw rows go to LDS as they arrive (the per-row sums of squares formed
-// on the way), so the hidden values are dead before the block reduction; after
-// it each thread normalizes its own chunks in place.  red: LDS scratch of at
-// least 4 * MB floats.
-template <typename T, int MB>
-__device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int B, int H, float eps, T* xs,
-                                            float* red) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int per_row = H / 8;
-  float ss[MB];
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < kNormChunks; ++j) {
-      const int c = tid + 256 * j;
-      const bool ok = c < per_row && b0 + m < B;
-      const Vec8<T> h = ok ? in.h[m][j] : Vec8<T>{};
-      if (c < per_row) *reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8) = h;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = h.get(e);
-        s = fmaf(x, x, s);
-      }
-    }
-    ss[m] = s;
-  }
-  wave_reduce_transpose<MB>(ss, lane);
-  if ((lane & (64 / MB - 1)) == 0) red[wave * MB + lane / (64 / MB)] = ss[0];
-  lds_barrier();
-  float rs[MB];
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    float total = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) total += red[w * MB + m];
-    rs[m] = rsqrtf(total / static_cast<float>(H) + eps);
-  }
-#pragma unroll
-  for (int j = 0; j < kNormChunks; ++j) {
-    const int c = tid + 256 * j;
-    if (c < per_row) {
-#pragma unroll
-      for (int m = 0; m < MB; ++m) {
-        Vec8<T>* p = reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8);
-        const Vec8<T> h = *p;
-        float out[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = Elt<T>::r(Elt<T>::r(h.get(e) * rs[m]) * in.w[j].get(e));
-        *p = Vec8<T>::from_floats(out);
-      }
-    }
-  }
-  lds_barrier();
-}
 
 // ---------------------------------------------------------------------------
 // Embedding gather (batched_decoder_step.py:289-291) and the step's RoPE table
@@ -360,7 +175,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   // the workgroup leaves together, after the barriers.
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
   NormIn<T, MB> nin;
-  norm_load<T, MB>(nin, static_cast<const T*>(a.hidden), static_cast<const T*>(a.norm_w), b0, a.B, H);
+  norm_load<T, MB>(nin, static_cast<const T*>(a.hidden), static_cast<const T*>(a.norm_w), b0, a.B, H, tid);
   // Unconditional (a wave past its range loads a valid pair it never uses):
   // with no branch around them the waits below count exactly these 14 loads.
   Vec8<T> w[kSegChunks][kRowsPerWave];
@@ -371,7 +186,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   QkvEpi epi{};
   if constexpr (KIND == kQkv) epi = qkv_epilogue_inputs<T>(a, min(u, a.units - 1), row0, row1, b0 + lane);
   __builtin_amdgcn_sched_barrier(0);
-  norm_to_lds<T, MB>(nin, b0, a.B, H, a.eps, xs, red + 3 * WAVES * kRowsPerWave * MB);
+  norm_to_lds<T, MB>(nin, b0, a.B, H, a.eps, xs, red + 3 * WAVES * kRowsPerWave * MB, tid);
   if (stop != 0) return;
   // argmax running state of lane m < MB (batch row b0+m), LM head only
   float best_v = 0.f;
@@ -530,12 +345,12 @@ __device__ __forceinline__ void resid_segment(const ResidArgs& a, T* xs, float* 
   const size_t hrow = (size_t)min(b0 + lane, a.B - 1) * a.N;
   const T h0 = Hd[hrow + 2 * uc], h1 = Hd[hrow + 2 * uc + 1];
   Vec8<T> xv[seg_vecs_per_thread<MB>()];
-  load_rows_block<T, MB>(xv, static_cast<const T*>(a.x), a.K, b0, a.B, k0, len);
+  load_rows_block<T, MB>(xv, static_cast<const T*>(a.x), a.K, b0, a.B, k0, len, tid);
   Vec8<T> w[kSegChunks][kRowsPerWave];
   const T* wr[kRowsPerWave] = {W + (size_t)(2 * uc) * a.K, W + (size_t)(2 * uc + 1) * a.K};
   load_rows<T, kRowsPerWave, FULL>(w, wr, k0, len, lane);
   __builtin_amdgcn_sched_barrier(0);
-  store_rows_block<T, MB>(xv, b0, a.B, len, xs, kSeg);
+  store_rows_block<T, MB>(xv, b0, a.B, len, xs, kSeg, tid);
   if (stop != 0 || u >= units) return;
   float acc[kRowsPerWave][MB];
 #pragma unroll
@@ -792,10 +607,13 @@ void plan_grids(LaunchPlan& p, const Dims& d, int cus) {
   }
 }
 
-int step_op_count(const KernelEnv& env) { return 2 + kOpsPerLayer * env.dims.layers; }
-int gateup_op_index(int layer) { return 1 + kOpsPerLayer * layer + kGateUpOp; }
+int step_op_count(const KernelEnv& env) { return env.plan.fused ? 2 : 2 + kOpsPerLayer * env.dims.layers; }
+int timed_op_index(const KernelEnv& env, int layer) {
+  return env.plan.fused ? 1 : 1 + kOpsPerLayer * layer + kGateUpOp;
+}
 
 hipError_t launch_step_ops(const KernelEnv& env, const StepPtrs& step, hipStream_t stream, int begin, int end) {
+  if (env.plan.fused) return launch_fused_ops(env, step, stream, begin, end);
   const bool bf16 = env.dims.dtype_bytes == 2;
   if (env.plan.mb == 4)
     return bf16 ? decoder_step_t<bf16_t, 4>(env, step, stream, begin, end)

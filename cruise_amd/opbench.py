@@ -89,7 +89,9 @@ def main() -> int:
         raise SystemExit(f"--context must be in [1, {capacity}]")
     cfg = EngineConfig(
         model=ModelSpec(),
-        engine=EngineSpec(batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=capacity),
+        engine=EngineSpec(
+            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=capacity, fused_step=False
+        ),
         weights=WeightSpec("synthetic", 1, 0.02),
         tuning=json.loads(args.tuning) if args.tuning else {},
     )
