@@ -90,7 +90,7 @@ __device__ __forceinline__ void load_tile(Vec8<T> (&v)[AttnShape<D>::kLoads], co
 }
 
 __device__ __forceinline__ float attn_block_max(float v, float* red, int tid) {
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index(tid);
   v = wave_max(v);
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -102,7 +102,7 @@ __device__ __forceinline__ float attn_block_max(float v, float* red, int tid) {
 }
 
 __device__ __forceinline__ float attn_block_sum(float v, float* red, int tid) {
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index(tid);
   v = wave_sum(v);
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -162,36 +162,52 @@ __device__ __forceinline__ void load_part(Vec8<T> (&v)[N], const T* cache, const
 }
 
 // Scores of loads [i0, i0 + N) of tile t into sc; returns the running max.
+// The L lanes of a row group sum their partial products through LDS (dots:
+// this wave's [kRg][N][L] floats) instead of a shuffle tree, which would hold
+// every partial in registers: lane c < N adds the L partials of its load in
+// the pairing order of group_reduce_transpose<L> (lanes l and l+L/2 first,
+// then l+L/4, ...), so the score is bit-identical to attn_body's.
 template <typename T, int D, int N>
 __device__ __forceinline__ float lean_scores(const Vec8<T> (&kv)[N], const int (&off)[N], const Vec8<T>& qv, int i0,
                                              int t, int w, int r, int c, int neff, bool uniform, float* sc,
-                                             float smax) {
+                                             float* dots, float smax) {
   constexpr int L = AttnShape<D>::kLpr;
-  float pd[N];
+  float* mine = dots + r * N * L;
 #pragma unroll
-  for (int k = 0; k < N; ++k) pd[k] = off[k] >= 0 ? dot8(kv[k], qv, 0.f) : 0.f;
-  group_reduce_partial<N, L>(pd, c);
-  if (c % (L / N) == 0) {
-    const int j = tile_pos<D>(t, w, i0 + c / (L / N), r);
-    float s = pd[0];
-    if constexpr (sizeof(T) == 2) s = round_bf16(s);  // ExactQk output is bf16
-    s = round_bf16(s / sqrtf(static_cast<float>(D)));
-    if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
+  for (int k = 0; k < N; ++k) mine[k * L + c] = off[k] >= 0 ? dot8(kv[k], qv, 0.f) : 0.f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  if (c < N) {
+    float v[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) v[l] = mine[c * L + l];
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1)
+#pragma unroll
+      for (int l = 0; l < m; ++l) v[l] = v[l] + v[l + m];
+    const int j = tile_pos<D>(t, w, i0 + c, r);
+    float sv = v[0];
+    if constexpr (sizeof(T) == 2) sv = round_bf16(sv);  // ExactQk output is bf16
+    sv = round_bf16(sv / sqrtf(static_cast<float>(D)));
+    if (uniform) sv = -3.38953139e38f;  // every position masked to bf16 min
     if (j < neff) {
-      sc[j] = s;
-      smax = fmaxf(smax, s);
+      sc[j] = sv;
+      smax = fmaxf(smax, sv);
     }
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();  // the next half rewrites this wave's region
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
   return smax;
 }
 
 // The attention of one (batch row, query head) inside the persistent step
 // kernel, with attn_body's arithmetic, its work layout and its reduction
 // trees (so the results are bit-identical), in half the registers: each
-// tile's loads go out as two halves of kLoads/2 rows per lane.  With one tile
-// (contexts up to 256) both key halves are requested together and each value
-// half as soon as its key half has been scored, so the keys and the values
-// still take one round trip each.  q and the caches are read with ordinary
+// tile's loads go out as two halves of kLoads/2 rows per lane, the key
+// halves together and the value halves together after the softmax, so the
+// keys and the values take one round trip each per tile.  q and the caches are read with ordinary
 // loads at offsets carrying z (zero, read after the dependency wait): every
 // line they touch was last written before this launch or by a coherent store
 // of the qkv phase that signalled before the wait, and none was cached by
@@ -210,7 +226,7 @@ __device__ __forceinline__ void attn_body_lean(const AttnArgs& a, int block, uns
   const int grp = block % groups, hi = block / groups;
   const int b = grp / a.kv_heads, g = grp - b * a.kv_heads;
   const int h = g * G + hi;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = wave_index(tid);
   const int r = lane / L, c = lane % L;
   const int n = a.len[b];
   const bool uniform = n <= 0;
@@ -225,6 +241,9 @@ __device__ __forceinline__ void attn_body_lean(const AttnArgs& a, int block, uns
   const Vec8<T> qv = Vec8<T>::load_cached(static_cast<const T*>(a.q) + q_elem + z);
   lds_barrier();
 
+  // partial products of the scores: this wave's [kRg][NH][L] floats of the
+  // P.V partial region, which is free until the end
+  float* dots = part + w * S::kRg * NH * L;
   int off0[NH], off1[NH];
   Vec8<T> x0[NH], x1[NH];
   float smax = -INFINITY;
@@ -233,10 +252,8 @@ __device__ __forceinline__ void attn_body_lean(const AttnArgs& a, int block, uns
     tile_offsets_part<D, NH>(off1, NH, tabs, t, w, r, c, neff, a, g);
     load_part<T, NH>(x0, KC, off0, c);
     load_part<T, NH>(x1, KC, off1, c);
-    smax = lean_scores<T, D, NH>(x0, off0, qv, 0, t, w, r, c, neff, uniform, sc, smax);
-    if (ntiles == 1) load_part<T, NH>(x0, VC, off0, c);
-    smax = lean_scores<T, D, NH>(x1, off1, qv, NH, t, w, r, c, neff, uniform, sc, smax);
-    if (ntiles == 1) load_part<T, NH>(x1, VC, off1, c);
+    smax = lean_scores<T, D, NH>(x0, off0, qv, 0, t, w, r, c, neff, uniform, sc, dots, smax);
+    smax = lean_scores<T, D, NH>(x1, off1, qv, NH, t, w, r, c, neff, uniform, sc, dots, smax);
   }
   const float mx = attn_block_max(smax, red, tid);
   float esum = 0.f;
@@ -249,7 +266,7 @@ __device__ __forceinline__ void attn_body_lean(const AttnArgs& a, int block, uns
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   for (int t = 0; t < ntiles; ++t) {
-    if (ntiles > 1) {
+    {
       tile_offsets_part<D, NH>(off0, 0, tabs, t, w, r, c, neff, a, g);
       tile_offsets_part<D, NH>(off1, NH, tabs, t, w, r, c, neff, a, g);
       load_part<T, NH>(x0, VC, off0, c);
@@ -303,7 +320,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
   const int grp = block % groups, hi = block / groups;
   const int b = grp / a.kv_heads, g = grp - b * a.kv_heads;
   const int h = g * G + hi;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = wave_index(tid);
   const int r = lane / L, c = lane % L;
   const int n = a.len[b];
   const bool uniform = n <= 0;

@@ -231,9 +231,27 @@ __device__ __forceinline__ Vec8<float> co_load_vec8<float>(const CoBuf& buf, uin
   return r;
 }
 
+// The same (wave-uniform) pointer, marked as global memory, so loads and
+// stores through it compile to global_* instead of flat_* instructions (a
+// flat access also counts against lgkmcnt, so every LDS wait would wait for
+// it too).  Needed where the compiler cannot see that a pointer came from a
+// kernel argument.  The global-address-space copy passes through an empty
+// asm so the compiler cannot fold the two casts back into the generic
+// pointer.
+template <typename T>
+__device__ __forceinline__ T* as_global(T* p) {
+  __attribute__((address_space(1))) T* g = (__attribute__((address_space(1))) T*)p;
+  asm volatile("" : "+s"(g));
+  return (T*)g;
+}
+
 // Wait until this wave's vector memory operations have completed (stores
 // acknowledged): vmcnt(0), expcnt and lgkmcnt left at their maxima.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+// The wave's index in its workgroup, as a scalar (the compiler cannot always
+// tell that threadIdx.x / 64 is the same for every lane of a wave).
+__device__ __forceinline__ int wave_index(int tid) { return __builtin_amdgcn_readfirstlane(tid >> 6); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -249,7 +249,7 @@ bool make_plan(Engine& e, const Json& cfg) {
   if (eng != nullptr && eng->bool_or("fused_step", false) && fused_step_eligible(d)) {
     p.fused_grid = fused_grid(d, e.cus);
     if (const Json* t = cfg.get("tuning")) p.fused_grid = static_cast<int>(t->number_or("fused_grid", p.fused_grid));
-    p.fused = p.fused_grid >= 1 && p.fused_grid <= fused_grid(d, e.cus) ? 1 : 0;
+    p.fused = fused_grid_valid(d, p.fused_grid, e.cus) ? 1 : 0;
     if (p.fused) p.lm_wg = p.fused_grid;
   }
   p.o_grid = (d.hidden / 2 + p.waves - 1) / p.waves;

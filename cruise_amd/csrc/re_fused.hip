@@ -61,7 +61,8 @@ constexpr int kCtrStride = 32;   // ints between counters: one 128-byte line eac
 constexpr int kRedFloats = 128;  // wave totals [0, 32), norm scratch [96, 112), LM combine [0, 48)
 constexpr int kNormRedOff = 3 * kFWaves * kRowsPerWave * kFMB;
 
-enum FusedPhase : int { kPhQkv = 0, kPhAttn = 1, kPhO = 2, kPhGu = 3, kPhDown = 4, kPhases = 5 };
+enum FusedPhase : int { kPhQkv = 0, kPhAttn = 1, kPhO = 2, kPhGu = 3, kPhDown = 4, kPhRed = 5, kPhases = 6 };
+constexpr int kRedWgs = 56;  // workgroups that sum DOWN's partials (one value per thread each)
 __host__ __device__ constexpr int ctr_index(int layer, int phase) { return 1 + layer * kPhases + phase; }
 
 struct FusedLayerW {
@@ -83,11 +84,12 @@ struct FusedArgs {
   const FT* hidden;       // [B, H] the step's embedding rows (layer 0's input)
   // Per-layer activations, each written once per launch: layer l's block at
   // act + l * act_stride holds q [B, heads*d], attn [B, heads*d], mlp [B, I],
-  // h_mid [B, H] (residual after attention) and h_out [B, H] (the layer's
-  // output, layer l+1's input).
+  // h_mid [B, H] (residual after attention), h_out [B, H] (the layer's
+  // output, layer l+1's input) and DOWN's fp32 segment partials
+  // [row group][segment][B][8 rows] (a row group's in whole 128-byte lines).
   uint8_t* act;
   long long act_stride;
-  int off_q, off_attn, off_mlp, off_hmid, off_hout;
+  int off_q, off_attn, off_mlp, off_hmid, off_hout, off_part;
   const float* rope;      // [B, d/2, 2]
   const int32_t* slot;
   const int32_t* active;
@@ -116,8 +118,10 @@ struct FusedArgs {
 struct Sched {
   int G;
   int qkv_pairs, qkv_items, attn_items, o_items, dn_items;
+  int dn_groups, dn_segs;  // DOWN: row groups (4 row pairs) x K-segments
   int base_o, base_dn;
-  int t_qkv, t_attn, t_o, t_gu, t_dn;  // producer workgroups of each phase
+  int gu_items;
+  int t_qkv, t_attn, t_o, t_gu, t_dn, t_red;  // producer workgroups of each phase
 };
 
 __device__ __forceinline__ Sched make_sched(const FusedArgs& a) {
@@ -127,14 +131,18 @@ __device__ __forceinline__ Sched make_sched(const FusedArgs& a) {
   s.qkv_items = (s.qkv_pairs + kFWaves - 1) / kFWaves;
   s.attn_items = a.B * a.heads;
   s.o_items = (a.H / 2 + kFWaves - 1) / kFWaves;
-  s.dn_items = s.o_items;
+  s.dn_groups = (a.H / 2 + kFWaves - 1) / kFWaves;
+  s.dn_segs = (a.I + kSeg - 1) / kSeg;
+  s.dn_items = s.dn_groups * s.dn_segs;
   s.base_o = s.attn_items % s.G;
   s.base_dn = s.qkv_items % s.G;
   s.t_qkv = min(s.G, s.qkv_items);
   s.t_attn = min(s.G, s.attn_items);
   s.t_o = min(s.G, s.o_items);
-  s.t_gu = min(s.G, a.I);
-  s.t_dn = min(s.G, s.dn_items);
+  s.gu_items = (a.I + kFWaves - 1) / kFWaves;
+  s.t_gu = min(s.G, s.gu_items);
+  s.t_red = min(s.G, kRedWgs);
+  s.t_dn = min(s.G, s.dn_items);  // workgroups with DOWN items (a static first one each)
   return s;
 }
 
@@ -149,11 +157,63 @@ __device__ __forceinline__ V opaque_v(V x) {
   asm volatile("" : "+v"(x));
   return x;
 }
-struct FusedArgs;
-__device__ __forceinline__ const FusedArgs& fargs() {
-  const void* p = (const void*)__builtin_amdgcn_kernarg_segment_ptr();
+// The pointers of the arguments are marked global again (the opaque copy
+// hides that they came from the kernel arguments).
+__device__ __forceinline__ FusedArgs fargs() {
+  typedef const __attribute__((address_space(4))) FusedArgs* ConstArgs;  // scalar loads
+  ConstArgs p = (ConstArgs)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(p));
-  return *static_cast<const FusedArgs*>(p);
+  // word by word through the constant address space (scalar loads); unused
+  // words are dropped by the compiler
+  static_assert(sizeof(FusedArgs) % 4 == 0, "argument block is whole words");
+  uint32_t words[sizeof(FusedArgs) / 4];
+  const __attribute__((address_space(4))) uint32_t* src = (const __attribute__((address_space(4))) uint32_t*)p;
+#pragma unroll
+  for (size_t i = 0; i < sizeof(FusedArgs) / 4; ++i) words[i] = src[i];
+  FusedArgs a;
+  __builtin_memcpy(&a, words, sizeof(FusedArgs));
+  a.done = as_global(a.done);
+  a.final_norm = as_global(a.final_norm);
+  a.lm_w = as_global(a.lm_w);
+  a.hidden = as_global(a.hidden);
+  a.act = as_global(a.act);
+  a.rope = as_global(a.rope);
+  a.slot = as_global(a.slot);
+  a.active = as_global(a.active);
+  a.len = as_global(a.len);
+  a.table = as_global(a.table);
+  a.key_cache = as_global(a.key_cache);
+  a.value_cache = as_global(a.value_cache);
+  a.logits = as_global(a.logits);
+  a.am_val = as_global(a.am_val);
+  a.am_idx = as_global(a.am_idx);
+  a.am_bad = as_global(a.am_bad);
+  a.sync = as_global(a.sync);
+  a.trace = as_global(a.trace);
+  return a;
+}
+
+__device__ __forceinline__ FusedLayerW layer_w(const FusedArgs& a, int l) {
+  typedef const __attribute__((address_space(4))) FusedLayerW* ConstTable;  // scalar loads (read-only table)
+  const ConstTable t = (ConstTable)a.lw + l;
+  FusedLayerW w;
+  w.in_norm = t->in_norm;
+  w.post_norm = t->post_norm;
+  w.qkv_w = t->qkv_w;
+  w.qkv_b = t->qkv_b;
+  w.o_w = t->o_w;
+  w.gate_w = t->gate_w;
+  w.up_w = t->up_w;
+  w.down_w = t->down_w;
+  w.in_norm = as_global(w.in_norm);
+  w.post_norm = as_global(w.post_norm);
+  w.qkv_w = as_global(w.qkv_w);
+  w.qkv_b = as_global(w.qkv_b);
+  w.o_w = as_global(w.o_w);
+  w.gate_w = as_global(w.gate_w);
+  w.up_w = as_global(w.up_w);
+  w.down_w = as_global(w.down_w);
+  return w;
 }
 __device__ __forceinline__ int phase_tid() { return opaque_v(static_cast<int>(threadIdx.x)); }
 
@@ -162,6 +222,22 @@ __device__ __forceinline__ int phase_tid() { return opaque_v(static_cast<int>(th
 // inputs are ready (the wait returned) and when it ends.
 enum TraceMark : int { kTrStart = 0, kTrReady = 1, kTrEnd = 2 };
 __device__ __forceinline__ void trace_mark(const FusedArgs& a, int slot, int mark);
+
+// Progress-based wave priority for the streaming phases.  The SIMD arbiter
+// favours older waves, so with equal static shares the youngest workgroups
+// would finish last while the older ones already idle, and the phase would
+// end with a fraction of the chip streaming.  A wave that has done `done` of
+// its `total` units drops from priority 3 towards 0, which lets the waves
+// that are behind catch up.
+__device__ __forceinline__ void progress_prio(int done, int total) {
+  const int p = total > 0 ? 3 - min(3, (4 * done) / total) : 0;
+  switch (p) {
+    case 3: __builtin_amdgcn_s_setprio(3); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    default: __builtin_amdgcn_s_setprio(0); break;
+  }
+}
 
 // First item of a phase whose item i runs on workgroup (base + i) mod G.
 __device__ __forceinline__ int first_item(int base, int G) { return ((int)blockIdx.x - base + G) % G; }
@@ -231,10 +307,37 @@ __device__ __forceinline__ CoBuf cobuf(const void* p, long long bytes) {
 // after that write (lines cached before the launch were invalidated at its
 // start).  Buffers are never reused within a launch for the same reason.
 __device__ __forceinline__ FT* act_buf(const FusedArgs& a, int l, int off) {
-  return reinterpret_cast<FT*>(a.act + (size_t)l * a.act_stride + off);
+  return as_global(reinterpret_cast<FT*>(a.act + (size_t)l * a.act_stride + off));
 }
 __device__ __forceinline__ const FT* layer_input(const FusedArgs& a, int l) {
   return l == 0 ? a.hidden : act_buf(a, l - 1, a.off_hout);
+}
+
+// RMSNorm prologue of QKV, GATEUP and the LM head: the rows come straight
+// into LDS (global->LDS loads, no registers), the norm weight into
+// registers, then the in-place norm (norm_to_lds's arithmetic).  rows must
+// already carry the ordering zero.
+__device__ __forceinline__ void norm_prologue(const FusedArgs& a, const FT* rows, const FT* norm_w, const Lds& s,
+                                              int tid) {
+  Vec8<FT> wn[kNormChunks];
+  const int per_row = a.H / 8;
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) wn[j] = Vec8<FT>::load_cached(norm_w + min(tid + 256 * j, per_row - 1) * 8);
+  lds_barrier();  // every earlier reader of xs is done
+  dma_rows<kFMB>(s.xs, a.H, rows, a.H, a.B, 0, a.H, tid);
+  wait_vmem();
+  lds_barrier();
+  norm_in_lds<kFMB>(s.xs, wn, a.H, a.eps, s.red + kNormRedOff, tid);
+}
+
+// Activation rows of a projection into xs [MB][kSeg] (columns [k0, k0+len)
+// of X), after every earlier reader of xs is done.
+__device__ __forceinline__ void stage_rows(const FusedArgs& a, const FT* X, int ldg, int k0, int len, const Lds& s,
+                                           int tid) {
+  lds_barrier();
+  dma_rows<kFMB>(s.xs, kSeg, X, ldg, a.B, k0, len, tid);
+  wait_vmem();
+  lds_barrier();
 }
 
 // ---------------------------------------------------------------------------
@@ -243,43 +346,50 @@ __device__ __forceinline__ const FT* layer_input(const FusedArgs& a, int l) {
 // arithmetic (batched_decoder_step.py:224-229, 305-324, 250-264).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool ph_qkv(int l, const Lds& s) {
-  const FusedArgs& a = fargs();
+  const FusedArgs a = fargs();
   const Sched sc = make_sched(a);
   int i = first_item(0, sc.G);
   if (i >= sc.qkv_items) return true;
   trace_mark(a, l * kPhases + kPhQkv, kTrStart);
-  const FusedLayerW w = a.lw[l];
+  const FusedLayerW w = layer_w(a, l);
   FT* kc = a.key_cache + (size_t)l * a.layer_elems;
   FT* vc = a.value_cache + (size_t)l * a.layer_elems;
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int tid = phase_tid(), lane = tid & 63, wave = wave_index(tid);
   const int half = a.head_dim >> 1;
   const int nq = a.heads, nkv = a.kv_heads;
   float* wred = s.red + wave * (kRowsPerWave * kFMB);
   const CoBuf qb = cobuf(act_buf(a, l, a.off_q), (long long)a.B * nq * a.head_dim * 2);
   const long long cache_bytes = a.layer_elems * 2;
   const CoBuf kb = cobuf(kc, cache_bytes), vb = cobuf(vc, cache_bytes);
-  bool first = true;
-  for (; i < sc.qkv_items; i += sc.G) {
-    const int u = i * kFWaves + wave;
+  // The item's q/k/v rows j and j + d/2 of head hg, their biases and the
+  // rows' RoPE cos/sin, requested together (before the wait on the first).
+  Vec8<FT> wv[kSegChunks][kRowsPerWave];
+  int u = 0, hg = 0, j = 0;
+  float bias0 = 0.f, bias1 = 0.f, cs = 1.f, sn = 0.f;
+  auto issue = [&](int item) {
+    u = item * kFWaves + wave;
     const int uc = min(u, sc.qkv_pairs - 1);
-    const int hg = uc / half, j = uc - hg * half;
+    hg = uc / half;
+    j = uc - hg * half;
     const int row0 = hg * a.head_dim + j, row1 = row0 + half;
     const FT* wr[kRowsPerWave] = {w.qkv_w + (size_t)row0 * a.H, w.qkv_w + (size_t)row1 * a.H};
-    Vec8<FT> wv[kSegChunks][kRowsPerWave];
     load_rows<FT, kRowsPerWave, true>(wv, wr, 0, a.H, lane);
-    const float bias0 = bf16_to_f(w.qkv_b[row0]), bias1 = bf16_to_f(w.qkv_b[row1]);
+    bias0 = bf16_to_f(w.qkv_b[row0]);
+    bias1 = bf16_to_f(w.qkv_b[row1]);
     const int bc = min(lane, a.B - 1);
-    const float cs = a.rope[((size_t)bc * half + j) * 2], sn = a.rope[((size_t)bc * half + j) * 2 + 1];
+    cs = a.rope[((size_t)bc * half + j) * 2];
+    sn = a.rope[((size_t)bc * half + j) * 2 + 1];
+  };
+  issue(i);
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    const int z = wait_for(a, l == 0 ? -1 : ctr_index(l - 1, kPhRed), sc.t_red, s);
+    if (z < 0) return false;
+    trace_mark(a, l * kPhases + kPhQkv, kTrReady);
+    norm_prologue(a, layer_input(a, l) + z, w.in_norm, s, tid);
+  }
+  for (;;) {
     __builtin_amdgcn_sched_barrier(0);
-    if (first) {
-      const int z = wait_for(a, l == 0 ? -1 : ctr_index(l - 1, kPhDown), sc.t_dn, s);
-      if (z < 0) return false;
-      trace_mark(a, l * kPhases + kPhQkv, kTrReady);
-      NormIn<FT, kFMB> nin;
-      norm_load<FT, kFMB>(nin, layer_input(a, l) + z, w.in_norm, 0, a.B, a.H, tid);
-      norm_to_lds<FT, kFMB>(nin, 0, a.B, a.H, a.eps, s.xs, s.red + kNormRedOff, tid);
-      first = false;
-    }
     float acc[kRowsPerWave][kFMB];
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r)
@@ -312,6 +422,9 @@ __device__ __forceinline__ bool ph_qkv(int l, const Lds& s) {
         }
       }
     }
+    i += sc.G;
+    if (i >= sc.qkv_items) break;
+    issue(i);
   }
   signal(a, ctr_index(l, kPhQkv));
   trace_mark(a, l * kPhases + kPhQkv, kTrEnd);
@@ -322,7 +435,7 @@ __device__ __forceinline__ bool ph_qkv(int l, const Lds& s) {
 // ATTN: one (batch row, query head) per item, the paged decode attention.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool ph_attn(int l, const Lds& s) {
-  const FusedArgs& a = fargs();
+  const FusedArgs a = fargs();
   const Sched sc = make_sched(a);
   int i = first_item(0, sc.G);
   if (i >= sc.attn_items) return true;
@@ -364,13 +477,13 @@ __device__ __forceinline__ bool ph_attn(int l, const Lds& s) {
 // (batched_decoder_step.py:380-386).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool ph_oproj(int l, const Lds& s) {
-  const FusedArgs& a = fargs();
+  const FusedArgs a = fargs();
   const Sched sc = make_sched(a);
   int i = first_item(sc.base_o, sc.G);
   if (i >= sc.o_items) return true;
   trace_mark(a, l * kPhases + kPhO, kTrStart);
-  const FusedLayerW w = a.lw[l];
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const FusedLayerW w = layer_w(a, l);
+  const int tid = phase_tid(), lane = tid & 63, wave = wave_index(tid);
   const int units = a.H / 2;
   const int K = a.heads * a.head_dim;  // == kSeg
   float* wred = s.red + wave * (kRowsPerWave * kFMB);
@@ -393,12 +506,9 @@ __device__ __forceinline__ bool ph_oproj(int l, const Lds& s) {
       z = static_cast<uint32_t>(zz);
       first = false;
     }
-    Vec8<FT> xv[seg_vecs_per_thread<kFMB>()];
-    load_rows_block<FT, kFMB>(xv, attn + z, K, 0, a.B, 0, K, tid);
     const size_t hidx = (size_t)min(lane, a.B - 1) * a.H + 2 * uc;
     const uint32_t hp = *reinterpret_cast<const uint32_t*>(hin + hidx + z);
-    lds_barrier();  // the previous item's products have read xs
-    store_rows_block<FT, kFMB>(xv, 0, a.B, K, s.xs, kSeg, tid);
+    stage_rows(a, attn + z, K, 0, K, s, tid);
     float acc[kRowsPerWave][kFMB];
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r)
@@ -421,36 +531,37 @@ __device__ __forceinline__ bool ph_oproj(int l, const Lds& s) {
 // ---------------------------------------------------------------------------
 // GATEUP: RMSNorm prologue, gate row u and up row u per wave, SiLU(gate)*up
 // -- k_proj<kGateUp>'s arithmetic (batched_decoder_step.py:388-398).  Each
-// workgroup owns a contiguous range of units.
+// workgroup owns a contiguous range of units, its waves taking every fourth.
+// A unit's output is stored after the next unit's rows are requested, so the
+// store's acknowledgement never delays those rows.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool ph_gateup(int l, const Lds& s) {
-  const FusedArgs& a = fargs();
+  const FusedArgs a = fargs();
   const Sched sc = make_sched(a);
   const int U = a.I;
   const int u0 = (int)((long long)blockIdx.x * U / sc.G), u1 = (int)((long long)(blockIdx.x + 1) * U / sc.G);
   if (u0 >= u1) return true;
   trace_mark(a, l * kPhases + kPhGu, kTrStart);
-  const FusedLayerW w = a.lw[l];
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const FusedLayerW w = layer_w(a, l);
+  const int tid = phase_tid(), lane = tid & 63, wave = wave_index(tid);
   float* wred = s.red + wave * (kRowsPerWave * kFMB);
   const CoBuf mb = cobuf(act_buf(a, l, a.off_mlp), (long long)a.B * U * 2);
-  int u = u0 + wave;
   Vec8<FT> wv[kSegChunks][kRowsPerWave];
-  {
+  auto issue = [&](int u) {
     const int uc = min(u, u1 - 1);
     const FT* wr[kRowsPerWave] = {w.gate_w + (size_t)uc * a.H, w.up_w + (size_t)uc * a.H};
     load_rows<FT, kRowsPerWave, true>(wv, wr, 0, a.H, lane);
-  }
+  };
+  int u = u0 + wave;
+  const int mine = (u1 - u0 - wave + kFWaves - 1) / kFWaves;  // this wave's units
+  issue(u);
   __builtin_amdgcn_sched_barrier(0);
   const int z = wait_for(a, ctr_index(l, kPhO), sc.t_o, s);
   if (z < 0) return false;
   trace_mark(a, l * kPhases + kPhGu, kTrReady);
-  {
-    NormIn<FT, kFMB> nin;
-    norm_load<FT, kFMB>(nin, act_buf(a, l, a.off_hmid) + z, w.post_norm, 0, a.B, a.H, tid);
-    norm_to_lds<FT, kFMB>(nin, 0, a.B, a.H, a.eps, s.xs, s.red + kNormRedOff, tid);
-  }
-  while (u < u1) {
+  norm_prologue(a, act_buf(a, l, a.off_hmid) + z, w.post_norm, s, tid);
+  for (int done = 0; u < u1; ++done) {
+    progress_prio(done, mine);
     __builtin_amdgcn_sched_barrier(0);
     float acc[kRowsPerWave][kFMB];
 #pragma unroll
@@ -459,101 +570,116 @@ __device__ __forceinline__ bool ph_gateup(int l, const Lds& s) {
       for (int m = 0; m < kFMB; ++m) acc[r][m] = 0.f;
     dot_rows<FT, kFMB, kRowsPerWave, true>(wv, s.xs, a.H, 0, a.H, lane, acc);
     wave_totals<kFMB, kRowsPerWave>(acc, lane, wred);
+    bf16_t out = 0;
     if (lane < a.B) {
       const float g = round_bf16(wred[0 * kFMB + lane]);
       const float up = round_bf16(wred[1 * kFMB + lane]);
       const float sg = round_bf16(g / (1.0f + expf(-g)));
-      mb.store2(static_cast<uint32_t>(((size_t)lane * U + u) * 2), f_to_bf16(round_bf16(sg * up)));
+      out = f_to_bf16(round_bf16(sg * up));
     }
+    const int cur = u;
     u += kFWaves;
-    if (u < u1) {
-      const FT* wr[kRowsPerWave] = {w.gate_w + (size_t)u * a.H, w.up_w + (size_t)u * a.H};
-      load_rows<FT, kRowsPerWave, true>(wv, wr, 0, a.H, lane);
-    }
+    if (u < u1) issue(u);
+    if (lane < a.B) mb.store2(static_cast<uint32_t>(((size_t)lane * U + cur) * 2), out);
   }
+  __builtin_amdgcn_s_setprio(0);
   signal(a, ctr_index(l, kPhGu));
   trace_mark(a, l * kPhases + kPhGu, kTrEnd);
   return true;
 }
 
-// ---------------------------------------------------------------------------
-// DOWN: rows 2p, 2p+1 of Wd per wave over every K-segment of the SwiGLU
-// output in order; the segment totals are summed in segment order, rounded,
-// and added to the residual -- k_resid + k_resid_reduce's arithmetic
-// (batched_decoder_step.py:399-403).
-// ---------------------------------------------------------------------------
-// One K-segment of a DOWN item.  The segment's weight rows are requested
-// first; the item's first segment then waits for GATEUP (so those rows are in
-// flight during the wait).
-template <bool FULL>
-__device__ __forceinline__ bool down_segment(const FusedArgs& a, const Sched& sc, int l,
-                                             const FT* const (&wr)[kRowsPerWave], const FT* mlp, int k0, int len,
-                                             int& z, const Lds& s, float* wred, int tid, float (&run)[kRowsPerWave]) {
-  const int lane = tid & 63;
-  Vec8<FT> wv[kSegChunks][kRowsPerWave];
-  load_rows<FT, kRowsPerWave, FULL>(wv, wr, k0, len, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  if (z < 0) {
-    z = wait_for(a, ctr_index(l, kPhGu), sc.t_gu, s);
-    if (z < 0) return false;
-    trace_mark(a, l * kPhases + kPhDown, kTrReady);
-  }
-  Vec8<FT> xv[seg_vecs_per_thread<kFMB>()];
-  load_rows_block<FT, kFMB>(xv, mlp + z, a.I, 0, a.B, k0, len, tid);
-  lds_barrier();  // the previous segment's products have read xs
-  store_rows_block<FT, kFMB>(xv, 0, a.B, len, s.xs, kSeg, tid);
-  float acc[kRowsPerWave][kFMB];
-#pragma unroll
-  for (int r = 0; r < kRowsPerWave; ++r)
-#pragma unroll
-    for (int m = 0; m < kFMB; ++m) acc[r][m] = 0.f;
-  dot_rows<FT, kFMB, kRowsPerWave, FULL>(wv, s.xs, kSeg, 0, len, lane, acc);
-  wave_totals<kFMB, kRowsPerWave>(acc, lane, wred);
-  if (lane < kFMB) {
-    run[0] += wred[0 * kFMB + lane];
-    run[1] += wred[1 * kFMB + lane];
-  }
-  return true;
-}
-
+// DOWN, split over every workgroup: an item is (K-segment, row group of 4
+// row pairs); each wave computes its pair's totals over the segment and
+// stores them as fp32 partials [segment][B][H].  Workgroup g takes items g,
+// g + G, ...; it signals once, after its last item.
 __device__ __forceinline__ bool ph_down(int l, const Lds& s) {
-  const FusedArgs& a = fargs();
+  const FusedArgs a = fargs();
   const Sched sc = make_sched(a);
-  int i = first_item(sc.base_dn, sc.G);
-  if (i >= sc.dn_items) return true;
+  int item = blockIdx.x;
+  if (item >= sc.dn_items) return true;
   trace_mark(a, l * kPhases + kPhDown, kTrStart);
-  const FusedLayerW w = a.lw[l];
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const FusedLayerW w = layer_w(a, l);
+  const int tid = phase_tid(), lane = tid & 63, wave = wave_index(tid);
   const int units = a.H / 2;
   const int K = a.I;
   float* wred = s.red + wave * (kRowsPerWave * kFMB);
-  const FT* hmid = act_buf(a, l, a.off_hmid);
   const FT* mlp = act_buf(a, l, a.off_mlp);
-  const CoBuf hout = cobuf(act_buf(a, l, a.off_hout), (long long)a.B * a.H * 2);
-  int z = -1;  // set by the first segment's wait
-  for (; i < sc.dn_items; i += sc.G) {
-    const int p = i * kFWaves + wave;
-    const int pc = min(p, units - 1);
+  const CoBuf pb = cobuf(act_buf(a, l, a.off_part), (long long)sc.dn_segs * a.B * a.H * sizeof(float));
+  const int mine = (sc.dn_items - item + sc.G - 1) / sc.G;  // this workgroup's items
+  Vec8<FT> wv[kSegChunks][kRowsPerWave];
+  int seg = 0, rg = 0, k0 = 0, len = 0;
+  auto issue = [&](int it) {
+    seg = it / sc.dn_groups;
+    rg = it - seg * sc.dn_groups;
+    k0 = seg * kSeg;
+    len = min(K - k0, kSeg);
+    const int pc = min(rg * kFWaves + wave, units - 1);
     const FT* wr[kRowsPerWave] = {w.down_w + (size_t)(2 * pc) * K, w.down_w + (size_t)(2 * pc + 1) * K};
-    const size_t hidx = (size_t)min(lane, a.B - 1) * a.H + 2 * pc;
-    float run[kRowsPerWave] = {0.f, 0.f};
-    uint32_t hp = 0;
-    int k0 = 0;
-    for (; k0 + kSeg <= K; k0 += kSeg) {
-      if (!down_segment<true>(a, sc, l, wr, mlp, k0, kSeg, z, s, wred, tid, run)) return false;
-      if (k0 == 0) hp = *reinterpret_cast<const uint32_t*>(hmid + hidx + z);  // the residual, after the wait
+    if (len == kSeg)
+      load_rows<FT, kRowsPerWave, true>(wv, wr, k0, len, lane);
+    else
+      load_rows<FT, kRowsPerWave, false>(wv, wr, k0, len, lane);
+  };
+  issue(item);
+  __builtin_amdgcn_sched_barrier(0);
+  const int z = wait_for(a, ctr_index(l, kPhGu), sc.t_gu, s);
+  if (z < 0) return false;
+  trace_mark(a, l * kPhases + kPhDown, kTrReady);
+  for (int done = 0;; ++done) {
+    progress_prio(done, mine);
+    stage_rows(a, mlp + z, K, k0, len, s, tid);
+    float acc[kRowsPerWave][kFMB];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+      for (int m = 0; m < kFMB; ++m) acc[r][m] = 0.f;
+    if (len == kSeg)
+      dot_rows<FT, kFMB, kRowsPerWave, true>(wv, s.xs, kSeg, 0, len, lane, acc);
+    else
+      dot_rows<FT, kFMB, kRowsPerWave, false>(wv, s.xs, kSeg, 0, len, lane, acc);
+    wave_totals<kFMB, kRowsPerWave>(acc, lane, wred);
+    const int p = rg * kFWaves + wave;
+    const bool have = p < units && lane < a.B;
+    const uint32_t o = static_cast<uint32_t>((((size_t)seg * a.B + min(lane, a.B - 1)) * a.H + 2 * p) * 4);
+    const float t0 = wred[0 * kFMB + lane], t1 = wred[1 * kFMB + lane];
+    item += sc.G;
+    if (item < sc.dn_items) issue(item);
+    if (have) {
+      pb.store4(o, __float_as_uint(t0));
+      pb.store4(o + 4, __float_as_uint(t1));
     }
-    if (k0 < K) {
-      if (!down_segment<false>(a, sc, l, wr, mlp, k0, K - k0, z, s, wred, tid, run)) return false;
-      if (k0 == 0) hp = *reinterpret_cast<const uint32_t*>(hmid + hidx + z);
-    }
-    if (p < units && lane < a.B) {
-      const float h0 = __uint_as_float(hp << 16), h1 = __uint_as_float(hp & 0xffff0000u);
-      hout.store4(static_cast<uint32_t>(hidx * 2), f2_to_bf16x2(h0 + round_bf16(run[0]), h1 + round_bf16(run[1])));
-    }
+    if (item >= sc.dn_items) break;
   }
+  __builtin_amdgcn_s_setprio(0);
   signal(a, ctr_index(l, kPhDown));
   trace_mark(a, l * kPhases + kPhDown, kTrEnd);
+  return true;
+}
+
+// REDUCE: the partials of every segment summed in segment order, rounded,
+// and added to the residual -- k_resid_reduce's arithmetic
+// (batched_decoder_step.py:399-403) -- one value per thread on the first
+// kRedWgs workgroups.
+__device__ __forceinline__ bool ph_reduce(int l, const Lds& s) {
+  const FusedArgs a = fargs();
+  const Sched sc = make_sched(a);
+  if ((int)blockIdx.x >= sc.t_red) return true;
+  trace_mark(a, l * kPhases + kPhRed, kTrStart);
+  const int tid = phase_tid();
+  const int z = wait_for(a, ctr_index(l, kPhDown), sc.t_dn, s);
+  if (z < 0) return false;
+  trace_mark(a, l * kPhases + kPhRed, kTrReady);
+  const float* part = reinterpret_cast<const float*>(act_buf(a, l, a.off_part)) + z;
+  const FT* hmid = act_buf(a, l, a.off_hmid) + z;
+  const CoBuf hout = cobuf(act_buf(a, l, a.off_hout), (long long)a.B * a.H * 2);
+  const int n = a.B * a.H;
+  for (int e = (int)blockIdx.x * kFThreads + tid; e < n; e += sc.t_red * kFThreads) {
+    float run = 0.f;
+    for (int sg = 0; sg < sc.dn_segs; ++sg) run += part[(size_t)sg * n + e];
+    hout.store2(static_cast<uint32_t>(e * 2), f_to_bf16(bf16_to_f(hmid[e]) + round_bf16(run)));
+  }
+  signal(a, ctr_index(l, kPhRed));
+  trace_mark(a, l * kPhases + kPhRed, kTrEnd);
   return true;
 }
 
@@ -563,34 +689,33 @@ __device__ __forceinline__ bool ph_down(int l, const Lds& s) {
 // arithmetic (batched_decoder_step.py:405-408, CTRL:99-119).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void ph_lmhead(const Lds& s) {
-  const FusedArgs& a = fargs();
+  const FusedArgs a = fargs();
   const Sched sc = make_sched(a);
-  const int P = a.V / 2;
+  const int P = a.V / 2;  // vocabulary row pairs
   const int u0 = (int)((long long)blockIdx.x * P / sc.G), u1 = (int)((long long)(blockIdx.x + 1) * P / sc.G);
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int tid = phase_tid(), lane = tid & 63, wave = wave_index(tid);
   float* wred = s.red + wave * (kRowsPerWave * kFMB);
   float best_v = 0.f;
   int best_i = -1;
   int bad = 0;
   trace_mark(a, a.L * kPhases, kTrStart);
   if (u0 < u1) {
-    int u = u0 + wave;
     Vec8<FT> wv[kSegChunks][kRowsPerWave];
-    {
+    auto issue = [&](int u) {
       const int uc = min(u, u1 - 1);
       const FT* wr[kRowsPerWave] = {a.lm_w + (size_t)(2 * uc) * a.H, a.lm_w + (size_t)(2 * uc + 1) * a.H};
       load_rows<FT, kRowsPerWave, true>(wv, wr, 0, a.H, lane);
-    }
+    };
+    int u = u0 + wave;
+    const int mine = (u1 - u0 - wave + kFWaves - 1) / kFWaves;
+    issue(u);
     __builtin_amdgcn_sched_barrier(0);
-    const int z = wait_for(a, ctr_index(a.L - 1, kPhDown), sc.t_dn, s);
+    const int z = wait_for(a, ctr_index(a.L - 1, kPhRed), sc.t_red, s);
     if (z < 0) return;
     trace_mark(a, a.L * kPhases, kTrReady);
-    {
-      NormIn<FT, kFMB> nin;
-      norm_load<FT, kFMB>(nin, layer_input(a, a.L) + z, a.final_norm, 0, a.B, a.H, tid);
-      norm_to_lds<FT, kFMB>(nin, 0, a.B, a.H, a.eps, s.xs, s.red + kNormRedOff, tid);
-    }
-    while (u < u1) {
+    norm_prologue(a, layer_input(a, a.L) + z, a.final_norm, s, tid);
+    for (int done = 0; u < u1; ++done) {
+      progress_prio(done, mine);
       __builtin_amdgcn_sched_barrier(0);
       float acc[kRowsPerWave][kFMB];
 #pragma unroll
@@ -616,11 +741,9 @@ __device__ __forceinline__ void ph_lmhead(const Lds& s) {
         }
       }
       u += kFWaves;
-      if (u < u1) {
-        const FT* wr[kRowsPerWave] = {a.lm_w + (size_t)(2 * u) * a.H, a.lm_w + (size_t)(2 * u + 1) * a.H};
-        load_rows<FT, kRowsPerWave, true>(wv, wr, 0, a.H, lane);
-      }
+      if (u < u1) issue(u);
     }
+    __builtin_amdgcn_s_setprio(0);
   }
   // Combine the waves; ties go to the lowest index.  A workgroup without
   // vocabulary rows leaves index -1, which the merge ignores.
@@ -655,7 +778,7 @@ __device__ __forceinline__ void ph_lmhead(const Lds& s) {
   trace_mark(a, a.L * kPhases, kTrEnd);
 }
 
-__global__ void __launch_bounds__(kFThreads, 2) k_step_fused(FusedArgs args) {
+__global__ void __launch_bounds__(kFThreads, 4) k_step_fused(FusedArgs args) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   if (args.done != nullptr && __builtin_nontemporal_load(args.done) != 0) return;
   const size_t xs_bytes = (size_t)kFMB * kSeg * sizeof(FT);
@@ -665,11 +788,18 @@ __global__ void __launch_bounds__(kFThreads, 2) k_step_fused(FusedArgs args) {
   s.red = reinterpret_cast<float*>(smem_raw + xs_bytes);
   s.bcast = reinterpret_cast<int*>(s.red + kRedFloats);
   for (int l = 0; l < args.L; ++l) {
+    // The dependency chain runs at a raised wave priority, so the streaming
+    // waves sharing its SIMDs do not delay it.
+    __builtin_amdgcn_s_setprio(2);
     if (!ph_qkv(l, s)) return;
     if (!ph_attn(l, s)) return;
     if (!ph_oproj(l, s)) return;
+    __builtin_amdgcn_s_setprio(0);
     if (!ph_gateup(l, s)) return;
     if (!ph_down(l, s)) return;
+    __builtin_amdgcn_s_setprio(2);
+    if (!ph_reduce(l, s)) return;
+    __builtin_amdgcn_s_setprio(0);
   }
   ph_lmhead(s);
 }
@@ -733,23 +863,38 @@ FusedActLayout fused_act_layout(const Dims& d) {
   al.mlp = al.attn + up((size_t)d.batch * d.q_dim() * T);
   al.h_mid = al.mlp + up((size_t)d.batch * d.intermediate * T);
   al.h_out = al.h_mid + up((size_t)d.batch * d.hidden * T);
-  al.stride = al.h_out + up((size_t)d.batch * d.hidden * T);
+  al.part = al.h_out + up((size_t)d.batch * d.hidden * T);
+  const size_t segs = (d.intermediate + kSeg - 1) / kSeg;
+  al.stride = al.part + up(segs * d.batch * d.hidden * sizeof(float));
   return al;
 }
 size_t fused_act_bytes(const Dims& d) { return fused_act_layout(d).stride * d.layers; }
 size_t fused_layer_table_bytes(const Dims& d) { return (size_t)d.layers * sizeof(FusedLayerW); }
+// Phase counters, one 128-byte line each.
 int fused_sync_ints(const Dims& d) { return (1 + d.layers * kPhases) * kCtrStride; }
 size_t fused_trace_bytes(const Dims& d, int grid) {
   return (size_t)grid * (d.layers * kPhases + 1) * 3 * sizeof(unsigned long long);
 }
 
-int fused_grid(const Dims& d, int cus) {
+int fused_grid_capacity(const Dims& d, int cus) {
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_step_fused, kFThreads, fused_lds_bytes_impl(d)) !=
           hipSuccess ||
       per_cu < 1)
     return 0;
   return per_cu * cus;
+}
+
+// Default grid: two workgroups per CU.  The waves of a CU's later-dispatched
+// workgroups are served after the earlier ones', so with equal static shares
+// the third and fourth workgroup of a CU finish a streaming phase 20-50%
+// later than the first two; two per CU streamed the 28-layer Qwen2.5-7B step
+// in 4.76 ms against 5.24 ms at three and 5.78 ms at four.
+int fused_grid(const Dims& d, int cus) { return std::min(2 * cus, fused_grid_capacity(d, cus)); }
+
+// A grid the kernel can run with: every workgroup resident at once.
+bool fused_grid_valid(const Dims& d, int grid, int cus) {
+  return grid >= 1 && grid <= fused_grid_capacity(d, cus);
 }
 
 hipError_t write_fused_layer_table(const Dims& d, const uint8_t* weights, const LayerOffsets* lo, void* dst) {
@@ -806,6 +951,7 @@ hipError_t launch_fused_ops(const KernelEnv& env, const StepPtrs& st, hipStream_
     a.off_mlp = static_cast<int>(al.mlp);
     a.off_hmid = static_cast<int>(al.h_mid);
     a.off_hout = static_cast<int>(al.h_out);
+    a.off_part = static_cast<int>(al.part);
     a.rope = scr.rope;
     a.slot = st.slot;
     a.active = st.active;

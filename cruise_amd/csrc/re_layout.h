@@ -189,10 +189,11 @@ size_t fused_lds_bytes(const Dims& d);
 size_t fused_layer_table_bytes(const Dims& d);
 int fused_sync_ints(const Dims& d);
 int fused_grid(const Dims& d, int cus);
+bool fused_grid_valid(const Dims& d, int grid, int cus);
 size_t fused_trace_bytes(const Dims& d, int grid);
 // Byte offsets inside one layer's activation block of the persistent kernel.
 struct FusedActLayout {
-  size_t q, attn, mlp, h_mid, h_out, stride;
+  size_t q, attn, mlp, h_mid, h_out, part, stride;
 };
 FusedActLayout fused_act_layout(const Dims& d);
 size_t fused_act_bytes(const Dims& d);
