@@ -30,6 +30,13 @@ __device__ __forceinline__ uint32_t f2_to_bf16x2(float lo, float hi) {
   if (hi != hi) p = (p & 0x0000ffffu) | 0x7fc00000u;
   return p;
 }
+// Two values rounded to bf16 (RNE) and packed (lo, hi), NaN left as the
+// hardware produces it: for values that stay inside a computation.
+__device__ __forceinline__ uint32_t f2_to_bf16x2_raw(float lo, float hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, re_bf16x2));
+}
 // Rounding to bf16 inside a computation: a NaN stays a NaN (its payload does
 // not matter until a value is stored, and stores canonicalize), so the
 // hardware conversion is used as is.

@@ -129,6 +129,32 @@ struct NormIn {
   Vec8<T> w[kNormChunks];
 };
 
+// The RMSNorm output of eight elements: T(T(h * rs) * w) for each
+// (batched_decoder_step.py:227-229).  bf16: the two roundings of an element
+// pair go through one packed conversion each, and the result keeps the
+// hardware's NaN (the rows stay in LDS as products' inputs, where a NaN's
+// payload does not matter): every non-NaN value is the one Elt<T>::r and
+// Vec8::from_floats give.
+template <typename T>
+__device__ __forceinline__ Vec8<T> norm_apply(const Vec8<T>& h, const Vec8<T>& w, float rs) {
+  float out[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = Elt<T>::r(Elt<T>::r(h.get(e) * rs) * w.get(e));
+  return Vec8<T>::from_floats(out);
+}
+template <>
+__device__ __forceinline__ Vec8<bf16_t> norm_apply<bf16_t>(const Vec8<bf16_t>& h, const Vec8<bf16_t>& w, float rs) {
+  Vec8<bf16_t> r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t hp = h.v[i], wp = w.v[i];
+    const uint32_t y = f2_to_bf16x2_raw(__uint_as_float(hp << 16) * rs, __uint_as_float(hp & 0xffff0000u) * rs);
+    r.v[i] = f2_to_bf16x2_raw(__uint_as_float(y << 16) * __uint_as_float(wp << 16),
+                              __uint_as_float(y & 0xffff0000u) * __uint_as_float(wp & 0xffff0000u));
+  }
+  return r;
+}
+
 template <typename T, int MB>
 __device__ __forceinline__ void norm_load(NormIn<T, MB>& in, const T* __restrict__ hidden, const T* __restrict__ norm_w,
                                           int b0, int B, int H, int tid) {
@@ -189,11 +215,7 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
         Vec8<T>* p = reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8);
-        const Vec8<T> h = *p;
-        float out[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = Elt<T>::r(Elt<T>::r(h.get(e) * rs[m]) * in.w[j].get(e));
-        *p = Vec8<T>::from_floats(out);
+        *p = norm_apply<T>(*p, in.w[j], rs[m]);
       }
     }
   }
@@ -270,11 +292,7 @@ __device__ __forceinline__ void norm_in_lds(bf16_t* xs, const Vec8<bf16_t> (&w)[
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
         Vec8<bf16_t>* p = reinterpret_cast<Vec8<bf16_t>*>(xs + m * H + c * 8);
-        const Vec8<bf16_t> h = *p;
-        float out[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = round_bf16(round_bf16(h.get(e) * rs[m]) * w[j].get(e));
-        *p = Vec8<bf16_t>::from_floats(out);
+        *p = norm_apply<bf16_t>(*p, w[j], rs[m]);
       }
     }
   }
