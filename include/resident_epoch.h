@@ -168,8 +168,12 @@ int32_t resident_epoch_write_state(void *engine, const char *name,
  * "kv_heads", "head_dim", "intermediate", "vocab", "physical_blocks",
  * "block_size", "blocks_per_row", "capacity", "dtype_bytes",
  * "feed_bytes", "fetch_bytes", "cache_bytes", "weight_bytes",
- * "streamed_weight_bytes", "configured_eos", "graph_kernels" (kernels in one
- * decoder step).  Return 0 or -1 for an unknown key. */
+ * "streamed_weight_bytes", "configured_eos", "import_feed_bytes",
+ * "step_ops" (entries of a decoder step's launch list), "ops_per_layer",
+ * "timing_layer", launch-plan sizes ("qkv_grid", "gateup_grid", "lm_grid",
+ * "o_segments", "down_segments", "gemv_rows_per_pass"), "fused_step" (1: a
+ * step is the persistent kernel), "fused_grid" (its workgroups),
+ * "compute_units".  Return 0 or -1 for an unknown key. */
 int32_t resident_epoch_info(void *engine, const char *key, int64_t *value);
 
 /* Kernel timing in the epoch: when enabled, each epoch runs as graph part 1,
