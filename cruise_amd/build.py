@@ -1,8 +1,8 @@
 """Build libresident_epoch.so for gfx950 with hipcc (in-tree, no JIT cache).
 
 ``python -m cruise_amd.build`` compiles ``cruise_amd/csrc/*.hip`` into
-``cruise_amd/lib/libresident_epoch.so``.  The library links only the HIP
-runtime: PyTorch is never linked into it.
+``cruise_amd/lib/libresident_epoch.so``.  The library links the HIP runtime
+and hipBLASLt (the batched-prefill GEMMs): PyTorch is never linked into it.
 """
 from __future__ import annotations
 
@@ -20,7 +20,8 @@ LIBRARY = LIBDIR / "libresident_epoch.so"
 SERVER = LIBDIR / "resident_epoch_server"
 SERVER_SOURCE = "re_server.cpp"
 INCLUDE = PACKAGE.parent / "include"
-SOURCES = ("re_step.hip", "re_attn.hip", "re_fused.hip", "re_ctrl.hip", "re_prefill.hip", "re_engine.hip")
+SOURCES = ("re_step.hip", "re_attn.hip", "re_fused.hip", "re_ctrl.hip", "re_prefill.hip", "re_blas.hip", "re_engine.hip")
+LINK_LIBS = ("-lhipblaslt",)  # batched-prefill GEMMs (re_blas.hip)
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -69,7 +70,7 @@ def build(verbose: bool = False, defines: tuple[str, ...] = (), output: Path | N
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
         objects = list(pool.map(compile_one, SOURCES))
     tmp = library.with_suffix(".so.tmp")
-    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), *LINK_LIBS, "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")

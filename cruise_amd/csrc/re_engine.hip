@@ -98,6 +98,8 @@ struct Engine {
   // Batched prefill scratch (grown on demand, freed with the engine).
   uint8_t* pf_mem = nullptr;
   size_t pf_bytes = 0;
+  PrefillBlas* pf_blas = nullptr;  // created on the first bf16 batched prefill
+  bool pf_blas_tried = false;
   bool pf_ready = false;
   // Device-IPC import: mapped source allocations, keyed by the 64-byte
   // handle, with their mapped sizes; closed when the engine is destroyed.
@@ -591,6 +593,7 @@ void free_engine(Engine* e) {
   if (e->h_fetch) hipHostFree(e->h_fetch);
   for (auto& kv : e->ipc_maps) (void)hipIpcCloseMemHandle(kv.second.ptr);
   if (e->pf_mem) hipFree(e->pf_mem);
+  prefill_blas_destroy(e->pf_blas);
   if (e->stream) hipStreamDestroy(e->stream);
   delete e;
 }
@@ -1213,6 +1216,10 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
                                         hipMemcpyHostToDevice) == hipSuccess)) &&
                   hipMemcpy(b + o_blocks, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice) == hipSuccess;
   if (!ok) return -2;
+  if (d.dtype_bytes == 2 && !e.pf_blas_tried) {
+    e.pf_blas_tried = true;
+    e.pf_blas = prefill_blas_create();
+  }
   const KernelEnv env = e.env();
   if (launch_clear_blocks(env, e.key_cache, e.value_cache, reinterpret_cast<const int32_t*>(b + o_blocks),
                           static_cast<int>(tables.size()), s) != hipSuccess)
@@ -1252,6 +1259,19 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
         g.lda = lda;
         g.ldw = K;
         g.ldo = ldo;
+        if (e.pf_blas != nullptr) {
+          // hipBLASLt: a store GEMM directly; a residual GEMM into the free
+          // normalized-row buffer, then h = T(h + T(A W^T))
+          GemmArgs y = g;
+          if (epi == kGemmResidual) {
+            y.out = b + o_xn;
+            y.ldo = N;
+          }
+          if (prefill_blas_gemm(e.pf_blas, y, s)) {
+            if (epi == kGemmResidual) run(launch_prefill_residual(b + out_off, b + o_xn, M, N, ldo, N, s));
+            return;
+          }
+        }
         run(launch_gemm(g, epi, d.dtype_bytes, s));
       };
       run(launch_prefill_rmsnorm(b + o_hidden, e.weights + lo.input_norm, b + o_xn, M, d.hidden, d.rms_eps,

@@ -267,6 +267,13 @@ hipError_t launch_prefill_swiglu(const void* gate, const void* up, void* out, lo
                                  hipStream_t stream);
 hipError_t launch_prefill_qkv_post(const PrefillQkv& a, int dtype_bytes, hipStream_t stream);
 hipError_t launch_gemm(const GemmArgs& a, int epi, int dtype_bytes, hipStream_t stream);
+// hipBLASLt for the bf16 prefill projections (re_blas.hip).
+struct PrefillBlas;
+PrefillBlas* prefill_blas_create();  // nullptr when hipBLASLt is unusable
+void prefill_blas_destroy(PrefillBlas* b);
+bool prefill_blas_gemm(PrefillBlas* b, const GemmArgs& g, hipStream_t stream);  // out = T(A W^T (+ bias))
+hipError_t launch_prefill_residual(void* h, const void* y, long long rows, int N, long long ldh, long long ldy,
+                                   hipStream_t stream);  // h = T(h + y)
 // The MFMA attention serves bf16 models with head_dim 128 (64-query tiles).
 bool prefill_attention_mfma(const Dims& d);
 size_t prefill_attention_lds(const Dims& d, int max_keys);
