@@ -100,6 +100,7 @@ struct Engine {
   size_t pf_bytes = 0;
   PrefillBlas* pf_blas = nullptr;  // created on the first bf16 batched prefill
   bool pf_blas_tried = false;
+  bool prefill_blas_allowed = true;  // "tuning": {"prefill_blas": 0} keeps the hand-written GEMM
   bool pf_ready = false;
   // Device-IPC import: mapped source allocations, keyed by the 64-byte
   // handle, with their mapped sizes; closed when the engine is destroyed.
@@ -242,6 +243,7 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));
     p.lm_wg = p.lm_grid;
   }
+  if (const Json* t = cfg.get("tuning")) e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
   // The persistent step kernel serves the shapes it is written for when the
   // configuration asks for it ("engine": {"fused_step": true}).
   const Json* eng = cfg.get("engine");
@@ -1218,7 +1220,7 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
   if (!ok) return -2;
   if (d.dtype_bytes == 2 && !e.pf_blas_tried) {
     e.pf_blas_tried = true;
-    e.pf_blas = prefill_blas_create();
+    if (e.prefill_blas_allowed) e.pf_blas = prefill_blas_create();
   }
   const KernelEnv env = e.env();
   if (launch_clear_blocks(env, e.key_cache, e.value_cache, reinterpret_cast<const int32_t*>(b + o_blocks),

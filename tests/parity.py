@@ -12,6 +12,8 @@ Comparison rules (the bar for this path):
 """
 from __future__ import annotations
 
+from dataclasses import replace
+
 import numpy as np
 import torch
 
@@ -55,8 +57,11 @@ def engine_config(w: Workload, *, capacity: int | None = None, weights: WeightSp
     )
 
 
-def make_runtime(w: Workload, weights: dict, *, capacity: int | None = None) -> ResidentEpochRuntime:
-    rt = ResidentEpochRuntime(engine_config(w, capacity=capacity), weights=weights)
+def make_runtime(w: Workload, weights: dict, *, capacity: int | None = None, tuning: dict | None = None) -> ResidentEpochRuntime:
+    cfg = engine_config(w, capacity=capacity)
+    if tuning:
+        cfg = replace(cfg, tuning=dict(tuning))
+    rt = ResidentEpochRuntime(cfg, weights=weights)
     # RoPE frequencies exactly as the oracle computes them (fp32 torch pow).
     from oracle.decoder import inv_freq
 

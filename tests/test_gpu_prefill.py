@@ -82,14 +82,14 @@ def epoch_after_prefill(W, rt, ctl, table, prompts, gens, K):
     assert ctrl[3] == 0
 
 
-def run_against_oracle(W, weights_dev, weights_cpu, lengths, seed, K):
+def run_against_oracle(W, weights_dev, weights_cpu, lengths, seed, K, tuning=None):
     B = W.geometry.batch
     dtype = W.dims.torch_dtype
     rng = np.random.default_rng(seed)
     table = random_tables(rng, B, W.geometry.blocks_per_row, W.geometry.physical_blocks)
     prompts = [list(map(int, rng.integers(0, W.dims.vocab, size=n))) for n in lengths]
     gens = np.arange(1, B + 1, dtype=np.int32) + seed % 1000
-    rt = make_runtime(W, weights_dev)
+    rt = make_runtime(W, weights_dev, tuning=tuning)
     try:
         _, ctl = oracle_controller(W, weights_cpu)
         reset(rt, dtype, B)
@@ -126,6 +126,13 @@ def c2_weights():
 def test_bf16_layer_prefill_matches_oracle(c2_weights):
     dev, cpu = c2_weights
     run_against_oracle(C2, dev, cpu, [41, 5, 70, 1], seed=5102, K=4)
+
+
+def test_bf16_layer_prefill_hand_written_gemm_matches_oracle(c2_weights):
+    """The same check with the projections on the hand-written MFMA GEMM
+    (the path taken when hipBLASLt cannot plan a shape)."""
+    dev, cpu = c2_weights
+    run_against_oracle(C2, dev, cpu, [41, 5, 70, 1], seed=5104, K=4, tuning={"prefill_blas": 0})
 
 
 def test_bf16_layer_prefill_matches_single_row_prefill(c2_weights):
