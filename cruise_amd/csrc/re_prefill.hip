@@ -440,22 +440,43 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
     lds_barrier();
   }
   tile_load(0, voff);  // the first value tile travels during the softmax
-  // Softmax of each query row: four threads per row.
+  // Softmax of each query row: four threads per row, eight scores per
+  // 16-byte LDS access.  Exact global max and sum, then each p rounded to
+  // bf16; exp(x) is the hardware 2^(x log2 e) (v_exp_f32), whose fp32 error
+  // is far below the bf16 rounding of p.  Keys past the row's causal limit
+  // hold -inf (p = 0); a padding query row (nvalid = 0) gets p = 0.
   {
     const int qi = tid >> 2, part = tid & 3;
     const int nvalid = qi < nqt ? p0 + qi + 1 : 0;
-    bf16_t* srow = S + qi * sld;
+    const int nvec = (nvalid + 7) / 8, nall = nkt * kAk / 8;
+    Vec8<bf16_t>* srow = reinterpret_cast<Vec8<bf16_t>*>(S + qi * sld);
     float mx = -INFINITY;
-    for (int j = part; j < nvalid; j += 4) mx = fmaxf(mx, bf16_to_f(srow[j]));
+    for (int v = part; v < nvec; v += 4) {
+      const Vec8<bf16_t> x = srow[v];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x.get(e));
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    constexpr float kLog2e = 1.44269504088896340736f;
+    const float base = mx * kLog2e;
     float es = 0.f;
-    for (int j = part; j < nvalid; j += 4) es += expf(bf16_to_f(srow[j]) - mx);
+    for (int v = part; v < nvec; v += 4) {
+      const Vec8<bf16_t> x = srow[v];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) es += __builtin_amdgcn_exp2f(fmaf(x.get(e), kLog2e, -base));
+    }
     es += __shfl_xor(es, 1, 64);
     es += __shfl_xor(es, 2, 64);
-    const float inv = 1.0f / es;
-    for (int j = part; j < nkt * kAk; j += 4)
-      srow[j] = j < nvalid ? f_to_bf16(expf(bf16_to_f(srow[j]) - mx) * inv) : static_cast<bf16_t>(0);
+    const float inv = nvalid > 0 ? 1.0f / es : 0.f;
+    for (int v = part; v < nall; v += 4) {
+      const Vec8<bf16_t> x = srow[v];
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pv[e] = v * 8 + e < nvalid ? __builtin_amdgcn_exp2f(fmaf(x.get(e), kLog2e, -base)) * inv : 0.f;
+      srow[v] = Vec8<bf16_t>::from_floats(pv);
+    }
   }
   lds_barrier();
   // O = P V, fp32 accumulation.
