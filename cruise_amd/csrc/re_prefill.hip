@@ -399,8 +399,8 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
   const float scale_div = sqrtf(static_cast<float>(kAd));
   const bf16_t neg_inf = 0xFF80;
 
-  // A 64-row tile of keys (or values) in registers: vector v = tid + 256 i is
-  // row v / 16, elements (v % 16) * 8 ..+8; rows past the keys read the last.
+  // A 64-row tile of keys in registers: vector v = tid + 256 i is row v / 16,
+  // elements (v % 16) * 8 ..+8; rows past the keys read the last.
   re_u32x4 pre[4];
   auto tile_load = [&](int kt, size_t col) {
 #pragma unroll
@@ -408,6 +408,18 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
       const int v = tid + 256 * i;
       const int tok = r0 + min(min(kt, nkt - 1) * kAk + (v >> 4), nkeys - 1);
       pre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + col + (v & 15) * 8);
+    }
+  };
+  // A 64-row tile of values: vector v is row v % 64, elements (v / 64) * 8
+  // ..+8, so the 64 lanes of a wave hold one 8-column slice of 64 keys and
+  // the transposed LDS writes of one instruction cover 64 consecutive keys of
+  // one row (128 contiguous bytes, no bank conflicts).
+  auto tile_load_v = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + 256 * i;
+      const int tok = r0 + min(min(kt, nkt - 1) * kAk + (v & 63), nkeys - 1);
+      pre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + voff + (v >> 6) * 8);
     }
   };
 
@@ -439,7 +451,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
     }
     lds_barrier();
   }
-  tile_load(0, voff);  // the first value tile travels during the softmax
+  tile_load_v(0);  // the first value tile travels during the softmax
   // Softmax of each query row: four threads per row, eight scores per
   // 16-byte LDS access.  Exact global max and sum, then each p rounded to
   // bf16; exp(x) is the hardware 2^(x log2 e) (v_exp_f32), whose fp32 error
@@ -488,7 +500,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
   for (int kt = 0; kt < nkt; ++kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int v = tid + 256 * i, key = v >> 4, c = (v & 15) * 8;
+      const int v = tid + 256 * i, key = v & 63, c = (v >> 6) * 8;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t w = pre[i][e];
@@ -496,7 +508,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
         kv[(c + 2 * e + 1) * kAvld + key] = static_cast<bf16_t>(w >> 16);
       }
     }
-    tile_load(kt + 1, voff);
+    tile_load_v(kt + 1);
     lds_barrier();
 #pragma unroll
     for (int ks = 0; ks < kAk / 16; ++ks) {
