@@ -238,6 +238,18 @@ bool make_plan(Engine& e, const Json& cfg) {
   plan_grids(p, d, e.cus);
   // Optional overrides for tuning sweeps ("tuning": {"qkv_grid": n, ...}).
   if (const Json* t = cfg.get("tuning")) {
+    // "slot_weights": [w0, w1, w2, w3] (positive), or [] for equal ranges
+    if (const Json* sw = t->get("slot_weights"); sw != nullptr && sw->kind == Json::kArray && p.slot_cus > 0) {
+      bool ok = sw->arr.size() == 4;
+      for (const Json& v : sw->arr) ok = ok && v.kind == Json::kNumber && v.num >= 1 && v.num <= 1e6;
+      if (ok) {
+        for (int s = 0; s < 4; ++s) p.slot_w[s] = static_cast<int>(sw->arr[s].num);
+      } else {
+        p.slot_cus = 0;
+        p.gu_grid = p.gu_grid_eq;
+        p.lm_grid = p.lm_grid_eq;
+      }
+    }
     p.qkv_grid = std::max(1, static_cast<int>(t->number_or("qkv_grid", p.qkv_grid)));
     p.gu_grid = std::max(1, static_cast<int>(t->number_or("gu_grid", p.gu_grid)));
     p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));

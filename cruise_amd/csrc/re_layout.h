@@ -136,6 +136,9 @@ struct LaunchPlan {
   int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)
+  int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
+  int slot_w[4];   // their per-slot weights
+  int gu_grid_eq, lm_grid_eq;  // the grids for equal ranges
   int fused;       // 1: a step is the persistent kernel (re_fused.hip)
   int fused_grid;  // its workgroups: the chip's resident capacity
 };

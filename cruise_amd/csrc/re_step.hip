@@ -99,7 +99,29 @@ struct ProjArgs {
   long long slots;
   int B, H, units, heads, kv_heads, head_dim;
   float eps;
+  // Slot-weighted unit ranges (gate/up and LM head; slot_cus == 0: equal
+  // ranges): workgroup i runs in dispatch slot i / slot_cus of its CU and
+  // takes a share of the units proportional to slot_w[slot].
+  int slot_cus;
+  int slot_w[4];
 };
+
+// Unit range of workgroup g when the grid is 4 x slot_cus workgroups,
+// dispatched round-robin over the CUs (g in slot g / cus of CU g % cus).
+// The SIMD arbiter issues for the oldest waves first, so the later slots of
+// a CU stream more slowly; giving them fewer units lets every slot finish
+// together, which keeps enough loads in flight until the end.
+__device__ __forceinline__ int slot_prefix(const ProjArgs& a, int g) {
+  const int cus = a.slot_cus;
+  long long p = 0, tot = 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    tot += (long long)cus * a.slot_w[s];
+    if (s < g / cus) p += (long long)cus * a.slot_w[s];
+    else if (s == g / cus) p += (long long)(g % cus) * a.slot_w[s];
+  }
+  return g >= 4 * cus ? a.units : static_cast<int>((long long)a.units * p / tot);
+}
 
 template <int KIND, typename T>
 __device__ __forceinline__ void proj_rows(const ProjArgs& a, int u, const T* W0, const T* W1,
@@ -165,9 +187,16 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   const T* W0 = static_cast<const T*>(a.w0);
   const T* W1 = static_cast<const T*>(a.w1);
   float* wred = red + wave * (kRowsPerWave * MB);
-  const int iters = (a.units + gridDim.x * WAVES - 1) / (gridDim.x * WAVES);
-  const int u_end = min((int)(blockIdx.x + 1) * iters * WAVES, a.units);
-  int u = blockIdx.x * iters * WAVES + wave;
+  int u_begin, u_end;
+  if (a.slot_cus > 0) {
+    u_begin = slot_prefix(a, blockIdx.x);
+    u_end = slot_prefix(a, blockIdx.x + 1);
+  } else {
+    const int iters = (a.units + gridDim.x * WAVES - 1) / (gridDim.x * WAVES);
+    u_begin = blockIdx.x * iters * WAVES;
+    u_end = min((int)(blockIdx.x + 1) * iters * WAVES, a.units);
+  }
+  int u = u_begin + wave;
 
   // Issue order (loads complete in issue order): the early-exit flag, the
   // hidden rows and norm weight, then the first row pair's weights, so the
@@ -428,6 +457,16 @@ static void launch_proj(const ProjArgs& a, dim3 grid, size_t smem, hipStream_t s
     k_proj<T, MB, WAVES, KIND, false><<<grid, WAVES * 64, smem, stream>>>(a);
 }
 
+// Slot-weighted ranges when the plan has them and the grid is exactly four
+// workgroups per CU.
+static void set_slots(ProjArgs& a, const LaunchPlan& p, int grid) {
+  a.slot_cus = 0;
+  if (p.slot_cus > 0 && grid == 4 * p.slot_cus && p.row_tiles == 1) {
+    a.slot_cus = p.slot_cus;
+    for (int s = 0; s < 4; ++s) a.slot_w[s] = p.slot_w[s];
+  }
+}
+
 template <typename T, int MB>
 static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipStream_t stream, int begin,
                                  int end) {
@@ -535,6 +574,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     gu.H = d.hidden;
     gu.units = d.intermediate;
     gu.eps = d.rms_eps;
+    set_slots(gu, p, p.gu_grid);
     if (want()) launch_proj<T, MB, WAVES, kGateUp>(gu, dim3(p.gu_grid, p.row_tiles), proj_smem, stream);
 
     ResidArgs dn{};
@@ -566,6 +606,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
   lm.H = d.hidden;
   lm.units = d.vocab / 2;
   lm.eps = d.rms_eps;
+  set_slots(lm, p, p.lm_grid);
   if (want()) launch_proj<T, MB, WAVES, kLmHead>(lm, dim3(p.lm_grid, p.row_tiles), proj_smem, stream);
   return hipGetLastError();
 }
@@ -593,6 +634,23 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
                   (d.intermediate + WAVES - 1) / WAVES);
   p.lm_grid = fit(full ? k_proj<T, MB, WAVES, kLmHead, true> : k_proj<T, MB, WAVES, kLmHead, false>,
                   (d.vocab / 2 + WAVES - 1) / WAVES);
+  // Slot-weighted ranges for gate/up and the LM head at four workgroups per
+  // CU (bf16, one row tile): 1 : 1 : 0.9 : 0.8 measured best on MI355X.
+  p.gu_grid_eq = p.gu_grid;
+  p.lm_grid_eq = p.lm_grid;
+  p.slot_cus = 0;
+  int per_cu = 0;
+  if (sizeof(T) == 2 && p.row_tiles == 1 &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, full ? k_proj<T, MB, WAVES, kGateUp, true> : k_proj<T, MB, WAVES, kGateUp, false>, WAVES * 64,
+          smem) == hipSuccess &&
+      per_cu == 4 && d.intermediate >= 16 * cus && d.vocab / 2 >= 16 * cus) {
+    p.slot_cus = cus;
+    const int w[4] = {1000, 1000, 900, 800};
+    for (int s = 0; s < 4; ++s) p.slot_w[s] = w[s];
+    p.gu_grid = 4 * cus;
+    p.lm_grid = 4 * cus;
+  }
   p.lm_wg = p.lm_grid;
 }
 
