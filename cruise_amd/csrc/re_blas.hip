@@ -105,7 +105,7 @@ PrefillBlas* prefill_blas_create() {
 
 void prefill_blas_destroy(PrefillBlas* b) {
   if (b == nullptr) return;
-  if (b->workspace) hipFree(b->workspace);
+  if (b->workspace) (void)hipFree(b->workspace);
   if (b->handle) hipblasLtDestroy(b->handle);
   delete b;
 }

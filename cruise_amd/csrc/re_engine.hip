@@ -255,7 +255,9 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));
     p.lm_wg = p.lm_grid;
   }
-  if (const Json* t = cfg.get("tuning")) e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
+  if (const Json* t = cfg.get("tuning")) {
+    e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
+  }
   // The persistent step kernel serves the shapes it is written for when the
   // configuration asks for it ("engine": {"fused_step": true}).
   const Json* eng = cfg.get("engine");
@@ -1255,8 +1257,6 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
     er.V = d.vocab;
     er.head_dim = d.head_dim;
     run(launch_prefill_embed(er, d.dtype_bytes, s));
-    int max_keys = 1;
-    for (const auto& p : prompts) max_keys = std::max(max_keys, static_cast<int>(p.size()) - 1);
     const long long cache_layer_elems = d.slots() * d.kv_dim();
     for (int l = 0; l < d.layers && err == hipSuccess; ++l) {
       const LayerOffsets& lo = e.layer_off[l];
@@ -1314,7 +1314,6 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
       at.heads = d.heads;
       at.kv_heads = d.kv_heads;
       at.head_dim = d.head_dim;
-      at.score_ld = (max_keys + 63) / 64 * 64 + 8;
       run(launch_prefill_attention(at, d, static_cast<int>(tiles.size()), s));
       gemm(o_attn, d.q_dim(), lo.o_w, SIZE_MAX, o_hidden, d.hidden, d.hidden, d.q_dim(), kGemmResidual);
       run(launch_prefill_rmsnorm(b + o_hidden, e.weights + lo.post_norm, b + o_xn, M, d.hidden, d.rms_eps,

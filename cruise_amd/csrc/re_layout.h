@@ -252,7 +252,7 @@ struct PrefillAttn {           // causal attention within each row's prompt
   void* out;                   // T [M, heads * d]
   const int32_t* pos;          // [M]
   const int4* tiles;           // MFMA path: {first query token, row's first token, queries, first position}
-  int M, ld, heads, kv_heads, head_dim, score_ld;
+  int M, ld, heads, kv_heads, head_dim;
 };
 enum GemmEpilogue : int { kGemmStore = 0, kGemmResidual = 1 };
 struct GemmArgs {              // out[M,N] (epilogue) A[M,K] W[N,K]^T

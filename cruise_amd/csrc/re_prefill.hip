@@ -361,21 +361,37 @@ __global__ void __launch_bounds__(256) k_pf_attn_rows(PrefillAttn a) {
   }
 }
 
-// bf16, head_dim 128: one workgroup per (tile of up to 64 queries of one row,
-// head).  Wave w owns queries (w / 2) * 32 ..+32 and, per 64-key tile, keys
-// (w % 2) * 32 ..+32 of Q K^T; for P V it owns output columns (w % 2) * 64
-// ..+64.  The tile's bf16 scores, then probabilities, stay in LDS
-// (64 x keys), so the softmax is exact: global max and sum, then each p
-// rounded to bf16, as the decode step does.
-constexpr int kAq = 64, kAk = 64, kAd = 128;
+// Tile shapes of the MFMA attention below (keys per tile, head dim; the
+// query tiles of up to 64 come from the launch's tile list).
+constexpr int kAk = 64, kAd = 128;
 constexpr int kAkld = kAd + 8;  // K tile row stride (elements)
 constexpr int kAvld = kAk + 8;  // transposed V tile row stride
 
-__global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16_t* kv = reinterpret_cast<bf16_t*>(smem_raw);  // K tile [64][136] or V^T tile [128][72]
-  bf16_t* S = kv + kAd * kAvld;                      // [64][sld]
-  const int sld = a.score_ld;
+// bf16, head_dim 128: one workgroup per (tile of up to 64 queries of one row,
+// head), two passes over the key tiles of 64, no score tile in LDS.
+// Wave w owns queries (w / 2) * 32 ..+32 and, in every key tile, keys
+// (w % 2) * 32 ..+32.  S^T = K Q^T on MFMA (keys are the A rows, queries the
+// B columns), so a lane holds 16 scores of one query (its column).
+//   pass 1: every score s = bf16(bf16(q.k) / sqrt(d)) (keys past the
+//     query's causal limit are -inf); per lane a running max and the sum of
+//     exp(s - max) rescaled as the max grows; lanes l and l ^ 32 and the two
+//     key halves are then combined: the exact row max M and the sum L.
+//   pass 2: the scores again, p = bf16(exp(s - M) / L) -- the reference's
+//     rounding point -- and O += P V on MFMA straight from the score
+//     registers: for each 16-key block the MFMA's k index runs over the keys
+//     in the order the accumulator layout holds them (j 0-7 from lanes 0-31:
+//     keys +0..3 and +8..11; j 8-15 from lanes 32-63: keys +4..7 and
+//     +12..15), and the value rows are read from the transposed V tile in
+//     the same order.  The two key halves' partial O are added at the end.
+// LDS: one K tile and one transposed V tile (about 36 KB), independent of
+// the prompt length.
+constexpr int kFlashLds = kAk * kAkld * 2 + kAd * kAvld * 2;
+
+__global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
+  __shared__ __align__(16) unsigned char smem[kFlashLds];
+  __shared__ float stat[2][2][32][2];  // [query half][key half][query][max, sum]
+  bf16_t* Ks = reinterpret_cast<bf16_t*>(smem);  // [64 keys][136]
+  bf16_t* Vt = Ks + kAk * kAkld;                  // [128 d][72 keys]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int4 tile = a.tiles[blockIdx.x];  // first query token, first token of the row, queries, first query's position
   const int h = blockIdx.y;
@@ -384,152 +400,193 @@ __global__ void __launch_bounds__(256) k_pf_attn_mfma(PrefillAttn a) {
   const bf16_t* qkv = static_cast<const bf16_t*>(a.qkv);
   const size_t koff = (size_t)nq * kAd + (size_t)kvh * kAd;
   const size_t voff = (size_t)(nq + a.kv_heads) * kAd + (size_t)kvh * kAd;
-  const int nkeys = p0 + nqt;  // keys 0 .. p0 + nqt - 1 of the row
+  const int nkeys = p0 + nqt;
   const int nkt = (nkeys + kAk - 1) / kAk;
-  const int sm = wave >> 1, sn = wave & 1;
+  const int sm = wave >> 1, sn = wave & 1, hi = lane >> 5;
+  const int qloc = sm * 32 + (lane & 31);  // this lane's query within the tile
+  const int qlim = p0 + qloc;              // its visible keys: j <= qlim
+  constexpr float kLog2e = 1.44269504088896340736f;
+  const float scale_div = sqrtf(static_cast<float>(kAd));
 
-  // Q fragments of this wave's 32 queries (rows past the tile read the last one)
+  // Q fragments (B operand): query qloc (rows past the tile read the last one)
   bf16x8_t qf[kAd / 16];
   {
-    const int qi = min(sm * 32 + (lane & 31), nqt - 1);
-    const bf16_t* qrow = qkv + (size_t)(m_start + qi) * a.ld + (size_t)h * kAd + (lane >> 5) * 8;
+    const int qi = min(qloc, nqt - 1);
+    const bf16_t* qrow = qkv + (size_t)(m_start + qi) * a.ld + (size_t)h * kAd + hi * 8;
 #pragma unroll
     for (int ks = 0; ks < kAd / 16; ++ks) qf[ks] = lds_frag(qrow + ks * 16);
   }
-  const float scale_div = sqrtf(static_cast<float>(kAd));
-  const bf16_t neg_inf = 0xFF80;
-
-  // A 64-row tile of keys in registers: vector v = tid + 256 i is row v / 16,
-  // elements (v % 16) * 8 ..+8; rows past the keys read the last.
-  re_u32x4 pre[4];
-  auto tile_load = [&](int kt, size_t col) {
+  // Key tile in registers: vector v = tid + 256 i is key v / 16, elements
+  // (v % 16) * 8 ..+8.  Value tile: key v % 64, elements (v / 64) * 8 ..+8
+  // (the transposed LDS writes of one instruction cover 64 consecutive keys
+  // of one row).  Keys past the row read the last one.
+  re_u32x4 kpre[4], vpre[4];
+  auto load_k = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i;
       const int tok = r0 + min(min(kt, nkt - 1) * kAk + (v >> 4), nkeys - 1);
-      pre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + col + (v & 15) * 8);
+      kpre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + koff + (v & 15) * 8);
     }
   };
-  // A 64-row tile of values: vector v is row v % 64, elements (v / 64) * 8
-  // ..+8, so the 64 lanes of a wave hold one 8-column slice of 64 keys and
-  // the transposed LDS writes of one instruction cover 64 consecutive keys of
-  // one row (128 contiguous bytes, no bank conflicts).
-  auto tile_load_v = [&](int kt) {
+  auto load_v = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i;
       const int tok = r0 + min(min(kt, nkt - 1) * kAk + (v & 63), nkeys - 1);
-      pre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + voff + (v >> 6) * 8);
+      vpre[i] = *reinterpret_cast<const re_u32x4*>(qkv + (size_t)tok * a.ld + voff + (v >> 6) * 8);
     }
   };
-
-  // Scores: S[q][j] = bf16(bf16(q.k_j) / sqrt(d)), causal mask as -inf.  The
-  // next key tile is in flight while this one is multiplied.
-  tile_load(0, koff);
-  for (int kt = 0; kt < nkt; ++kt) {
+  auto store_k = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i;
-      *reinterpret_cast<re_u32x4*>(&kv[(v >> 4) * kAkld + (v & 15) * 8]) = pre[i];
+      *reinterpret_cast<re_u32x4*>(&Ks[(v >> 4) * kAkld + (v & 15) * 8]) = kpre[i];
     }
-    tile_load(kt + 1, koff);
-    lds_barrier();
-    f32x16_t acc;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < kAd / 16; ++ks) {
-      const bf16x8_t bfr = lds_frag(&kv[(sn * 32 + (lane & 31)) * kAkld + ks * 16 + (lane >> 5) * 8]);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[ks], bfr, acc, 0, 0, 0);
-    }
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int qi = sm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      const int kj = kt * kAk + sn * 32 + (lane & 31);
-      const float s = round_bf16(round_bf16(acc[v]) / scale_div);
-      S[qi * sld + kj] = kj <= p0 + qi ? f_to_bf16(s) : neg_inf;
-    }
-    lds_barrier();
-  }
-  tile_load_v(0);  // the first value tile travels during the softmax
-  // Softmax of each query row: four threads per row, eight scores per
-  // 16-byte LDS access.  Exact global max and sum, then each p rounded to
-  // bf16; exp(x) is the hardware 2^(x log2 e) (v_exp_f32), whose fp32 error
-  // is far below the bf16 rounding of p.  Keys past the row's causal limit
-  // hold -inf (p = 0); a padding query row (nvalid = 0) gets p = 0.
-  {
-    const int qi = tid >> 2, part = tid & 3;
-    const int nvalid = qi < nqt ? p0 + qi + 1 : 0;
-    const int nvec = (nvalid + 7) / 8, nall = nkt * kAk / 8;
-    Vec8<bf16_t>* srow = reinterpret_cast<Vec8<bf16_t>*>(S + qi * sld);
-    float mx = -INFINITY;
-    for (int v = part; v < nvec; v += 4) {
-      const Vec8<bf16_t> x = srow[v];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x.get(e));
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    constexpr float kLog2e = 1.44269504088896340736f;
-    const float base = mx * kLog2e;
-    float es = 0.f;
-    for (int v = part; v < nvec; v += 4) {
-      const Vec8<bf16_t> x = srow[v];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) es += __builtin_amdgcn_exp2f(fmaf(x.get(e), kLog2e, -base));
-    }
-    es += __shfl_xor(es, 1, 64);
-    es += __shfl_xor(es, 2, 64);
-    const float inv = nvalid > 0 ? 1.0f / es : 0.f;
-    for (int v = part; v < nall; v += 4) {
-      const Vec8<bf16_t> x = srow[v];
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        pv[e] = v * 8 + e < nvalid ? __builtin_amdgcn_exp2f(fmaf(x.get(e), kLog2e, -base)) * inv : 0.f;
-      srow[v] = Vec8<bf16_t>::from_floats(pv);
-    }
-  }
-  lds_barrier();
-  // O = P V, fp32 accumulation.
-  f32x16_t o[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
-  for (int kt = 0; kt < nkt; ++kt) {
+  };
+  auto store_v = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i, key = v & 63, c = (v >> 6) * 8;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t w = pre[i][e];
-        kv[(c + 2 * e) * kAvld + key] = static_cast<bf16_t>(w & 0xffffu);
-        kv[(c + 2 * e + 1) * kAvld + key] = static_cast<bf16_t>(w >> 16);
+        const uint32_t w = vpre[i][e];
+        Vt[(c + 2 * e) * kAvld + key] = static_cast<bf16_t>(w & 0xffffu);
+        Vt[(c + 2 * e + 1) * kAvld + key] = static_cast<bf16_t>(w >> 16);
       }
     }
-    tile_load_v(kt + 1);
+  };
+  // Scores of key tile kt for this lane's query: s[v] is key
+  // kt * 64 + sn * 32 + 8 (v / 4) + 4 hi + v % 4.
+  auto scores = [&](int kt, float (&sc)[16]) {
+    f32x16_t acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < kAd / 16; ++ks) {
+      const bf16x8_t kf = lds_frag(&Ks[(sn * 32 + (lane & 31)) * kAkld + ks * 16 + hi * 8]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int j = kt * kAk + sn * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+      const float x = round_bf16(round_bf16(acc[v]) / scale_div);
+      sc[v] = j <= qlim ? x : -INFINITY;
+    }
+  };
+
+  // Pass 1: row max and sum.
+  float m = -INFINITY, l = 0.f;
+  load_k(0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    store_k();
+    load_k(kt + 1);
     lds_barrier();
+    float sc[16];
+    scores(kt, sc);
+    float tmax = sc[0];
 #pragma unroll
-    for (int ks = 0; ks < kAk / 16; ++ks) {
-      const bf16x8_t af = lds_frag(&S[(sm * 32 + (lane & 31)) * sld + kt * kAk + ks * 16 + (lane >> 5) * 8]);
+    for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, sc[v]);
+    const float mn = fmaxf(m, tmax);
+    if (mn != -INFINITY) {
+      const float bn = mn * kLog2e;
+      float add = 0.f;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const bf16x8_t bfr = lds_frag(&kv[((sn * 2 + t) * 32 + (lane & 31)) * kAvld + ks * 16 + (lane >> 5) * 8]);
-        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr, o[t], 0, 0, 0);
+      for (int v = 0; v < 16; ++v) add += sc[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[v], kLog2e, -bn));
+      l = (m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -bn))) + add;
+      m = mn;
+    }
+    lds_barrier();
+  }
+  {
+    const float m2 = __shfl_xor(m, 32, 64), l2 = __shfl_xor(l, 32, 64);
+    const float mm = fmaxf(m, m2);
+    const float bm = mm * kLog2e;
+    const float a1 = m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -bm));
+    const float a2 = m2 == -INFINITY ? 0.f : l2 * __builtin_amdgcn_exp2f(fmaf(m2, kLog2e, -bm));
+    m = mm;
+    l = a1 + a2;
+  }
+  if (hi == 0) {
+    stat[sm][sn][lane & 31][0] = m;
+    stat[sm][sn][lane & 31][1] = l;
+  }
+  lds_barrier();
+  float M, inv;
+  {
+    const float m0 = stat[sm][0][lane & 31][0], l0 = stat[sm][0][lane & 31][1];
+    const float m1 = stat[sm][1][lane & 31][0], l1 = stat[sm][1][lane & 31][1];
+    M = fmaxf(m0, m1);
+    const float bm = M * kLog2e;
+    const float a0 = m0 == -INFINITY ? 0.f : l0 * __builtin_amdgcn_exp2f(fmaf(m0, kLog2e, -bm));
+    const float a1 = m1 == -INFINITY ? 0.f : l1 * __builtin_amdgcn_exp2f(fmaf(m1, kLog2e, -bm));
+    const float L = a0 + a1;
+    inv = L > 0.f ? 1.0f / L : 0.f;
+  }
+  const float base = M * kLog2e;
+
+  // Pass 2: P V.
+  f32x16_t o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
+  load_k(0);
+  load_v(0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    store_k();
+    store_v();
+    load_k(kt + 1);
+    load_v(kt + 1);
+    lds_barrier();
+    float sc[16];
+    scores(kt, sc);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = sc[8 * b + e];
+        pv[e] = x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -base)) * inv;
+      }
+      re_u32x4 pw;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pw[e] = f2_to_bf16x2(pv[2 * e], pv[2 * e + 1]);
+      const bf16x8_t af = __builtin_bit_cast(bf16x8_t, pw);
+      const int kb = sn * 32 + 16 * b + 4 * hi;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16_t* vr = &Vt[(t * 32 + (lane & 31)) * kAvld + kb];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 up = *reinterpret_cast<const uint2*>(vr + 8);
+        const re_u32x4 bw = {lo.x, lo.y, up.x, up.y};
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8_t, bw), o[t], 0, 0, 0);
       }
     }
     lds_barrier();
   }
-  bf16_t* out = static_cast<bf16_t*>(a.out);
+  // The two key halves' partial O: the sn = 1 waves hand theirs over in LDS
+  // (the tiles are free now), the sn = 0 waves add (sn 0 + sn 1) and store.
+  float* ox = reinterpret_cast<float*>(smem);  // [2 query halves][4][16][64]
+  if (sn == 1) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int qi = sm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      const int col = (sn * 2 + t) * 32 + (lane & 31);
-      if (qi < nqt) out[(size_t)(m_start + qi) * nq * kAd + (size_t)h * kAd + col] = f_to_bf16(o[t][v]);
-    }
+      for (int v = 0; v < 16; ++v) ox[((sm * 4 + t) * 16 + v) * 64 + lane] = o[t][v];
+  }
+  lds_barrier();
+  if (sn == 0) {
+    bf16_t* out = static_cast<bf16_t*>(a.out);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int qi = sm * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+        const int col = t * 32 + (lane & 31);
+        const float y = o[t][v] + ox[((sm * 4 + t) * 16 + v) * 64 + lane];
+        if (qi < nqt) out[(size_t)(m_start + qi) * nq * kAd + (size_t)h * kAd + col] = f_to_bf16(y);
+      }
+  }
 }
 
 }  // namespace
@@ -595,25 +652,19 @@ hipError_t launch_gemm(const GemmArgs& a, int epi, int dtype_bytes, hipStream_t 
   return hipGetLastError();
 }
 
-// The tile's scores for the whole window must fit the LDS (window <= 1024).
-bool prefill_attention_mfma(const Dims& d) {
-  const size_t bytes = (size_t)kAd * kAvld * 2 + (size_t)kAq * ((d.capacity + kAk - 1) / kAk * kAk + 8) * 2;
-  return d.dtype_bytes == 2 && d.head_dim == kAd && bytes <= 160 * 1024;
-}
+// The MFMA attention serves bf16 models with head_dim 128 (any window: its
+// LDS does not depend on the prompt length).
+bool prefill_attention_mfma(const Dims& d) { return d.dtype_bytes == 2 && d.head_dim == kAd; }
 
+// Dynamic LDS of the per-(token, head) kernel: the scores of the window.
 size_t prefill_attention_lds(const Dims& d, int max_keys) {
-  if (prefill_attention_mfma(d)) {
-    const int nk = (max_keys + kAk - 1) / kAk * kAk;
-    return (size_t)kAd * kAvld * 2 + (size_t)kAq * (nk + 8) * 2;
-  }
+  (void)d;
   return (size_t)max_keys * sizeof(float);
 }
 
 hipError_t prepare_prefill(const Dims& d) {
+  if (prefill_attention_mfma(d)) return hipSuccess;
   const int bytes = static_cast<int>(prefill_attention_lds(d, d.capacity));
-  if (prefill_attention_mfma(d))
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(k_pf_attn_mfma),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   if (d.dtype_bytes == 2)
     return hipFuncSetAttribute(reinterpret_cast<const void*>(k_pf_attn_rows<bf16_t>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -624,9 +675,8 @@ hipError_t prepare_prefill(const Dims& d) {
 hipError_t launch_prefill_attention(const PrefillAttn& a, const Dims& d, int ntiles, hipStream_t stream) {
   if (a.M <= 0) return hipSuccess;
   if (prefill_attention_mfma(d)) {
-    if (ntiles <= 0 || a.score_ld % 8 != 0) return hipErrorInvalidValue;
-    const size_t bytes = (size_t)kAd * kAvld * 2 + (size_t)kAq * a.score_ld * 2;
-    k_pf_attn_mfma<<<dim3(ntiles, d.heads), 256, bytes, stream>>>(a);
+    if (ntiles <= 0) return hipErrorInvalidValue;
+    k_pf_attn_flash<<<dim3(ntiles, d.heads), 256, 0, stream>>>(a);
   } else {
     if (256 % d.head_dim != 0 || d.head_dim % 8 != 0) return hipErrorInvalidValue;
     const size_t bytes = (size_t)d.capacity * sizeof(float);
