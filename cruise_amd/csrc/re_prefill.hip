@@ -82,15 +82,24 @@ __global__ void __launch_bounds__(256) k_pf_rmsnorm(const void* x, const void* w
 
 // gate = silu(g), product with up (batched_decoder_step.py:391-398); g and up
 // arrive rounded to T by their GEMMs.
+// Eight elements per thread and step (16-byte bf16 accesses); n % 8 == 0.
 template <typename T>
 __global__ void __launch_bounds__(256) k_pf_swiglu(const void* gate, const void* up, void* out, long long n) {
   const T* g = static_cast<const T*>(gate);
   const T* u = static_cast<const T*>(up);
   T* o = static_cast<T*>(out);
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
-    const float gv = Elt<T>::f(g[i]);
-    const float sg = Elt<T>::r(gv / (1.0f + expf(-gv)));
-    o[i] = Elt<T>::t(Elt<T>::r(sg * Elt<T>::f(u[i])));
+  const long long nv = n / 8;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += (long long)gridDim.x * blockDim.x) {
+    const Vec8<T> gv = Vec8<T>::load(g + i * 8);
+    const Vec8<T> uv = Vec8<T>::load(u + i * 8);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = gv.get(e);
+      const float sg = Elt<T>::r(x / (1.0f + expf(-x)));
+      y[e] = Elt<T>::r(sg * uv.get(e));
+    }
+    *reinterpret_cast<Vec8<T>*>(o + i * 8) = Vec8<T>::from_floats(y);
   }
 }
 
@@ -616,7 +625,8 @@ hipError_t launch_prefill_rmsnorm(const void* x, const void* w, void* y, int M, 
 hipError_t launch_prefill_swiglu(const void* gate, const void* up, void* out, long long n, int dtype_bytes,
                                  hipStream_t stream) {
   if (n <= 0) return hipSuccess;
-  const int blocks = static_cast<int>(std::min<long long>((n + 255) / 256, 8192));
+  if (n % 8 != 0) return hipErrorInvalidValue;  // rows of the intermediate size, a multiple of 8
+  const int blocks = static_cast<int>(std::min<long long>((n / 8 + 255) / 256, 16384));
   if (dtype_bytes == 2)
     k_pf_swiglu<bf16_t><<<blocks, 256, 0, stream>>>(gate, up, out, n);
   else
