@@ -6,9 +6,8 @@ for bit: decoder-step logits, written and untouched KV, and, over several
 consecutive K=8 epochs after prefilling 2-5 token prompts, the epoch
 histories, control records and the resident caches.  A difference in any bit
 means a hand-off between workgroups of the persistent kernel read a value
-before it was written (or a stale copy).  The oracle parity of the default
-(persistent) path is covered by the C2/C3 tests; here the per-op path is the
-reference.
+before it was written (or a stale copy).  The per-op path (the default) is
+checked against the oracle by the C1-C5 tests; here it is the reference.
 
 Workloads: one Qwen2.5-7B layer (C2 shape, block table permuted over a
 64-block pool) and the full 28-layer model (the bench workload), plus an
