@@ -15,6 +15,8 @@ the oracle's (teacher forced where the top-2 margin is not decisive).
 """
 from __future__ import annotations
 
+from dataclasses import replace
+
 import numpy as np
 import pytest
 import torch
@@ -22,6 +24,7 @@ import torch
 from cruise_amd.runtime import pack_feed, tiling_bytes
 from oracle.controller import EpochFeed, control_input_elements
 from oracle.weights import generate_weights
+from oracle.decoder import PagedGeometry
 from oracle.workloads import C1, C2, random_tables, slot_of
 from parity import TeacherForcing, assert_close_rel, make_runtime, oracle_controller, rel_tol
 
@@ -156,6 +159,37 @@ def test_bf16_layer_prefill_matches_single_row_prefill(c2_weights):
         reset(rt, torch.bfloat16, B)
         print("batched prefill, prompt lengths", lengths, flush=True)
         rt.prefill_batch(list(range(B)), [20 + r for r in range(B)], prompts, table)
+        k, v = read_caches(rt, torch.bfloat16)
+        slots = written_slots(table, prompts, W.geometry.block_size)
+        check_caches(W, k, k_ref, slots, "keys")
+        check_caches(W, v, v_ref, slots, "values")
+        np.testing.assert_array_equal(rt.resident_rows(), rows_ref)
+    finally:
+        rt.close()
+
+
+def test_bf16_layer_long_prompts_match_single_row_prefill(c2_weights):
+    """1,500- and 700-token prompts (window 1,536: up to 24 key tiles per
+    query tile, partial last tiles): the batched pass against the engine's
+    own per-row decoder steps."""
+    dev, _ = c2_weights
+    W = replace(C2, name="qwen7b-1layer-long",
+                geometry=PagedGeometry(batch=2, physical_blocks=32, block_size=128, blocks_per_row=12, window=1536))
+    B = W.geometry.batch
+    rng = np.random.default_rng(5105)
+    table = random_tables(rng, B, W.geometry.blocks_per_row, W.geometry.physical_blocks)
+    prompts = [list(map(int, rng.integers(0, W.dims.vocab, size=n))) for n in (1500, 700)]
+    rt = make_runtime(W, dev)
+    try:
+        reset(rt, torch.bfloat16, B)
+        print("single-row prefill, prompt lengths", [len(p) for p in prompts], flush=True)
+        for r in range(B):
+            rt.prefill(r, 40 + r, prompts[r], table[r])
+        k_ref, v_ref = read_caches(rt, torch.bfloat16)
+        rows_ref = rt.resident_rows().copy()
+        reset(rt, torch.bfloat16, B)
+        print("batched prefill", flush=True)
+        rt.prefill_batch(list(range(B)), [40 + r for r in range(B)], prompts, table)
         k, v = read_caches(rt, torch.bfloat16)
         slots = written_slots(table, prompts, W.geometry.block_size)
         check_caches(W, k, k_ref, slots, "keys")
