@@ -486,10 +486,14 @@ bool load_bundle(Engine& e, const std::string& dir) {
       std::vector<float> inv(e.dims.head_dim / 2);
       f.seekg(0);
       f.read(reinterpret_cast<char*>(inv.data()), inv.size() * sizeof(float));
-      if (f) hipMemcpy(e.scratch.inv_freq, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice);
+      // a present but unreadable file fails the load rather than leaving the
+      // computed frequencies in place silently
+      if (!f || hipMemcpy(e.scratch.inv_freq, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice) !=
+                    hipSuccess)
+        ok = false;
     }
   }
-  hipHostFree(staging);
+  (void)hipHostFree(staging);
   return ok;
 }
 
@@ -572,12 +576,12 @@ hipGraphExec_t epoch_graph(Engine& e, int K, FeedMode mode, int part) {
   hipError_t rec = record_epoch(e, K, mode, part);
   hipError_t end = hipStreamEndCapture(e.stream, &graph);
   if (rec != hipSuccess || end != hipSuccess || graph == nullptr) {
-    if (graph) hipGraphDestroy(graph);
+    if (graph) (void)hipGraphDestroy(graph);
     return nullptr;
   }
   hipGraphExec_t exec = nullptr;
   if (hipGraphInstantiateWithFlags(&exec, graph, 0) != hipSuccess) {
-    hipGraphDestroy(graph);
+    (void)hipGraphDestroy(graph);
     return nullptr;
   }
   e.graphs[key] = exec;
@@ -586,8 +590,8 @@ hipGraphExec_t epoch_graph(Engine& e, int K, FeedMode mode, int part) {
 }
 
 void drop_graphs(Engine& e) {
-  for (auto& kv : e.graphs) hipGraphExecDestroy(kv.second);
-  for (auto& kv : e.graph_defs) hipGraphDestroy(kv.second);
+  for (auto& kv : e.graphs) (void)hipGraphExecDestroy(kv.second);
+  for (auto& kv : e.graph_defs) (void)hipGraphDestroy(kv.second);
   e.graphs.clear();
   e.graph_defs.clear();
 }
@@ -597,20 +601,20 @@ void free_engine(Engine* e) {
   drop_graphs(*e);
   if (e->ev_start) (void)hipEventDestroy(e->ev_start);
   if (e->ev_stop) (void)hipEventDestroy(e->ev_stop);
-  if (e->weights) hipFree(e->weights);
-  if (e->key_cache) hipFree(e->key_cache);
-  if (e->value_cache) hipFree(e->value_cache);
-  if (e->state_mem) hipFree(e->state_mem);
-  if (e->scratch_mem) hipFree(e->scratch_mem);
-  if (e->step_mem) hipFree(e->step_mem);
-  if (e->dec_key) hipFree(e->dec_key);
-  if (e->dec_value) hipFree(e->dec_value);
-  if (e->h_feed) hipHostFree(e->h_feed);
-  if (e->h_fetch) hipHostFree(e->h_fetch);
+  if (e->weights) (void)hipFree(e->weights);
+  if (e->key_cache) (void)hipFree(e->key_cache);
+  if (e->value_cache) (void)hipFree(e->value_cache);
+  if (e->state_mem) (void)hipFree(e->state_mem);
+  if (e->scratch_mem) (void)hipFree(e->scratch_mem);
+  if (e->step_mem) (void)hipFree(e->step_mem);
+  if (e->dec_key) (void)hipFree(e->dec_key);
+  if (e->dec_value) (void)hipFree(e->dec_value);
+  if (e->h_feed) (void)hipHostFree(e->h_feed);
+  if (e->h_fetch) (void)hipHostFree(e->h_fetch);
   for (auto& kv : e->ipc_maps) (void)hipIpcCloseMemHandle(kv.second.ptr);
-  if (e->pf_mem) hipFree(e->pf_mem);
+  if (e->pf_mem) (void)hipFree(e->pf_mem);
   prefill_blas_destroy(e->pf_blas);
-  if (e->stream) hipStreamDestroy(e->stream);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
 
@@ -1029,7 +1033,7 @@ extern "C" void resident_epoch_destroy(void* opaque) {
   Engine* e = static_cast<Engine*>(opaque);
   {
     std::lock_guard<std::mutex> lock(e->execute_mutex);
-    hipStreamSynchronize(e->stream);
+    (void)hipStreamSynchronize(e->stream);  // teardown proceeds whatever a failed launch left
   }
   free_engine(e);
   g_engine_active = false;
@@ -1218,7 +1222,7 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
   const size_t o_tok = take(8 * (size_t)M), o_pos = take(4 * (size_t)M), o_slot = take(4 * (size_t)M);
   const size_t o_tiles = take(sizeof(int4) * tiles.size()), o_blocks = take(4 * tables.size());
   if (off > e.pf_bytes) {
-    if (e.pf_mem) hipFree(e.pf_mem);
+    if (e.pf_mem) (void)hipFree(e.pf_mem);
     e.pf_mem = nullptr;
     e.pf_bytes = 0;
     if (hipMalloc(&e.pf_mem, off) != hipSuccess) return -2;
