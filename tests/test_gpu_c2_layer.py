@@ -79,10 +79,12 @@ def test_decoder_step_random_tables(rt, weights_pair, seed):
             assert int(logits[r].argmax()) == int(row.argmax())
 
 
-def test_epoch_k8_random_tables(rt, weights_pair):
-    """Prefill 2-5 token prompts into random blocks, then one K=8 epoch."""
+@pytest.mark.parametrize("K", [1, 2, 4, 8])
+def test_epoch_random_tables(rt, weights_pair, K):
+    """Prefill 2-5 token prompts into random blocks, then one K-step epoch
+    (every K of the resident epoch: each runs its own captured graph)."""
     _, cpu = weights_pair
-    rng = np.random.default_rng(77)
+    rng = np.random.default_rng(77 + K)
     table = random_tables(rng, B, W.geometry.blocks_per_row, W.geometry.physical_blocks)
     ps = [list(map(int, rng.integers(0, W.dims.vocab, size=int(rng.integers(2, 6))))) for _ in range(B)]
     dec, ctl = oracle_controller(W, cpu)
@@ -98,7 +100,7 @@ def test_epoch_k8_random_tables(rt, weights_pair):
     lengths = (positions + 1).astype(np.int32)
     active = np.ones(B, dtype=np.int32)
     control = np.zeros(control_input_elements(B), dtype=np.int32)
-    control[0] = 8
+    control[0] = K
     control[1 : 1 + B] = W.eos
     control[3 + B : 3 + 2 * B] = 10 + np.arange(B)
     slots = np.array([slot_of(table, r, int(positions[r]), BS) for r in range(B)], dtype=np.int32)
@@ -109,7 +111,7 @@ def test_epoch_k8_random_tables(rt, weights_pair):
     assert not tf.mismatches, tf.mismatches
     np.testing.assert_array_equal(hist, ref.history)
     np.testing.assert_array_equal(ctrl_out, ref.control)
-    assert ctrl_out[3] == 0 and ctrl_out[4] == 8
+    assert ctrl_out[3] == 0 and ctrl_out[4] == K
     gk = torch.zeros(rt.cache_bytes // 2, dtype=torch.bfloat16)
     rt.read_state("key_cache", gk)
     assert_close_rel(gk.view_as(ctl.resident_key), ctl.resident_key, rel_tol(W.dims), "resident keys")
