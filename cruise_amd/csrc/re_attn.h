@@ -66,14 +66,29 @@ __device__ __forceinline__ int tile_pos(int t, int w, int i, int r) {
 // lane loads: row chunk c of positions tile_pos(t, w, i, r); -1 where the
 // position is >= neff or its slot is outside the cache.  tabs: the row's
 // block table in LDS.
-template <int D>
+// Block and position within the block of position j >= 0: by division, or
+// (P2: a power-of-two block size, a.bs_shift its log2) by shift and mask.
+template <bool P2>
+__device__ __forceinline__ void block_of(int j, const AttnArgs& a, int& blk, int& in_blk) {
+  if constexpr (P2) {
+    blk = j >> a.bs_shift;
+    in_blk = j & (a.block_size - 1);
+  } else {
+    blk = j / a.block_size;
+    in_blk = j % a.block_size;
+  }
+}
+
+template <int D, bool P2 = false>
 __device__ __forceinline__ void tile_offsets(int (&off)[AttnShape<D>::kLoads], const int* tabs, int t, int w,
                                              int r, int c, int neff, const AttnArgs& a, int g) {
 #pragma unroll
   for (int i = 0; i < AttnShape<D>::kLoads; ++i) {
     const int j = tile_pos<D>(t, w, i, r);
-    const int blk = min(j / a.block_size, a.blocks_per_row - 1);
-    const long long slot = (long long)tabs[blk] * a.block_size + (j % a.block_size);
+    int bq, jb;
+    block_of<P2>(j, a, bq, jb);
+    const int blk = min(bq, a.blocks_per_row - 1);
+    const long long slot = (long long)tabs[blk] * a.block_size + jb;
     const bool ok = j < neff && slot >= 0 && slot < a.slots;
     off[i] = ok ? static_cast<int>((slot * a.kv_heads + g) * D + c * 8) : -1;
   }
@@ -307,7 +322,8 @@ __device__ __forceinline__ void attn_body_lean(const AttnArgs& a, int block, uns
 
 // The attention of one (batch row, query head): block = group + groups *
 // head_in_group.  smem: dynamic LDS (attention_lds_bytes), red: 4 floats.
-template <typename T, int D>
+// P2: the block size is a power of two (a.bs_shift).
+template <typename T, int D, bool P2 = false>
 __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned char* smem_raw, float* red,
                                           int tid) {
   using S = AttnShape<D>;
@@ -339,7 +355,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
   lds_barrier();
   if (stop != 0) return;  // uniform over the workgroup
   int off[S::kLoads];
-  tile_offsets<D>(off, tabs, 0, w, r, c, neff, a, g);
+  tile_offsets<D, P2>(off, tabs, 0, w, r, c, neff, a, g);
   Vec8<T> kr[S::kLoads], vr[S::kLoads];
   load_tile<T, D>(kr, KC, off, c);
   load_tile<T, D>(vr, VC, off, c);
@@ -349,7 +365,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
   float smax = -INFINITY;
   for (int t = 0; t < ntiles; ++t) {
     if (t > 0) {
-      tile_offsets<D>(off, tabs, t, w, r, c, neff, a, g);
+      tile_offsets<D, P2>(off, tabs, t, w, r, c, neff, a, g);
       load_tile<T, D>(kr, KC, off, c);
     }
     // a missing row (slot outside the cache) is a zero key: score 0
@@ -381,10 +397,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   for (int t = 0; t < ntiles; ++t) {
     if (t > 0) {
-      tile_offsets<D>(off, tabs, t, w, r, c, neff, a, g);
+      tile_offsets<D, P2>(off, tabs, t, w, r, c, neff, a, g);
       load_tile<T, D>(vr, VC, off, c);
     } else if (ntiles > 1) {
-      tile_offsets<D>(off, tabs, 0, w, r, c, neff, a, g);  // the score loop moved on
+      tile_offsets<D, P2>(off, tabs, 0, w, r, c, neff, a, g);  // the score loop moved on
     }
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {

@@ -5,20 +5,25 @@
 namespace re {
 namespace {
 
-template <typename T, int D>
+template <typename T, int D, bool P2>
 __global__ void __launch_bounds__(kAttnThreads) k_attn(AttnArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __shared__ float red[kAttnThreads / 64];
-  attn_body<T, D>(a, blockIdx.x, smem_raw, red, threadIdx.x);
+  attn_body<T, D, P2>(a, blockIdx.x, smem_raw, red, threadIdx.x);
 }
 
 size_t smem_bytes(int window, int blocks_per_row) {
   return (size_t)window * sizeof(float) + (size_t)kAttnThreads * 8 * sizeof(float) + (size_t)blocks_per_row * sizeof(int);
 }
 
+// Power-of-two block sizes take the shift-and-mask position arithmetic.
 template <typename T, int D>
 hipError_t launch_t(const AttnArgs& a, hipStream_t stream) {
-  k_attn<T, D><<<a.B * a.heads, kAttnThreads, smem_bytes(a.window, a.blocks_per_row), stream>>>(a);
+  const size_t smem = smem_bytes(a.window, a.blocks_per_row);
+  if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size)
+    k_attn<T, D, true><<<a.B * a.heads, kAttnThreads, smem, stream>>>(a);
+  else
+    k_attn<T, D, false><<<a.B * a.heads, kAttnThreads, smem, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -26,8 +31,11 @@ hipError_t launch_t(const AttnArgs& a, hipStream_t stream) {
 // with the capacity); the static reduction scratch comes on top of it.
 template <typename T, int D>
 hipError_t allow_t(size_t bytes) {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn<T, D>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                             static_cast<int>(bytes));
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn<T, D, false>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn<T, D, true>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
 }
 
 }  // namespace

@@ -154,6 +154,7 @@ struct AttnArgs {
   void* out;               // T [B, NH*d]
   int B, heads, kv_heads, head_dim, block_size, blocks_per_row, window;
   long long slots;
+  int bs_shift;            // log2(block_size) when it is a power of two, else -1
 };
 size_t attention_lds_bytes(const Dims& d);
 hipError_t prepare_attention(const Dims& d);
