@@ -48,8 +48,13 @@ __device__ __forceinline__ void group_reduce_transpose(float (&v)[N], int c) {
     const bool upper = (c & mask) != 0;
 #pragma unroll
     for (int i = 0; i < h; ++i) {
-      const float send = upper ? v[i] : v[i + h];
-      const float keep = upper ? v[i + h] : v[i];
+      // Opaque copies keep the selects on registers: a select between two
+      // elements of v is otherwise folded into a read of v at a runtime
+      // index, which lowers to a compare-and-select chain over all of v.
+      float lo = v[i], hi = v[i + h];
+      asm("" : "+v"(lo), "+v"(hi));
+      const float send = upper ? lo : hi;
+      const float keep = upper ? hi : lo;
       v[i] = keep + __shfl_xor(send, mask, 64);
     }
     mask >>= 1;
@@ -142,8 +147,13 @@ __device__ __forceinline__ void group_reduce_partial(float (&v)[N], int c) {
     const bool upper = (c & mask) != 0;
 #pragma unroll
     for (int i = 0; i < h; ++i) {
-      const float send = upper ? v[i] : v[i + h];
-      const float keep = upper ? v[i + h] : v[i];
+      // Opaque copies keep the selects on registers: a select between two
+      // elements of v is otherwise folded into a read of v at a runtime
+      // index, which lowers to a compare-and-select chain over all of v.
+      float lo = v[i], hi = v[i + h];
+      asm("" : "+v"(lo), "+v"(hi));
+      const float send = upper ? lo : hi;
+      const float keep = upper ? hi : lo;
       v[i] = keep + __shfl_xor(send, mask, 64);
     }
     mask >>= 1;
