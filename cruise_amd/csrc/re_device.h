@@ -166,8 +166,13 @@ __device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
     const bool upper = (lane & mask) != 0;
 #pragma unroll
     for (int i = 0; i < h; ++i) {
-      float send = upper ? v[i] : v[i + h];
-      float keep = upper ? v[i + h] : v[i];
+      // Opaque copies keep the selects on registers: a select between two
+      // elements of v is otherwise folded into a read of v at a runtime
+      // index, which lowers to a compare-and-select chain over all of v.
+      float lo = v[i], hi = v[i + h];
+      asm("" : "+v"(lo), "+v"(hi));
+      float send = upper ? lo : hi;
+      float keep = upper ? hi : lo;
       float recv = __shfl_xor(send, mask, 64);
       v[i] = keep + recv;
     }
