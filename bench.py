@@ -12,16 +12,14 @@ A benchmark "step" is one K=8 epoch.  ``value`` is decoded tokens per second
 (sum of executed steps over all rows / wall time of the timed epochs, inputs
 resident in HBM; each epoch is one graph launch).
 
-``roofline`` reports the dominant kernel.  With the persistent step kernel
-(``--fused``) that is the kernel itself: one launch runs the 28
-layers and the LM head of a decoder step, so its algorithmic bytes are the
-step's streamed weights (14,141,238,272 B) and its launch duration is timed
-with HIP events on the engine's stream around the last step of each of
-``--kernel-epochs`` further epochs (the rest of each epoch runs as graphs
-before and after it).  With the per-op path (the default) it is the gate/up
-projection (54% of the streamed bytes), timed over ``--kernel-iters``
-back-to-back launches.  ``cpu_baseline`` times the oracle's CPU decoder step
-on the host cores.
+``roofline`` reports the dominant kernel, the gate/up projection (54% of the
+streamed bytes).  Its launch duration is timed inside the epoch: for
+``--kernel-epochs`` further epochs the engine launches the middle layer's
+gate/up of each epoch's last step between two HIP events on its own stream,
+with the rest of the epoch as captured graphs before and after it, so the
+launch follows the previous layers' traffic exactly as in the graph (cold
+weights, no back-to-back re-reads).  ``cpu_baseline`` times the oracle's CPU
+decoder on the host cores over K=8 epochs of the same workload.
 """
 from __future__ import annotations
 
@@ -48,9 +46,7 @@ def parse_args():
     p.add_argument("--seed", type=int, default=20263)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-steps", type=int, default=48)
-    p.add_argument("--kernel-iters", type=int, default=50)
     p.add_argument("--kernel-epochs", type=int, default=10)
-    p.add_argument("--fused", action="store_true", help="run each decoder step as the persistent step kernel")
     return p.parse_args()
 
 
@@ -74,7 +70,7 @@ def main() -> int:
     cfg = EngineConfig(
         model=ModelSpec(),
         engine=EngineSpec(
-            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=256, fused_step=args.fused
+            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=256
         ),
         weights=WeightSpec(source="synthetic", seed=args.seed, std=0.02),
     )
@@ -141,39 +137,33 @@ def main() -> int:
         run_epoch(True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
+    # copies of one timed epoch, counted from its captured graph's nodes
+    copies = {k: rt.info(f"epoch_{k}_copies") for k in ("h2d", "d2h", "other")}
     tok_s = executed_total / elapsed
     ms_per_epoch = elapsed * 1e3 / args.steps
     streamed = rt.info("streamed_weight_bytes")
     decoder_steps = executed_total / B
     ms_per_decoder_step = elapsed * 1e3 / decoder_steps
     step_gbs = streamed / (ms_per_decoder_step * 1e-3) / 1e9
-    fused = rt.info("fused_step") == 1
-    if fused:
-        # The persistent step kernel of each epoch's last step, between HIP
-        # events on the engine's stream (untimed epochs after the timed ones).
-        rt.enable_kernel_timing(True)
-        for _ in range(args.kernel_epochs):
-            run_epoch(False)
-        torch.cuda.synchronize()
-        launches = rt.timed_launch_ms()
-        rt.enable_kernel_timing(False)
-        if not launches:
-            raise RuntimeError("no timed launch of the step kernel completed")
-        k_avg_ms = statistics.mean(launches)
-        k_bytes = streamed
-        k_name = f"persistent decoder-step kernel k_step_fused ({rt.info('fused_grid')} workgroups; 28 layers + LM head per launch)"
-    else:
-        # gate/up of the middle layer, timed on the engine's stream (HIP events)
-        gu_op = rt.op_index(rt.info("timing_layer"), "gate_up")
-        k_avg_ms = rt.time_ops(gu_op, gu_op + 1, args.kernel_iters)
-        inter = rt.info("intermediate")
-        hidden = rt.info("hidden")
-        k_bytes = 2 * inter * hidden * 2 + hidden * 2 + B * hidden * 2 + B * inter * 2
-        k_name = "gate/up projection (k_proj<bf16,4,4,GateUp>)"
+    # gate/up of the middle layer in each epoch's last step, between HIP
+    # events on the engine's stream (untimed epochs after the timed ones)
+    rt.enable_kernel_timing(True)
+    for _ in range(args.kernel_epochs):
+        run_epoch(False)
+    torch.cuda.synchronize()
+    launches = rt.timed_launch_ms()
+    rt.enable_kernel_timing(False)
+    if not launches:
+        raise RuntimeError("no timed gate/up launch completed")
+    k_avg_ms = statistics.mean(launches)
+    inter = rt.info("intermediate")
+    hidden = rt.info("hidden")
+    k_bytes = 2 * inter * hidden * 2 + hidden * 2 + B * hidden * 2 + B * inter * 2
+    k_name = "gate/up projection (k_proj<bf16,4,4,GateUp>), in-epoch launch"
     k_gbs = k_bytes / (k_avg_ms * 1e-3) / 1e9
     log(
         f"{tok_s:.1f} tok/s, {ms_per_decoder_step:.3f} ms/decoder step, {step_gbs:.0f} GB/s step, "
-        f"{'step kernel' if fused else 'gate/up'} {k_avg_ms * 1e3:.1f} us ({k_gbs:.0f} GB/s)"
+        f"gate/up {k_avg_ms * 1e3:.1f} us ({k_gbs:.0f} GB/s)"
     )
 
     cpu = None
@@ -206,8 +196,9 @@ def main() -> int:
         "step_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "host_control_wall_ms_p50": round(statistics.median(host_ms), 4),
         "native_wall_us_p50": int(statistics.median(walls)),
-        "h2d_copies_per_epoch": 1,
-        "d2h_copies_per_epoch": 1,
+        "h2d_copies_per_epoch": copies["h2d"],
+        "d2h_copies_per_epoch": copies["d2h"],
+        "other_copies_per_epoch": copies["other"],
         "roofline": {
             "bound": "hbm",
             "kernel": k_name,
@@ -215,7 +206,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes(fused),
+            "traffic": traffic_bytes(),
             "avg_launch_us": round(k_avg_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": k_bytes,
         },
@@ -225,12 +216,11 @@ def main() -> int:
     return 0
 
 
-def traffic_bytes(fused: bool):
+def traffic_bytes():
     """HBM bytes per launch of the reported kernel from the committed
     rocprofv3 PMC passes (FETCH_SIZE and WRITE_SIZE, each scaled by what the
     counter reads for a plain copy of known size), or None without them."""
-    name = "step_kernel_qwen7b_b4_traffic.json" if fused else "gate_up_qwen7b_b4_traffic.json"
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_qwen7b_b4_traffic.json")
     try:
         with open(path) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])

@@ -133,203 +133,6 @@ __device__ __forceinline__ float attn_block_sum(float v, float* red, int tid) {
   return s;
 }
 
-// Halving exchange of N values over the M >= N lanes of a group (lane offset
-// c = lane % M): afterwards lanes c with c % (M/N) == 0 hold the total of
-// value c / (M/N).  The lane pairs are those of group_reduce_transpose<M>
-// (masks M/2, ..., 1), so a total is bit-identical to the one that
-// reduction forms.
-template <int N, int M>
-__device__ __forceinline__ void group_reduce_partial(float (&v)[N], int c) {
-  int mask = M >> 1;
-#pragma unroll
-  for (int n = N; n > 1; n >>= 1) {
-    const int h = n >> 1;
-    const bool upper = (c & mask) != 0;
-#pragma unroll
-    for (int i = 0; i < h; ++i) {
-      // Opaque copies keep the selects on registers: a select between two
-      // elements of v is otherwise folded into a read of v at a runtime
-      // index, which lowers to a compare-and-select chain over all of v.
-      float lo = v[i], hi = v[i + h];
-      asm("" : "+v"(lo), "+v"(hi));
-      const float send = upper ? lo : hi;
-      const float keep = upper ? hi : lo;
-      v[i] = keep + __shfl_xor(send, mask, 64);
-    }
-    mask >>= 1;
-  }
-#pragma unroll
-  for (; mask >= 1; mask >>= 1) v[0] += __shfl_xor(v[0], mask, 64);
-}
-
-// Offsets of the loads [i0, i0 + n) of one tile (tile_offsets restricted to
-// a range of its loads).
-template <int D, int N>
-__device__ __forceinline__ void tile_offsets_part(int (&off)[N], int i0, const int* tabs, int t, int w, int r, int c,
-                                                  int neff, const AttnArgs& a, int g) {
-#pragma unroll
-  for (int k = 0; k < N; ++k) {
-    const int j = tile_pos<D>(t, w, i0 + k, r);
-    const int blk = min(j / a.block_size, a.blocks_per_row - 1);
-    const long long slot = (long long)tabs[blk] * a.block_size + (j % a.block_size);
-    const bool ok = j < neff && slot >= 0 && slot < a.slots;
-    off[k] = ok ? static_cast<int>((slot * a.kv_heads + g) * D + c * 8) : -1;
-  }
-}
-
-template <typename T, int N>
-__device__ __forceinline__ void load_part(Vec8<T> (&v)[N], const T* cache, const int (&off)[N], int c) {
-#pragma unroll
-  for (int k = 0; k < N; ++k) {
-    const int e = off[k] >= 0 ? off[k] : c * 8;
-    v[k] = Vec8<T>::load_cached(cache + e);
-  }
-}
-
-// Scores of loads [i0, i0 + N) of tile t into sc; returns the running max.
-// The L lanes of a row group sum their partial products through LDS (dots:
-// this wave's [kRg][N][L] floats) instead of a shuffle tree, which would hold
-// every partial in registers: lane c < N adds the L partials of its load in
-// the pairing order of group_reduce_transpose<L> (lanes l and l+L/2 first,
-// then l+L/4, ...), so the score is bit-identical to attn_body's.
-template <typename T, int D, int N>
-__device__ __forceinline__ float lean_scores(const Vec8<T> (&kv)[N], const int (&off)[N], const Vec8<T>& qv, int i0,
-                                             int t, int w, int r, int c, int neff, bool uniform, float* sc,
-                                             float* dots, float smax) {
-  constexpr int L = AttnShape<D>::kLpr;
-  float* mine = dots + r * N * L;
-#pragma unroll
-  for (int k = 0; k < N; ++k) mine[k * L + c] = off[k] >= 0 ? dot8(kv[k], qv, 0.f) : 0.f;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-  if (c < N) {
-    float v[L];
-#pragma unroll
-    for (int l = 0; l < L; ++l) v[l] = mine[c * L + l];
-#pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1)
-#pragma unroll
-      for (int l = 0; l < m; ++l) v[l] = v[l] + v[l + m];
-    const int j = tile_pos<D>(t, w, i0 + c, r);
-    float sv = v[0];
-    if constexpr (sizeof(T) == 2) sv = round_bf16(sv);  // ExactQk output is bf16
-    sv = round_bf16(sv / sqrtf(static_cast<float>(D)));
-    if (uniform) sv = -3.38953139e38f;  // every position masked to bf16 min
-    if (j < neff) {
-      sc[j] = sv;
-      smax = fmaxf(smax, sv);
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();  // the next half rewrites this wave's region
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-  return smax;
-}
-
-// The attention of one (batch row, query head) inside the persistent step
-// kernel, with attn_body's arithmetic, its work layout and its reduction
-// trees (so the results are bit-identical), in half the registers: each
-// tile's loads go out as two halves of kLoads/2 rows per lane, the key
-// halves together and the value halves together after the softmax, so the
-// keys and the values take one round trip each per tile.  q and the caches are read with ordinary
-// loads at offsets carrying z (zero, read after the dependency wait): every
-// line they touch was last written before this launch or by a coherent store
-// of the qkv phase that signalled before the wait, and none was cached by
-// this workgroup's L2 in between.  The output goes out through CoBuf.
-template <typename T, int D>
-__device__ __forceinline__ void attn_body_lean(const AttnArgs& a, int block, unsigned char* smem_raw, float* red,
-                                               uint32_t z, int tid) {
-  using S = AttnShape<D>;
-  constexpr int L = S::kLpr;
-  constexpr int NH = S::kLoads / 2;
-  const int W = a.window;
-  float* sc = reinterpret_cast<float*>(smem_raw);  // [W] scores, then probabilities
-  float* part = sc + W;                            // [4 waves][64 lanes][8] P.V partials
-  const int G = a.heads / a.kv_heads;
-  const int groups = a.B * a.kv_heads;
-  const int grp = block % groups, hi = block / groups;
-  const int b = grp / a.kv_heads, g = grp - b * a.kv_heads;
-  const int h = g * G + hi;
-  const int lane = tid & 63, w = wave_index(tid);
-  const int r = lane / L, c = lane % L;
-  const int n = a.len[b];
-  const bool uniform = n <= 0;
-  const int neff = uniform ? W : min(n, W);
-  const int ntiles = (neff + kAttnTile - 1) / kAttnTile;
-  const T* KC = static_cast<const T*>(a.key_cache) + z;
-  const T* VC = static_cast<const T*>(a.value_cache) + z;
-  const int32_t* tab = a.table + (size_t)b * a.blocks_per_row;
-  int* tabs = reinterpret_cast<int*>(part + kAttnThreads * 8);  // [blocks_per_row]
-  for (int e = tid; e < a.blocks_per_row; e += kAttnThreads) tabs[e] = tab[e];
-  const size_t q_elem = ((size_t)b * a.heads + h) * D + c * 8;
-  const Vec8<T> qv = Vec8<T>::load_cached(static_cast<const T*>(a.q) + q_elem + z);
-  lds_barrier();
-
-  // partial products of the scores: this wave's [kRg][NH][L] floats of the
-  // P.V partial region, which is free until the end
-  float* dots = part + w * S::kRg * NH * L;
-  int off0[NH], off1[NH];
-  Vec8<T> x0[NH], x1[NH];
-  float smax = -INFINITY;
-  for (int t = 0; t < ntiles; ++t) {
-    tile_offsets_part<D, NH>(off0, 0, tabs, t, w, r, c, neff, a, g);
-    tile_offsets_part<D, NH>(off1, NH, tabs, t, w, r, c, neff, a, g);
-    load_part<T, NH>(x0, KC, off0, c);
-    load_part<T, NH>(x1, KC, off1, c);
-    smax = lean_scores<T, D, NH>(x0, off0, qv, 0, t, w, r, c, neff, uniform, sc, dots, smax);
-    smax = lean_scores<T, D, NH>(x1, off1, qv, NH, t, w, r, c, neff, uniform, sc, dots, smax);
-  }
-  const float mx = attn_block_max(smax, red, tid);
-  float esum = 0.f;
-  for (int j = tid; j < neff; j += kAttnThreads) esum += expf(sc[j] - mx);
-  const float inv = 1.0f / attn_block_sum(esum, red, tid);
-  for (int j = tid; j < neff; j += kAttnThreads) sc[j] = round_bf16(expf(sc[j] - mx) * inv);
-  __syncthreads();
-
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int t = 0; t < ntiles; ++t) {
-    {
-      tile_offsets_part<D, NH>(off0, 0, tabs, t, w, r, c, neff, a, g);
-      tile_offsets_part<D, NH>(off1, NH, tabs, t, w, r, c, neff, a, g);
-      load_part<T, NH>(x0, VC, off0, c);
-      load_part<T, NH>(x1, VC, off1, c);
-    }
-#pragma unroll
-    for (int k = 0; k < NH; ++k) {
-      const float p = off0[k] >= 0 ? sc[tile_pos<D>(t, w, k, r)] : 0.f;
-      const Vec8<T> v = off0[k] >= 0 ? x0[k] : Vec8<T>{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, v.get(e), acc[e]);
-    }
-#pragma unroll
-    for (int k = 0; k < NH; ++k) {
-      const float p = off1[k] >= 0 ? sc[tile_pos<D>(t, w, NH + k, r)] : 0.f;
-      const Vec8<T> v = off1[k] >= 0 ? x1[k] : Vec8<T>{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, v.get(e), acc[e]);
-    }
-  }
-  // Combine the 64/L row groups of each wave and the 4 waves, in a fixed order.
-#pragma unroll
-  for (int e = 0; e < 8; ++e) part[(w * 64 + lane) * 8 + e] = acc[e];
-  __syncthreads();
-  if (tid < D) {
-    const int cc = tid / 8, e = tid % 8;
-    float o = 0.f;
-    for (int ww = 0; ww < kAttnThreads / 64; ++ww)
-      for (int rr = 0; rr < S::kRg; ++rr) o += part[(ww * 64 + rr * L + cc) * 8 + e];
-    const size_t o_elem = ((size_t)b * a.heads + h) * D + tid;
-    const CoBuf ob = CoBuf::make(a.out, static_cast<uint32_t>((size_t)a.B * a.heads * D * sizeof(T)));
-    if constexpr (sizeof(T) == 2)
-      ob.store2(static_cast<uint32_t>(o_elem * 2), Elt<T>::t(o));
-    else
-      ob.store4(static_cast<uint32_t>(o_elem * 4), __float_as_uint(o));
-  }
-}
-
 // The attention of one (batch row, query head): block = group + groups *
 // head_in_group.  smem: dynamic LDS (attention_lds_bytes), red: 4 floats.
 // P2: the block size is a power of two (a.bs_shift).

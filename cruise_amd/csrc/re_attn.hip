@@ -1,5 +1,4 @@
-// Paged decode attention launches (the body lives in re_attn.h, shared with
-// the persistent step kernel).
+// Paged decode attention launches (the body lives in re_attn.h).
 #include "re_attn.h"
 
 namespace re {

@@ -21,7 +21,6 @@ struct CtrlArgs {
   const float* am_val;
   const int32_t* am_idx;
   const int32_t* am_bad;
-  const int32_t* model_abort;  // persistent step kernel's abort flag (nullptr: per-op path)
   int has_payload;
 };
 
@@ -102,7 +101,8 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
   s.misc[2] = graph_variant;
   s.misc[3] = flagged ? 1 : 0;
   s.misc[4] = import_mask;
-  s.misc[5] = 0;  // 1 once the import is applied (copy + checksum run)
+  s.misc[5] = 0;  // 1 once the import is complete (every masked row adopted)
+  s.misc[6] = 0;  // 1 once at least one masked row is adopted (its copy runs)
   *s.model_calls = 0;
   *s.status = kStatusOk;
   *s.done = 0;
@@ -174,6 +174,7 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
       if ((import_mask & (1 << r)) == 0) continue;
       if (f.active[r] != 1 || s.generation[r] <= 0) { status = kStatusInvalidMetadata; break; }
       s.clear_row[r] = 2;  // clear, then import block 0 of the row
+      s.misc[6] = 1;
       s.res_gen[r] = s.generation[r];
       s.res_token[r] = f.token[r];
       s.res_pos[r] = f.pos[r];
@@ -198,12 +199,14 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
     }
   }
   if (status != kStatusOk) {
-    // An import applied before the continuity check stays applied (its
-    // copy and checksum still run, CTRL:387-446 precede 448-471); the
+    // Rows the import loop adopted before the fallback stay adopted with
+    // their blocks copied, as CTRL:402-428 copies each row before it checks
+    // the next one.  The checksum runs only for a complete import (misc[5]):
+    // CTRL:430-445 is reached only after the whole mask.  The
     // new-generation clears are dropped.
     for (int r = 0; r < B; ++r) {
       s.reason[r] = kFinishFallback;
-      if (s.misc[5] == 0 || s.clear_row[r] != 2) s.clear_row[r] = 0;
+      if (s.misc[6] == 0 || s.clear_row[r] != 2) s.clear_row[r] = 0;
     }
     *s.status = status;
     *s.done = 1;
@@ -314,13 +317,6 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   const int call = ++(*s.model_calls);
   int64_t* history = reinterpret_cast<int64_t*>(s.fetch);
   int32_t status = kStatusOk;
-  // A step kernel that could not complete is a failed model call (CTRL:494-497).
-  if (a.model_abort != nullptr && *a.model_abort != 0) {
-    for (int r = 0; r < B; ++r) s.reason[r] = kFinishFallback;
-    *s.status = kStatusModelError;
-    *s.done = 1;
-    return;
-  }
   // next_position = where(active, pos + 1, pos) (batched_decoder_step.py:409-411)
   for (int r = 0; r < B; ++r) {
     const int64_t next_pos = s.cur_active[r] != 0 ? s.cur_pos[r] + 1 : s.cur_pos[r];
@@ -532,7 +528,6 @@ static CtrlArgs ctrl_args(const KernelEnv& env, const StatePtrs& st) {
   a.am_val = env.scratch.am_val;
   a.am_idx = env.scratch.am_idx;
   a.am_bad = env.scratch.am_bad;
-  a.model_abort = env.plan.fused ? env.scratch.sync : nullptr;
   return a;
 }
 

@@ -191,58 +191,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// ---------------------------------------------------------------------------
-// Device-coherent access for data that workgroups of one launch hand to each
-// other.  The eight XCDs of the chip have separate L2 caches; an ordinary
-// load may hit a line that another XCD has since rewritten.  Buffer accesses
-// with the sc1 cache-policy bit are served at the device-coherence point
-// (the same accesses the compiler emits for relaxed agent-scope atomics), so
-// a store acknowledged to its writer (s_waitcnt vmcnt(0)) is seen by every
-// later sc1 load, without the agent-scope L2 write-back and invalidate that
-// an acquire/release fence would cost.  The base is wave-uniform; offsets
-// are bytes; accesses at or past `bytes` read zero and write nothing.
-// ---------------------------------------------------------------------------
-constexpr int kCoherent = 16;  // sc1 bit of the buffer instructions' cache policy
-
-struct CoBuf {
-  __amdgpu_buffer_rsrc_t r;
-  __device__ __forceinline__ static CoBuf make(const void* base, uint32_t bytes) {
-    CoBuf b;
-    b.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                            static_cast<int>(bytes), 0x00020000);
-    return b;
-  }
-  __device__ __forceinline__ re_u32x4 load16(uint32_t off) const {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kCoherent);
-  }
-  __device__ __forceinline__ uint32_t load4(uint32_t off) const {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, kCoherent);
-  }
-  __device__ __forceinline__ void store2(uint32_t off, uint16_t v) const {
-    __builtin_amdgcn_raw_buffer_store_b16(v, r, static_cast<int>(off), 0, kCoherent);
-  }
-  __device__ __forceinline__ void store4(uint32_t off, uint32_t v) const {
-    __builtin_amdgcn_raw_buffer_store_b32(v, r, static_cast<int>(off), 0, kCoherent);
-  }
-};
-
-// Eight consecutive elements through CoBuf.
-template <typename T>
-__device__ __forceinline__ Vec8<T> co_load_vec8(const CoBuf& buf, uint32_t byte_off);
-template <>
-__device__ __forceinline__ Vec8<bf16_t> co_load_vec8<bf16_t>(const CoBuf& buf, uint32_t byte_off) {
-  Vec8<bf16_t> r;
-  r.v = buf.load16(byte_off);
-  return r;
-}
-template <>
-__device__ __forceinline__ Vec8<float> co_load_vec8<float>(const CoBuf& buf, uint32_t byte_off) {
-  Vec8<float> r;
-  r.a = __builtin_bit_cast(re_f32x4, buf.load16(byte_off));
-  r.b = __builtin_bit_cast(re_f32x4, buf.load16(byte_off + 16));
-  return r;
-}
-
 // The same (wave-uniform) pointer, marked as global memory, so loads and
 // stores through it compile to global_* instead of flat_* instructions (a
 // flat access also counts against lgkmcnt, so every LDS wait would wait for

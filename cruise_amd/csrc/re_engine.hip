@@ -29,6 +29,7 @@
 namespace re {
 namespace {
 
+constexpr int kBridgeRows = 4;  // rows of the bridge call's host arrays
 constexpr int kCreateOk = 0, kCreateArgs = 1, kCreateTiling = 2, kCreateConfig = 3, kCreateGraph = 4,
               kCreateWeights = 5, kCreateRuntime = 6, kCreateDevice = 7;
 
@@ -115,6 +116,10 @@ struct Engine {
   // the halves around the timed launch)
   std::map<int, hipGraphExec_t> graphs;
   std::map<int, hipGraph_t> graph_defs;
+  // Copies each captured graph holds, read back from its nodes: {host to
+  // device, device to host, other}; and the sums over the last epoch launched.
+  std::map<int, std::array<int, 3>> graph_copies;
+  std::array<int, 3> last_epoch_copies{{-1, -1, -1}};
   // Kernel timing: the gate/up launch of layer timing_layer in an epoch's last
   // step runs between two HIP events on the engine stream, outside the graphs.
   bool timing = false;
@@ -123,7 +128,6 @@ struct Engine {
   std::vector<float> timing_ms;
 
   std::mutex execute_mutex;
-  bool trace_step = false;  // "engine": {"trace_step": true}: persistent kernel phase trace
 
   KernelEnv env() const {
     KernelEnv e{};
@@ -258,18 +262,6 @@ bool make_plan(Engine& e, const Json& cfg) {
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
   }
-  // The persistent step kernel serves the shapes it is written for when the
-  // configuration asks for it ("engine": {"fused_step": true}).
-  const Json* eng = cfg.get("engine");
-  e.trace_step = eng != nullptr && eng->bool_or("trace_step", false);
-  p.fused = 0;
-  p.fused_grid = 0;
-  if (eng != nullptr && eng->bool_or("fused_step", false) && fused_step_eligible(d)) {
-    p.fused_grid = fused_grid(d, e.cus);
-    if (const Json* t = cfg.get("tuning")) p.fused_grid = static_cast<int>(t->number_or("fused_grid", p.fused_grid));
-    p.fused = fused_grid_valid(d, p.fused_grid, e.cus) ? 1 : 0;
-    if (p.fused) p.lm_wg = p.fused_grid;
-  }
   p.o_grid = (d.hidden / 2 + p.waves - 1) / p.waves;
   p.down_grid = p.o_grid;
   p.o_segments = (d.q_dim() + k_segment_elems() - 1) / k_segment_elems();
@@ -393,10 +385,6 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},
-      {reinterpret_cast<void**>(&e.scratch.sync), (size_t)fused_sync_ints(d) * sizeof(int32_t)},
-      {&e.scratch.fused_layers, fused_layer_table_bytes(d)},
-      {reinterpret_cast<void**>(&e.scratch.step_trace), e.trace_step ? fused_trace_bytes(d, p.fused_grid) : 0},
-      {&e.scratch.fused_act, p.fused ? fused_act_bytes(d) : 0},
   };
   off = 0;
   offs.clear();
@@ -407,7 +395,6 @@ bool alloc_state(Engine& e) {
   if (hipMalloc(&e.scratch_mem, off) != hipSuccess) return false;
   if (hipMemset(e.scratch_mem, 0, off) != hipSuccess) return false;
   for (size_t i = 0; i < sp.size(); ++i) *sp[i].p = e.scratch_mem + offs[i];
-  if (!e.trace_step) e.scratch.step_trace = nullptr;
   e.st.import_sum = e.checksum_dev;
 
   // decoder-step ABI inputs
@@ -567,8 +554,49 @@ hipError_t record_epoch(Engine& e, int K, FeedMode mode, int part) {
   return hipMemcpyAsync(e.h_fetch, e.st.fetch, e.fetch_bytes, hipMemcpyDeviceToHost, e.stream);
 }
 
+int graph_key(int K, FeedMode mode, int part) { return (K * 3 + mode) * 4 + part; }
+
+// Where a pointer lives: true for device memory.
+bool is_device_ptr(const void* p) {
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;  // unregistered pageable host memory
+  }
+  return attr.type == hipMemoryTypeDevice;
+}
+
+// The memory copies a captured graph holds, by direction, read from its
+// nodes: {host to device, device to host, other}.
+std::array<int, 3> count_copies(hipGraph_t graph) {
+  std::array<int, 3> c{{0, 0, 0}};
+  size_t n = 0;
+  if (hipGraphGetNodes(graph, nullptr, &n) != hipSuccess) return {{-1, -1, -1}};
+  std::vector<hipGraphNode_t> nodes(n);
+  if (n > 0 && hipGraphGetNodes(graph, nodes.data(), &n) != hipSuccess) return {{-1, -1, -1}};
+  for (hipGraphNode_t node : nodes) {
+    hipGraphNodeType type{};
+    if (hipGraphNodeGetType(node, &type) != hipSuccess) return {{-1, -1, -1}};
+    if (type == hipGraphNodeTypeMemset) {
+      ++c[2];
+      continue;
+    }
+    if (type != hipGraphNodeTypeMemcpy) continue;
+    hipMemcpy3DParms p{};
+    if (hipGraphMemcpyNodeGetParams(node, &p) != hipSuccess) return {{-1, -1, -1}};
+    const bool src_dev = is_device_ptr(p.srcPtr.ptr), dst_dev = is_device_ptr(p.dstPtr.ptr);
+    if (!src_dev && dst_dev)
+      ++c[0];
+    else if (src_dev && !dst_dev)
+      ++c[1];
+    else
+      ++c[2];
+  }
+  return c;
+}
+
 hipGraphExec_t epoch_graph(Engine& e, int K, FeedMode mode, int part) {
-  const int key = (K * 3 + mode) * 4 + part;
+  const int key = graph_key(K, mode, part);
   auto it = e.graphs.find(key);
   if (it != e.graphs.end()) return it->second;
   hipGraph_t graph = nullptr;
@@ -586,6 +614,7 @@ hipGraphExec_t epoch_graph(Engine& e, int K, FeedMode mode, int part) {
   }
   e.graphs[key] = exec;
   e.graph_defs[key] = graph;
+  e.graph_copies[key] = count_copies(graph);
   return exec;
 }
 
@@ -777,11 +806,16 @@ bool prepare_device_import(Engine& e, const ResidentEpochIpcMetadata* m, const i
 bool run_graph(Engine& e, int K, FeedMode mode) {
   if (!e.timing) {
     hipGraphExec_t g = epoch_graph(e, K, mode, 0);
-    return g != nullptr && hipGraphLaunch(g, e.stream) == hipSuccess;
+    if (g == nullptr) return false;
+    e.last_epoch_copies = e.graph_copies[graph_key(K, mode, 0)];
+    return hipGraphLaunch(g, e.stream) == hipSuccess;
   }
   hipGraphExec_t pre = epoch_graph(e, K, mode, 1);
   hipGraphExec_t post = epoch_graph(e, K, mode, 2);
   if (pre == nullptr || post == nullptr) return false;
+  const std::array<int, 3>& c1 = e.graph_copies[graph_key(K, mode, 1)];
+  const std::array<int, 3>& c2 = e.graph_copies[graph_key(K, mode, 2)];
+  for (int i = 0; i < 3; ++i) e.last_epoch_copies[i] = c1[i] + c2[i];
   const int op = timed_op_index(e.env(), e.timing_layer);
   return hipGraphLaunch(pre, e.stream) == hipSuccess && hipEventRecord(e.ev_start, e.stream) == hipSuccess &&
          launch_step_ops(e.env(), epoch_step_ptrs(e), e.stream, op, op + 1) == hipSuccess &&
@@ -812,13 +846,15 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
   if (g_engine_active || air_path == nullptr || graph_config == nullptr || func_config == nullptr ||
       external_weight_dir == nullptr)
     return nullptr;
+  // Check order of resident_epoch_bridge.cpp:364-375: arguments and the
+  // /dev/shm weight directory (1), then the tiling file (2), then the graph
+  // configuration (3).  The configuration may lift the /dev/shm rule
+  // ("engine": {"require_dev_shm": false}); an unreadable one keeps it.
   std::string cfg_text;
   Json cfg;
-  if (!read_file(graph_config, cfg_text) || !JsonParser(cfg_text).parse(cfg) || cfg.kind != Json::kObject) {
-    *status = kCreateConfig;
-    return nullptr;
-  }
-  const Json* eng = cfg.get("engine");
+  const bool cfg_ok =
+      read_file(graph_config, cfg_text) && JsonParser(cfg_text).parse(cfg) && cfg.kind == Json::kObject;
+  const Json* eng = cfg_ok ? cfg.get("engine") : nullptr;
   const bool require_shm = eng ? eng->bool_or("require_dev_shm", true) : true;
   if (require_shm && std::strncmp(external_weight_dir, "/dev/shm/", 9) != 0) return nullptr;  // bridge.cpp:369
   std::unique_ptr<Engine, void (*)(Engine*)> e(new Engine(), free_engine);
@@ -830,6 +866,10 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     }
     t.seekg(0);
     t.read(reinterpret_cast<char*>(e->tiling.data()), e->tiling.size());
+  }
+  if (!cfg_ok) {
+    *status = kCreateConfig;
+    return nullptr;
   }
   if (!parse_dims(cfg, e->dims)) {
     *status = kCreateConfig;
@@ -860,8 +900,7 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     *status = kCreateDevice;
     return nullptr;
   }
-  if (hipMemset(e->weights, 0, e->weight_bytes) != hipSuccess ||
-      write_fused_layer_table(e->dims, e->weights, e->layer_off.data(), e->scratch.fused_layers) != hipSuccess) {
+  if (hipMemset(e->weights, 0, e->weight_bytes) != hipSuccess) {
     *status = kCreateDevice;
     return nullptr;
   }
@@ -909,8 +948,11 @@ extern "C" int32_t resident_epoch_execute(
   const bool direct_device_import = ipc_metadata != nullptr;
   const bool importing = transfer_path != nullptr || direct_device_import;
   Engine* e = static_cast<Engine*>(opaque);
+  // The bridge's row arrays are four rows wide (resident_epoch_bridge.h:29-43):
+  // an engine of another batch is served through resident_epoch_proc only.
   const int B = e ? e->dims.batch : 0;
-  if (e == nullptr || request_count < 1 || request_count > B || max_steps < 1 || max_steps > kMaxEpochSteps ||
+  if (e == nullptr || B != kBridgeRows || request_count < 1 || request_count > B || max_steps < 1 ||
+      max_steps > kMaxEpochSteps ||
       input_token_ids == nullptr || input_positions == nullptr || input_sequence_lengths == nullptr ||
       input_eos_token_ids == nullptr || input_row_generations == nullptr || output_token_ids == nullptr ||
       output_executed == nullptr || output_row_generations == nullptr || output_model_calls == nullptr ||
@@ -1400,10 +1442,6 @@ int32_t state_access(Engine* e, const char* name, void* buf, int64_t bytes, Acce
   } else if (n == "logits") {
     dev = e->logits;
     size = (size_t)d.batch * d.vocab * sizeof(float);
-  } else if (n == "step_trace") {
-    if (e->scratch.step_trace == nullptr) return -1;
-    dev = e->scratch.step_trace;
-    size = fused_trace_bytes(d, e->plan.fused_grid);
   } else if (n == "inv_freq") {
     dev = e->scratch.inv_freq;
     size = (size_t)d.head_dim / 2 * sizeof(float);
@@ -1492,7 +1530,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"streamed_weight_bytes", static_cast<int64_t>(e->streamed_weight_bytes)},
       {"configured_eos", d.configured_eos},
       {"step_ops", re::step_op_count(e->env())},
-      {"ops_per_layer", e->plan.fused ? 0 : 7},
+      {"ops_per_layer", 7},
       {"timing_layer", e->timing_layer},
       {"qkv_grid", e->plan.qkv_grid},
       {"o_segments", e->plan.o_segments},
@@ -1500,9 +1538,10 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"gateup_grid", e->plan.gu_grid},
       {"down_segments", e->plan.down_segments},
       {"lm_grid", e->plan.lm_grid},
-      {"fused_step", e->plan.fused},
-      {"fused_grid", e->plan.fused_grid},
       {"compute_units", e->cus},
+      {"epoch_h2d_copies", e->last_epoch_copies[0]},
+      {"epoch_d2h_copies", e->last_epoch_copies[1]},
+      {"epoch_other_copies", e->last_epoch_copies[2]},
   };
   auto it = facts.find(k);
   if (it == facts.end()) return -1;

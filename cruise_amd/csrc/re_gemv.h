@@ -1,6 +1,5 @@
-// Building blocks of the weight-streaming skinny GEMMs (gfx950), shared by the
-// per-op decoder-step kernels (re_step.hip) and the persistent step kernel
-// (re_fused.hip).
+// Building blocks of the weight-streaming skinny GEMMs of the decoder step
+// (gfx950; re_step.hip).
 //
 // A wave owns two weight rows over one K-segment of up to 7 x 512 elements
 // and issues all 14 of its 16-byte non-temporal loads before touching them,
@@ -222,118 +221,6 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int
   lds_barrier();
 }
 
-
-// ---------------------------------------------------------------------------
-// Global -> LDS staging without registers (gfx950 16-byte LDS loads: lane i
-// of a wave instruction writes its 16 bytes at the wave's LDS base + 16 i).
-// The rows stay out of the register file, which is what the persistent step
-// kernel needs to keep four waves per SIMD with a weight row pair in flight.
-// ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void* re_lds_void;
-typedef __attribute__((address_space(1))) void* re_global_void;
-
-// Rows [0, MB) of X (row stride ldg elements; columns [k0, k0 + len), len a
-// multiple of 8) into xs [MB][ldx] (bf16): 1 KB pieces of 512 elements, wave
-// w taking pieces w, w + 4, ...  Rows >= B read row B-1 (they are never
-// used); lanes past len read inside the segment and land past column len,
-// which no product reads.  Completion: wait_vmem() then a workgroup barrier.
-template <int MB>
-__device__ __forceinline__ void dma_rows(bf16_t* xs, int ldx, const bf16_t* X, int ldg, int B, int k0, int len,
-                                         int tid) {
-  const int lane = tid & 63, wave = wave_index(tid);
-  const int per_row = (len + 511) / 512;
-  for (int p = wave; p < MB * per_row; p += 4) {
-    const int m = p / per_row, j = p - m * per_row;
-    const int k = min(j * 512 + lane * 8, len - 8);
-    const bf16_t* src = X + (size_t)min(m, B - 1) * ldg + k0 + k;
-    __builtin_amdgcn_global_load_lds((re_global_void)src, (re_lds_void)(xs + m * ldx + j * 512), 16, 0, 0);
-  }
-}
-
-// RMSNorm of rows [0, MB) already in xs [MB][H] (dma_rows), in place, with
-// norm_to_lds's arithmetic and reduction order: thread t owns chunks t and
-// t + 256 of every row; w: its two chunks of the norm weight.
-template <int MB>
-__device__ __forceinline__ void norm_in_lds(bf16_t* xs, const Vec8<bf16_t> (&w)[kNormChunks], int H, float eps,
-                                            float* red, int tid) {
-  const int lane = tid & 63, wave = wave_index(tid);
-  const int per_row = H / 8;
-  float ss[MB];
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < kNormChunks; ++j) {
-      const int c = tid + 256 * j;
-      const Vec8<bf16_t> h = c < per_row ? *reinterpret_cast<const Vec8<bf16_t>*>(xs + m * H + c * 8) : Vec8<bf16_t>{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = h.get(e);
-        s = fmaf(x, x, s);
-      }
-    }
-    ss[m] = s;
-  }
-  wave_reduce_transpose<MB>(ss, lane);
-  if ((lane & (64 / MB - 1)) == 0) red[wave * MB + lane / (64 / MB)] = ss[0];
-  lds_barrier();
-  float rs[MB];
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    float total = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) total += red[q * MB + m];
-    rs[m] = rsqrtf(total / static_cast<float>(H) + eps);
-  }
-#pragma unroll
-  for (int j = 0; j < kNormChunks; ++j) {
-    const int c = tid + 256 * j;
-    if (c < per_row) {
-#pragma unroll
-      for (int m = 0; m < MB; ++m) {
-        Vec8<bf16_t>* p = reinterpret_cast<Vec8<bf16_t>*>(xs + m * H + c * 8);
-        *p = norm_apply<bf16_t>(*p, w[j], rs[m]);
-      }
-    }
-  }
-  lds_barrier();
-}
-
-// ---------------------------------------------------------------------------
-// Device-coherent variants for activations written by other workgroups of
-// the same launch (the persistent step kernel): the rows come through CoBuf
-// (sc1) loads.  z is zero; it is read from LDS after the dependency wait, and
-// adding it to the offsets keeps the compiler from issuing these loads before
-// the wait.
-// ---------------------------------------------------------------------------
-// norm_load with the residual rows read through CoBuf (the norm weight is
-// read-only and comes through the cache).
-template <typename T, int MB>
-__device__ __forceinline__ void norm_load_co(NormIn<T, MB>& in, const CoBuf& hidden, const T* __restrict__ norm_w,
-                                             int b0, int B, int H, uint32_t z, int tid) {
-  const int per_row = H / 8;
-#pragma unroll
-  for (int j = 0; j < kNormChunks; ++j) {
-    const int c = min(tid + 256 * j, per_row - 1);
-    in.w[j] = Vec8<T>::load_cached(norm_w + c * 8);
-#pragma unroll
-    for (int m = 0; m < MB; ++m)
-      in.h[m][j] = co_load_vec8<T>(hidden, ((uint32_t)min(b0 + m, B - 1) * H + c * 8) * sizeof(T) + z);
-  }
-}
-
-// load_rows_block with the rows read through CoBuf.
-template <typename T, int MB>
-__device__ __forceinline__ void load_rows_block_co(Vec8<T> (&v)[seg_vecs_per_thread<MB>()], const CoBuf& X, int ldg,
-                                                   int b0, int B, int k0, int len, uint32_t z, int tid) {
-  const int per_row = max(len / 8, 1);
-#pragma unroll
-  for (int i = 0; i < seg_vecs_per_thread<MB>(); ++i) {
-    const int idx = min(tid + 256 * i, MB * per_row - 1);
-    const int m = idx / per_row, k = (idx - m * per_row) * 8;
-    v[i] = co_load_vec8<T>(X, ((uint32_t)min(b0 + m, B - 1) * ldg + k0 + k) * sizeof(T) + z);
-  }
-}
 
 }  // namespace
 }  // namespace re

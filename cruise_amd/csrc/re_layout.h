@@ -82,7 +82,8 @@ struct StatePtrs {
   int32_t* eos;         // [B]
   int32_t* initial_active;  // [B]
   int32_t* generation;  // [B] from control
-  int32_t* misc;        // [0] K, [1] sampling, [2] variant, [3] importing, [4] import mask
+  int32_t* misc;        // [0] K, [1] sampling, [2] variant, [3] importing, [4] import mask,
+                        // [5] import complete, [6] some import row adopted
   // resident state (CTRL:624-631)
   int32_t* res_gen;
   int64_t* res_token;
@@ -123,10 +124,6 @@ struct Scratch {
   int32_t* am_bad;    // non-finite flags [nwg, B]
   float* inv_freq;    // fp32 [d/2]
   float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
-  int32_t* sync;      // persistent step kernel: abort flag + phase counters
-  void* fused_layers; // persistent step kernel: per-layer weight pointers [L]
-  unsigned long long* step_trace;  // persistent step kernel phase trace (nullptr: off)
-  void* fused_act;    // persistent step kernel: per-layer activation blocks
 };
 
 struct LaunchPlan {
@@ -139,8 +136,6 @@ struct LaunchPlan {
   int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
   int slot_w[4];   // their per-slot weights
   int gu_grid_eq, lm_grid_eq;  // the grids for equal ranges
-  int fused;       // 1: a step is the persistent kernel (re_fused.hip)
-  int fused_grid;  // its workgroups: the chip's resident capacity
 };
 
 // Arguments of the paged decode attention (re_attn.hip).
@@ -183,26 +178,8 @@ struct KernelEnv {
 hipError_t launch_decoder_step(const KernelEnv& env, const StepPtrs& step, hipStream_t stream);
 hipError_t launch_step_ops(const KernelEnv& env, const StepPtrs& step, hipStream_t stream, int begin, int end);
 int step_op_count(const KernelEnv& env);
-// The op whose launch the epoch timing brackets: layer's gate/up projection
-// (per-op path) or the persistent step kernel.
+// The op whose launch the epoch timing brackets: layer's gate/up projection.
 int timed_op_index(const KernelEnv& env, int layer);
-// Persistent step kernel (re_fused.hip): bf16, B <= 4, hidden = q_dim = 3584,
-// head_dim 128.  Ops: 0 = embedding + counter reset, 1 = the kernel.
-bool fused_step_eligible(const Dims& d);
-size_t fused_lds_bytes(const Dims& d);
-size_t fused_layer_table_bytes(const Dims& d);
-int fused_sync_ints(const Dims& d);
-int fused_grid(const Dims& d, int cus);
-bool fused_grid_valid(const Dims& d, int grid, int cus);
-size_t fused_trace_bytes(const Dims& d, int grid);
-// Byte offsets inside one layer's activation block of the persistent kernel.
-struct FusedActLayout {
-  size_t q, attn, mlp, h_mid, h_out, part, stride;
-};
-FusedActLayout fused_act_layout(const Dims& d);
-size_t fused_act_bytes(const Dims& d);
-hipError_t write_fused_layer_table(const Dims& d, const uint8_t* weights, const LayerOffsets* lo, void* dst);
-hipError_t launch_fused_ops(const KernelEnv& env, const StepPtrs& st, hipStream_t stream, int begin, int end);
 // Grid sizes of the grid-stride projections from the kernels' occupancy.
 void plan_grids(LaunchPlan& p, const Dims& d, int cus);
 // Controller kernels.

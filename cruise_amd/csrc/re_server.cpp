@@ -12,7 +12,8 @@
 //   SOCKET must lie under /dev/shm/.  The server listens, accepts one client,
 //   creates the engine (resident_epoch_create with the other five
 //   arguments), sends a startup response whose transport status is 0 or
-//   100 + the create status, and then serves one request at a time:
+//   100 + the create status (101 also for an engine whose batch is not the
+//   wire records' four rows), and then serves one request at a time:
 //     1 EXECUTE, 2 WARM_UP      resident_epoch_execute, no KV import
 //     4 IMPORT_EXECUTE          import from the host snapshot file
 //                               SOCKET + ".kv-transfer" (deleted afterwards)
@@ -195,6 +196,14 @@ class Session {
     int32_t status = -1;
     engine_ = resident_epoch_create(create_args[0], create_args[1], create_args[2], create_args[3], create_args[4],
                                     &status);
+    // The wire records carry four rows: an engine of any other batch cannot
+    // be served and is reported as a creation failure with bad arguments (1).
+    int64_t batch = 0;
+    if (engine_ != nullptr && (resident_epoch_info(engine_, "batch", &batch) != 0 || batch != kRows)) {
+      resident_epoch_destroy(engine_);
+      engine_ = nullptr;
+      status = 1;
+    }
     const int32_t transport = engine_ == nullptr ? kExitCreateBase + status : 0;
     const WireResponse startup = blank_response(transport);
     const bool sent = send_exact(client_, &startup, sizeof(startup));

@@ -666,13 +666,13 @@ void plan_grids(LaunchPlan& p, const Dims& d, int cus) {
   }
 }
 
-int step_op_count(const KernelEnv& env) { return env.plan.fused ? 2 : 2 + kOpsPerLayer * env.dims.layers; }
+int step_op_count(const KernelEnv& env) { return 2 + kOpsPerLayer * env.dims.layers; }
 int timed_op_index(const KernelEnv& env, int layer) {
-  return env.plan.fused ? 1 : 1 + kOpsPerLayer * layer + kGateUpOp;
+  (void)env;
+  return 1 + kOpsPerLayer * layer + kGateUpOp;
 }
 
 hipError_t launch_step_ops(const KernelEnv& env, const StepPtrs& step, hipStream_t stream, int begin, int end) {
-  if (env.plan.fused) return launch_fused_ops(env, step, stream, begin, end);
   const bool bf16 = env.dims.dtype_bytes == 2;
   if (env.plan.mb == 4)
     return bf16 ? decoder_step_t<bf16_t, 4>(env, step, stream, begin, end)

@@ -90,7 +90,7 @@ def main() -> int:
     cfg = EngineConfig(
         model=ModelSpec(),
         engine=EngineSpec(
-            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=capacity, fused_step=False
+            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=capacity
         ),
         weights=WeightSpec("synthetic", 1, 0.02),
         tuning=json.loads(args.tuning) if args.tuning else {},

@@ -60,13 +60,6 @@ class EngineSpec:
     logical_capacity: int = 8
     configured_eos: int = 151645
     require_dev_shm: bool = True
-    # Run each decoder step as the persistent step kernel where the shape
-    # allows it (bf16, batch <= 4, hidden = q_dim = 3584, head_dim 128);
-    # False (the default) runs the per-op launches.
-    fused_step: bool = False
-    # Record per-workgroup phase timestamps of the persistent step kernel
-    # (read back with read_state("step_trace")); diagnostics only.
-    trace_step: bool = False
 
 
 @dataclass(frozen=True)
@@ -408,9 +401,8 @@ class ResidentEpochRuntime:
 
     def timed_launch_ms(self) -> list[float]:
         """Durations (ms) of the timed launches since the last read (the
-        persistent step kernel, or the per-op path's gate/up projection, in
-        each epoch's last step): one per completed epoch while timing is
-        enabled."""
+        gate/up projection of the timing layer in each epoch's last step):
+        one per completed epoch while timing is enabled."""
         n = 4096
         buf = (ctypes.c_float * n)()
         got = self.lib.resident_epoch_read_kernel_timing(self.handle, buf, n)

@@ -20,7 +20,6 @@ from __future__ import annotations
 
 from typing import Any
 
-from .benchmark_metrics import ResidentEpochBenchmarkMetrics
 from .config import EPOCH_STEP_CHOICES, ResidentEpochConfig
 from .contract import CONTRACT_VERSION, ResidentEpochPlan, ResidentEpochRequest, attach_plan, get_plan, get_result
 from .eligibility import request_rejection_reason
@@ -51,7 +50,6 @@ class ResidentEpochSchedulerMixin:
         self._resident_epoch_generations: dict[str, int] = {}
         self._resident_epoch_device_owned: set[str] = set()
         self._resident_epoch_next_generation = 1
-        self._resident_epoch_benchmark_metrics = ResidentEpochBenchmarkMetrics.from_env()
         if self.vllm_config.speculative_config is not None:
             raise ValueError("resident epoch scheduler cannot be combined with speculative decoding")
         if self.scheduler_config.async_scheduling:
@@ -76,7 +74,6 @@ class ResidentEpochSchedulerMixin:
             "_resident_epoch_rows": dict,
             "_resident_epoch_generations": dict,
             "_resident_epoch_device_owned": set,
-            "_resident_epoch_benchmark_metrics": ResidentEpochBenchmarkMetrics,
         }
         for name, make in defaults.items():
             if not hasattr(self, name):
@@ -172,7 +169,6 @@ class ResidentEpochSchedulerMixin:
         self._resident_epoch_last_rejection = rejection
         self._resident_epoch_last_plan = plan
         self._resident_epoch_last_result = None
-        self._resident_epoch_benchmark_metrics.record_schedule(plan, rejection)
         if plan is not None:
             attach_plan(output, plan)
         return output
@@ -278,7 +274,6 @@ class ResidentEpochSchedulerMixin:
         if result is None:
             raise RuntimeError("resident epoch plan did not receive execution metadata")
         self._resident_epoch_last_result = result
-        self._resident_epoch_benchmark_metrics.record_result(result)
         self._apply_resident_epoch_accounting(scheduler_output, model_runner_output, plan, result)
         return super().update_from_output(scheduler_output, model_runner_output)
 

@@ -55,7 +55,9 @@ typedef struct ResidentEpochIpcMetadata {
  * air_path, func_config: must be non-null (kept for call compatibility; the
  *   HIP library has no AIR graph or DataFlow function to load).
  * tiling_path: must name a file of exactly 72 bytes (bridge.cpp:97-106).
- * *status: 0 ok; 1 bad arguments or an engine already active; 2 tiling;
+ * *status, checked in the reference's order: 0 ok; 1 bad arguments, an
+ *   engine already active or a weight directory outside /dev/shm/ (unless
+ *   the configuration sets "engine": {"require_dev_shm": false}); 2 tiling;
  *   3 graph_config unreadable or invalid; 4 graph build failed; 5 weight
  *   load failed; 6 HIP runtime init failed; 7 no usable HIP device or device
  *   memory exhausted. */
@@ -65,8 +67,10 @@ void *resident_epoch_create(const char *air_path, const char *graph_config,
                             const char *tiling_path, int32_t *status);
 
 /* Replaces native/resident_epoch_bridge.h:29-43 (resident_epoch_bridge.cpp:424-649).
- * Host arrays of B rows (B=4 for the reference geometry); output_token_ids is
- * row-major [row * 8 + step].  Return: 0 ok; 10 arguments; 11 row metadata;
+ * Host arrays of 4 rows, as in the reference; an engine whose batch is not 4
+ * returns 10 (it is driven through resident_epoch_proc instead).
+ * output_token_ids is row-major [row * 8 + step].
+ * Return: 0 ok; 10 arguments; 11 row metadata;
  * 12 active rows != request_count; 13 transfer file; 30 epoch launch failed;
  * 31 epoch completion failed; 33 executed count out of range; 34 import
  * checksum mismatch; 35 IPC metadata invalid or not mappable (the engine maps
@@ -171,9 +175,11 @@ int32_t resident_epoch_write_state(void *engine, const char *name,
  * "streamed_weight_bytes", "configured_eos", "import_feed_bytes",
  * "step_ops" (entries of a decoder step's launch list), "ops_per_layer",
  * "timing_layer", launch-plan sizes ("qkv_grid", "gateup_grid", "lm_grid",
- * "o_segments", "down_segments", "gemv_rows_per_pass"), "fused_step" (1: a
- * step is the persistent kernel), "fused_grid" (its workgroups),
- * "compute_units".  Return 0 or -1 for an unknown key. */
+ * "o_segments", "down_segments", "gemv_rows_per_pass"), "compute_units",
+ * and the memory copies of the last epoch launched, counted from the nodes of
+ * its captured graph(s): "epoch_h2d_copies", "epoch_d2h_copies",
+ * "epoch_other_copies" (device-to-device copies and memsets; -1 before the
+ * first epoch).  Return 0 or -1 for an unknown key. */
 int32_t resident_epoch_info(void *engine, const char *key, int64_t *value);
 
 /* Kernel timing in the epoch: when enabled, each epoch runs as graph part 1,

@@ -104,3 +104,11 @@ extern "C" void resident_epoch_destroy(void* engine) {
   (void)engine;
   log_line("destroy");
 }
+
+// Only "batch" is known: 4, or STUB_BATCH when set.
+extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* value) {
+  if (engine != &g_engine || key == nullptr || value == nullptr || strcmp(key, "batch") != 0) return -1;
+  const char* forced = getenv("STUB_BATCH");
+  *value = forced != nullptr ? atoi(forced) : 4;
+  return 0;
+}

@@ -89,6 +89,44 @@ def oracle_controller(w: Workload, weights_cpu: dict, *, capacity: int | None = 
     return dec, ctl
 
 
+def engine_snapshot(rt: ResidentEpochRuntime, dtype: torch.dtype) -> tuple:
+    """The engine's resident state (caches on the device, resident rows)."""
+    elems = rt.cache_bytes // torch.tensor([], dtype=dtype).element_size()
+    k = torch.empty(elems, dtype=dtype, device="cuda")
+    v = torch.empty(elems, dtype=dtype, device="cuda")
+    rt.read_state("key_cache", k)
+    rt.read_state("value_cache", v)
+    return k, v, rt.resident_rows().copy()
+
+
+def engine_restore(rt: ResidentEpochRuntime, snap: tuple) -> None:
+    k, v, rows = snap
+    rt.write_state("key_cache", k)
+    rt.write_state("value_cache", v)
+    rt.write_state("resident_rows", rows)
+
+
+def oracle_snapshot(ctl: EpochController) -> dict:
+    return {
+        "key": ctl.resident_key.clone(),
+        "value": ctl.resident_value.clone(),
+        "rows": [list(ctl.resident_generation), list(ctl.resident_token), list(ctl.resident_position),
+                 list(ctl.resident_length), list(ctl.resident_valid)],
+    }
+
+
+def oracle_restore(ctl: EpochController, snap: dict) -> None:
+    ctl.resident_key = snap["key"].clone()
+    ctl.resident_value = snap["value"].clone()
+    (ctl.resident_generation, ctl.resident_token, ctl.resident_position, ctl.resident_length,
+     ctl.resident_valid) = (list(r) for r in snap["rows"])
+
+
+def first_max(row: np.ndarray) -> int:
+    """First index of the maximum (numpy's argmax returns the first occurrence)."""
+    return int(np.argmax(np.asarray(row, dtype=np.float32)))
+
+
 def assert_close_rel(actual, expected, rel: float, what: str) -> None:
     a = torch.as_tensor(actual).float()
     b = torch.as_tensor(expected).float()

@@ -123,6 +123,119 @@ def test_full_model_two_epochs_after_prefill(rt_weights):
             if executed[r] > 0:
                 tokens[r] = hist[executed[r] - 1, r]
                 positions[r] += executed[r]
+    check_caches(rt, ctl)
+
+
+def check_caches(rt, ctl):
+    for name, ref in (("key_cache", ctl.resident_key), ("value_cache", ctl.resident_value)):
+        got = torch.zeros(rt.cache_bytes // 2, dtype=torch.bfloat16)
+        rt.read_state(name, got)
+        assert_close_rel(got.view_as(ref), ref, rel_tol(W.dims), f"resident {name}")
+
+
+def fresh_prefilled(rt, cpu, seed, table):
+    rng = np.random.default_rng(seed)
+    ps = [list(map(int, rng.integers(0, W.dims.vocab, size=int(rng.integers(2, 6))))) for _ in range(B)]
+    _, ctl = oracle_controller(W, cpu)
+    zeros = torch.zeros(rt.cache_bytes // 2, dtype=torch.bfloat16, device="cuda")
+    rt.write_state("key_cache", zeros)
+    rt.write_state("value_cache", zeros)
+    rt.write_state("resident_rows", np.zeros((5, B), dtype=np.int64))
+    gens = np.arange(1, B + 1, dtype=np.int32) + seed % 97
+    for r in range(B):
+        rt.prefill(r, int(gens[r]), ps[r], table[r])
+        ctl.prefill_row(r, int(gens[r]), ps[r], table[r])
+    tokens = np.array([p[-1] for p in ps], dtype=np.int64)
+    positions = np.array([len(p) - 1 for p in ps], dtype=np.int64)
+    return ctl, tokens, positions, gens
+
+
+@pytest.mark.parametrize("K", [1, 2, 4])
+def test_full_model_epoch_k(rt_weights, K):
+    """One K-step epoch after prefilling, for each K of the sweep besides the
+    bench's K=8 (each K runs its own captured graph)."""
+    rt, cpu = rt_weights
+    table = np.array([[3, 0], [6, 1], [2, 7], [5, 4]], dtype=np.int32)
+    ctl, tokens, positions, gens = fresh_prefilled(rt, cpu, 3300 + K, table)
+    print(f"[c3] K={K} epoch from positions {positions.tolist()}", flush=True)
+    hist, ctrl = run_epoch(rt, ctl, tokens, positions, gens, table, K=K)
+    assert ctrl[3] == 0 and ctrl[4] == K
+    check_caches(rt, ctl)
+
+
+def test_full_model_import_epoch_at_reference_payload(rt_weights):
+    """A host-snapshot KV import at the reference's own geometry: 28 layers x 4
+    rows x (K, V) x one 128-slot block of 4 x 128 bf16 = 29,360,128 bytes
+    behind an 80-byte transfer header (native/resident_epoch_protocol.h:8-9,
+    kv_transfer.py:31), through the bridge call, then a K=2 epoch.  Rows 0
+    and 2 import a 3- and a 100-token prefix, row 1 starts a new generation,
+    row 3 is empty."""
+    import os
+    import struct
+    import tempfile
+    import zlib
+
+    from oracle.controller import IMPORT_GRAPH_FLAG
+
+    rt, cpu = rt_weights
+    L, KVH, D = W.dims.num_layers, W.dims.num_kv_heads, W.dims.head_dim
+    block_elems = BS * KVH * D
+    payload_t = (torch.randn(2 * L * B * block_elems, generator=torch.Generator().manual_seed(3307)) * 0.25).to(
+        torch.bfloat16
+    )
+    payload = payload_t.view(torch.uint8).numpy().tobytes()
+    assert len(payload) == 29_360_128
+    mask = 0b0101
+    gens = [7, 8, 9, 0]
+    block_bytes = block_elems * 2
+    checksum = 1
+    for base in (0, L * B * block_bytes):  # kv_transfer.py:159-174 restated with zlib
+        for layer in range(L):
+            for row in range(B):
+                if mask & (1 << row):
+                    off = base + (layer * B + row) * block_bytes
+                    checksum = zlib.adler32(payload[off : off + block_bytes], checksum)
+    header = struct.pack("<QIIQQI4i7I", 0x4352554953454B56, 1, 80, 4242, len(payload), mask, *[7, 0, 9, 0],
+                         L, B, BS, KVH, D, 2, checksum)
+    tokens, positions, lengths = [17, 42, 99, 0], [3, 0, 100, 0], [4, 1, 101, 0]
+    zeros = torch.zeros(rt.cache_bytes // 2, dtype=torch.bfloat16, device="cuda")
+    rt.write_state("key_cache", zeros)
+    rt.write_state("value_cache", zeros)
+    rt.write_state("resident_rows", np.zeros((5, B), dtype=np.int64))
+    fd, path = tempfile.mkstemp(prefix="cruise-kv7b-", dir="/dev/shm")
+    try:
+        with os.fdopen(fd, "wb") as f:
+            f.write(header)
+            f.write(payload)
+        out = rt.execute(3, 2, tokens, positions, lengths, [W.eos] * B, gens, transfer_path=path, transfer_id=4242)
+    finally:
+        os.unlink(path)
+    assert out.status == 0 and out.device_status == 0, (out.status, out.device_status)
+    assert out.kv_import_checksum == checksum & 0xFFFFFFFF
+    assert out.declared_input_bytes == 29_360_128 + 260 - 16
+    table = np.arange(B * BPR, dtype=np.int32).reshape(B, BPR)
+    control = np.zeros(control_input_elements(B), dtype=np.int32)
+    control[0] = 2
+    control[1 : 1 + B] = W.eos
+    control[2 + B] = IMPORT_GRAPH_FLAG | mask
+    control[3 + B :] = gens
+    _, ctl = oracle_controller(W, cpu)
+    hist = np.full((8, B), -1, dtype=np.int64)
+    for r in range(B):
+        hist[: out.executed[r], r] = out.token_ids[r, : out.executed[r]]
+    ctl.token_override = TeacherForcing(hist, rel_tol(W.dims))
+    ref = ctl.proc(EpochFeed(np.array(tokens), np.array(positions), np.array(lengths, dtype=np.int32),
+                             np.zeros(B, dtype=np.int32), np.array([1, 1, 1, 0], dtype=np.int32), table.reshape(-1),
+                             tiling_bytes(), control, import_payload=payload))
+    assert not ctl.token_override.mismatches, ctl.token_override.mismatches
+    np.testing.assert_array_equal(hist, ref.history)
+    assert int(np.uint32(np.int32(ref.control[5]))) == checksum & 0xFFFFFFFF
+    np.testing.assert_array_equal(out.executed, ref.control[6 + 2 * B : 6 + 3 * B])
+    check_caches(rt, ctl)
+    # the imported prefixes are the payload, bit for bit
     key = torch.zeros(rt.cache_bytes // 2, dtype=torch.bfloat16)
     rt.read_state("key_cache", key)
-    assert_close_rel(key.view_as(ctl.resident_key), ctl.resident_key, rel_tol(W.dims), "resident keys")
+    key = key.view(L, -1, BS, KVH, D)
+    src = payload_t.view(2, L, B, BS, KVH, D)
+    assert torch.equal(key[:, table[0, 0], :3].view(torch.int16), src[0, :, 0, :3].view(torch.int16))
+    assert torch.equal(key[:, table[2, 0], :100].view(torch.int16), src[0, :, 2, :100].view(torch.int16))

@@ -5,7 +5,7 @@ Exercises the 8-row projection tiles (eight row tiles per projection), the
 multi-tile attention (up to four 256-position tiles per row), the controller
 at B=64 and random block tables from the pool.  The resident state of every
 row is installed directly (seeded KV over the whole pool plus the rows'
-generation/token/position), then one K=4 epoch runs on the device and in the
+generation/token/position), then one K=8 epoch runs on the device and in the
 teacher-forced oracle.
 """
 from __future__ import annotations
@@ -75,7 +75,7 @@ def test_b64_decoder_step(rt, weights_pair):
         assert_close_rel(flat(got)[:, written], flat(ref)[:, written], rel_tol(W.dims), f"written {what}")
 
 
-def test_b64_epoch_k4(rt, weights_pair):
+def test_b64_epoch_k8(rt, weights_pair):
     _, cpu = weights_pair
     rng = np.random.default_rng(6401)
     table = random_tables(rng, B, BPR, W.geometry.physical_blocks)
@@ -95,7 +95,7 @@ def test_b64_epoch_k4(rt, weights_pair):
     ctl.resident_position = [int(p) for p in pos]
     ctl.resident_length = [int(p) + 1 for p in pos]
     ctl.resident_valid = [1] * B
-    K = 4
+    K = 8
     lengths = (pos + 1).astype(np.int32)
     active = np.ones(B, dtype=np.int32)
     control = np.zeros(control_input_elements(B), dtype=np.int32)
@@ -111,3 +111,7 @@ def test_b64_epoch_k4(rt, weights_pair):
     np.testing.assert_array_equal(hist, ref.history)
     np.testing.assert_array_equal(ctrl, ref.control)
     assert ctrl[3] == 0 and ctrl[4] == K
+    for name, ref in (("key_cache", ctl.resident_key), ("value_cache", ctl.resident_value)):
+        got = torch.zeros(rt.cache_bytes // 2, dtype=torch.bfloat16)
+        rt.read_state(name, got)
+        assert_close_rel(got.view_as(ref), ref, rel_tol(W.dims), f"resident {name}")

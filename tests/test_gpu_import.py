@@ -140,6 +140,34 @@ def test_import_then_continuity_fallback(rt, weights):
     assert rows[0][0] == 7 and rows[2][0] == 3 and rows[4][0] == 1  # row 0 adopted at position 3
 
 
+def test_partial_import_then_invalid_row(rt, weights):
+    """Mask 0b0011 with row 1 inactive: CTRL:402-428 copies row 0's block and
+    adopts it, then rejects row 1 (201) before the checksum.  Row 0's KV and
+    resident record must be the oracle's: adopted, block copied bit for bit,
+    the other blocks of the row cleared."""
+    payload = make_payload(14)
+    mask = 0b0011
+    hist, ctrl, ref, ctl = import_case(
+        rt, weights, mask=mask, tokens=[17, 42, 0, 0], positions=[3, 0, 0, 0], lengths=[4, 1, 0, 0],
+        active=[1, 0, 0, 0], gens=[7, 0, 0, 0], K=2, payload=payload,
+    )
+    assert ctrl[3] == 201 and ref.control[3] == 201
+    np.testing.assert_array_equal(hist, ref.history)
+    np.testing.assert_array_equal(ctrl, ref.control)
+    assert ctrl[5] == 0  # the import stopped before its checksum
+    rows = rt.resident_rows()
+    np.testing.assert_array_equal(rows[0], ctl.resident_generation)
+    np.testing.assert_array_equal(rows[1], ctl.resident_token)
+    np.testing.assert_array_equal(rows[2], ctl.resident_position)
+    np.testing.assert_array_equal(rows[3], ctl.resident_length)
+    np.testing.assert_array_equal(rows[4], ctl.resident_valid)
+    assert rows[0][0] == 7 and rows[4][0] == 1
+    for name, ref_cache in (("key_cache", ctl.resident_key), ("value_cache", ctl.resident_value)):
+        got = torch.zeros(rt.cache_bytes // 4, dtype=torch.float32)
+        rt.read_state(name, got)
+        assert torch.equal(got.view_as(ref_cache), ref_cache), f"{name} after a partial import"
+
+
 def write_transfer(path: str, transfer_id: int, mask: int, gens, payload: bytes, checksum: int) -> None:
     header = HEADER.pack(TRANSFER_MAGIC, 1, HEADER.size, transfer_id, len(payload), mask, *gens, L, B, BS, KVH, D, 4, checksum)
     assert len(header) == 80

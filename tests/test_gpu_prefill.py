@@ -138,6 +138,23 @@ def test_bf16_layer_prefill_hand_written_gemm_matches_oracle(c2_weights):
     run_against_oracle(C2, dev, cpu, [41, 5, 70, 1], seed=5104, K=4, tuning={"prefill_blas": 0})
 
 
+def test_bf16_two_layer_long_prompt_prefill_matches_oracle():
+    """A 250-token prompt (four query tiles, the last one partial) beside
+    130-, 3- and 1-token prompts on two Qwen2.5-7B layers: layer 1's keys and
+    values depend on layer 0's prefill attention over the whole prompt, so
+    the oracle's teacher-forced prefill pins the causal attention, not only
+    the projections."""
+    from oracle.decoder import ModelDims
+    from oracle.workloads import C2_DIMS
+
+    dims = replace(C2_DIMS, num_layers=2)
+    W = replace(C2, name="qwen7b-2layer", dims=dims, seed=C2.seed + 2)
+    dev = generate_weights(W.dims, W.seed, device="cuda")
+    cpu = {k: v.cpu() for k, v in dev.items()}
+    assert isinstance(W.dims, ModelDims)
+    run_against_oracle(W, dev, cpu, [250, 130, 3, 1], seed=5106, K=4)
+
+
 def test_bf16_layer_prefill_matches_single_row_prefill(c2_weights):
     """Prompts up to 250 tokens (four query tiles, partial last tile): the
     batched pass against the engine's own per-row decoder steps."""

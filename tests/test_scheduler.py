@@ -20,7 +20,6 @@ from types import SimpleNamespace
 import pytest
 
 from cruise_amd.backend import ModelRunnerOutput
-from cruise_amd.benchmark_metrics import ResidentEpochBenchmarkMetrics, replay_event_journal
 from cruise_amd.config import ResidentEpochConfig
 from cruise_amd.contract import (
     CONTRACT_VERSION,
@@ -412,32 +411,3 @@ def test_config_from_env(monkeypatch):
     monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_CAPACITY", "x")
     with pytest.raises(ValueError, match="must be an integer"):
         ResidentEpochConfig.from_env()
-
-
-def test_benchmark_counters_and_journal_replay(monkeypatch):
-    if not os.path.isdir("/dev/shm"):
-        pytest.skip("no /dev/shm")
-    path = Path("/dev/shm") / f"cruise-metrics-{uuid.uuid4().hex[:8]}" / "m.json"
-    path.parent.mkdir()
-    try:
-        monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_BENCHMARK_METRICS_PATH", str(path))
-        s = Scheduler()
-        s._resident_epoch_config = ResidentEpochConfig(max_steps=4)
-        greedy_requests(s, 2, max_tokens=4)
-        out = s.schedule()
-        commit_device_epoch(s, out, {"0": [1, 2, 3, 4], "1": [5, 6, 7, 8]})
-        s.schedule()  # nothing left: an empty host schedule
-        s._resident_epoch_benchmark_metrics.flush()
-        record = json.loads(path.read_text())
-        c = record["counters"]
-        assert (c["schedule_calls"], c["device_plan_calls"], c["host_schedule_calls"]) == (2, 1, 1)
-        assert (c["device_epochs"], c["device_model_calls"], c["device_request_tokens"]) == (1, 4, 8)
-        assert record["epoch_steps"] == {"4": 1} and record["rejections"] == {"empty-schedule": 1}
-        assert replay_event_journal(path.with_name("m.events.jsonl")) == record
-    finally:
-        for p in path.parent.iterdir():
-            p.unlink()
-        path.parent.rmdir()
-    monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_BENCHMARK_METRICS_PATH", "relative.json")
-    with pytest.raises(ValueError, match="absolute path"):
-        ResidentEpochBenchmarkMetrics.from_env()

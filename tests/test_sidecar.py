@@ -268,6 +268,15 @@ def test_startup_failure_reports_the_create_status(sidecar_env, monkeypatch):
         SidecarDataFlowEngine()
 
 
+def test_startup_refuses_an_engine_that_is_not_four_rows(sidecar_env, monkeypatch):
+    # the wire records hold four rows; a B=64 engine would overrun them
+    monkeypatch.setenv("STUB_BATCH", "64")
+    with pytest.raises(RuntimeError, match="native initialization failed: 101"):
+        SidecarDataFlowEngine()
+    log = Path(os.environ["STUB_LOG"]).read_text().splitlines()
+    assert log[0].startswith("create ") and log[-1] == "destroy"
+
+
 def test_server_exits_when_the_client_goes_away(sidecar_env):
     eng = SidecarDataFlowEngine()
     eng.socket.close()
