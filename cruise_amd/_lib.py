@@ -67,6 +67,11 @@ SIGNATURES: dict[str, tuple] = {
         [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
          ctypes.c_void_p],
     ),
+    "resident_epoch_prefill_batch_noalloc": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_void_p],
+    ),
     "resident_epoch_read_state": (
         ctypes.c_int32,
         [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int64],

@@ -27,6 +27,18 @@
 #include "re_layout.h"
 
 namespace re {
+// Scratch of resident_epoch_prefill_batch_noalloc: the batched prefill's
+// activations and token tables for callers that cannot allocate device
+// memory.  One copy per GPU, held until the process ends; every call on a
+// GPU shares it (calls are serialized by g_noalloc_mutex, and a call leaves
+// its contents behind: nothing in it needs to start at zero, every byte a
+// pass reads is written earlier in the same pass).
+constexpr size_t kNoAllocScratchBytes = 64ull << 20;
+}  // namespace re
+
+static __device__ __align__(256) uint8_t scratch[re::kNoAllocScratchBytes];
+
+namespace re {
 namespace {
 
 constexpr int kBridgeRows = 4;  // rows of the bridge call's host arrays
@@ -35,6 +47,33 @@ constexpr int kCreateOk = 0, kCreateArgs = 1, kCreateTiling = 2, kCreateConfig =
 
 std::mutex g_lifecycle_mutex;
 bool g_engine_active = false;
+
+// Device addresses of `scratch`, per device: host code never names the array
+// itself (its host-side name is not a device address).
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mutex;
+uint8_t* g_noalloc_ptr[kMaxDevices] = {};
+
+// Resolves the array's address on `device`, which must be current; once per
+// device (at engine creation).  False on a HIP error.
+bool noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+  if (g_noalloc_ptr[device] != nullptr) return true;
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    return false;
+  }
+  g_noalloc_ptr[device] = static_cast<uint8_t*>(ptr);
+  return true;
+}
+
+uint8_t* noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+  return g_noalloc_ptr[device];
+}
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -884,6 +923,11 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     *status = kCreateDevice;
     return nullptr;
   }
+  e->device = 0;
+  if (!noalloc_setup(e->device)) {  // the no-allocation scratch's address on this device
+    *status = kCreateRuntime;
+    return nullptr;
+  }
   hipDeviceProp_t prop{};
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess && prop.multiProcessorCount > 0)
     e->cus = prop.multiProcessorCount;
@@ -1223,8 +1267,13 @@ namespace {
 // One pass of the decoder over the prompt tokens of several rows (see
 // resident_epoch_prefill_batch).  Token i of the pass is (row, position);
 // a row's tokens are consecutive and start at position 0.
+// Scratch: the engine's own buffer, grown on demand, or (fixed != nullptr)
+// the caller's fixed buffer of fixed_bytes, in which case nothing is
+// allocated, the GEMMs are the hand-written ones (hipBLASLt keeps a
+// workspace of its own) and a pass that does not fit returns -3.
 int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector<int32_t>& gens,
-                      const std::vector<std::vector<int64_t>>& prompts, const std::vector<int32_t>& tables) {
+                      const std::vector<std::vector<int64_t>>& prompts, const std::vector<int32_t>& tables,
+                      uint8_t* fixed = nullptr, size_t fixed_bytes = 0) {
   using namespace re;
   const Dims& d = e.dims;
   const int nr = static_cast<int>(rows.size());
@@ -1263,14 +1312,16 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
   const size_t o_mlp = take(M * I * T), o_rope = take((size_t)M * d.head_dim * sizeof(float));
   const size_t o_tok = take(8 * (size_t)M), o_pos = take(4 * (size_t)M), o_slot = take(4 * (size_t)M);
   const size_t o_tiles = take(sizeof(int4) * tiles.size()), o_blocks = take(4 * tables.size());
-  if (off > e.pf_bytes) {
+  if (fixed != nullptr) {
+    if (off > fixed_bytes) return -3;
+  } else if (off > e.pf_bytes) {
     if (e.pf_mem) (void)hipFree(e.pf_mem);
     e.pf_mem = nullptr;
     e.pf_bytes = 0;
     if (hipMalloc(&e.pf_mem, off) != hipSuccess) return -2;
     e.pf_bytes = off;
   }
-  uint8_t* b = e.pf_mem;
+  uint8_t* b = fixed != nullptr ? fixed : e.pf_mem;
   const bool ok = (M == 0 || (hipMemcpy(b + o_tok, tok.data(), 8 * M, hipMemcpyHostToDevice) == hipSuccess &&
                               hipMemcpy(b + o_pos, pos.data(), 4 * M, hipMemcpyHostToDevice) == hipSuccess &&
                               hipMemcpy(b + o_slot, slot.data(), 4 * M, hipMemcpyHostToDevice) == hipSuccess &&
@@ -1278,10 +1329,11 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
                                         hipMemcpyHostToDevice) == hipSuccess)) &&
                   hipMemcpy(b + o_blocks, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice) == hipSuccess;
   if (!ok) return -2;
-  if (d.dtype_bytes == 2 && !e.pf_blas_tried) {
+  if (fixed == nullptr && d.dtype_bytes == 2 && !e.pf_blas_tried) {
     e.pf_blas_tried = true;
     if (e.prefill_blas_allowed) e.pf_blas = prefill_blas_create();
   }
+  PrefillBlas* blas = fixed == nullptr ? e.pf_blas : nullptr;
   const KernelEnv env = e.env();
   if (launch_clear_blocks(env, e.key_cache, e.value_cache, reinterpret_cast<const int32_t*>(b + o_blocks),
                           static_cast<int>(tables.size()), s) != hipSuccess)
@@ -1319,7 +1371,7 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
         g.lda = lda;
         g.ldw = K;
         g.ldo = ldo;
-        if (e.pf_blas != nullptr) {
+        if (blas != nullptr) {
           // hipBLASLt: a store GEMM directly; a residual GEMM into the free
           // normalized-row buffer, then h = T(h + T(A W^T))
           GemmArgs y = g;
@@ -1327,7 +1379,7 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
             y.out = b + o_xn;
             y.ldo = N;
           }
-          if (prefill_blas_gemm(e.pf_blas, y, s)) {
+          if (prefill_blas_gemm(blas, y, s)) {
             if (epi == kGemmResidual) run(launch_prefill_residual(b + out_off, b + o_xn, M, N, ldo, N, s));
             return;
           }
@@ -1388,38 +1440,72 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
 
 }  // namespace
 
+namespace {
+
+// The arguments of a batched prefill, checked and copied (false: -1).
+struct PrefillRequest {
+  std::vector<int> rows;
+  std::vector<int32_t> gens;
+  std::vector<std::vector<int64_t>> prompts;
+  std::vector<int32_t> tables;
+};
+
+bool parse_prefill(const re::Dims& d, int32_t n_rows, const int32_t* rows, const int32_t* generations,
+                   const int64_t* prompts, const int32_t* prompt_lens, const int32_t* block_tables,
+                   PrefillRequest& req) {
+  if (rows == nullptr || generations == nullptr || prompts == nullptr || prompt_lens == nullptr ||
+      block_tables == nullptr || n_rows < 1 || n_rows > d.batch)
+    return false;
+  req.rows.assign(n_rows, 0);
+  req.gens.assign(generations, generations + n_rows);
+  req.prompts.assign(n_rows, {});
+  req.tables.assign(block_tables, block_tables + (size_t)n_rows * d.blocks_per_row);
+  std::vector<bool> seen(d.batch, false);
+  size_t at = 0;
+  for (int i = 0; i < n_rows; ++i) {
+    const int r = rows[i];
+    if (r < 0 || r >= d.batch || seen[r] || req.gens[i] <= 0) return false;
+    seen[r] = true;
+    req.rows[i] = r;
+    const int len = prompt_lens[i];
+    if (len < 1 || len > d.capacity || (len > 1 && (len - 2) / d.block_size >= d.blocks_per_row)) return false;
+    req.prompts[i].assign(prompts + at, prompts + at + len);
+    at += len;
+    for (int64_t t : req.prompts[i])
+      if (t < 0 || t >= d.vocab) return false;
+  }
+  for (int32_t blk : req.tables)
+    if (blk < 0 || blk >= d.physical_blocks) return false;
+  return true;
+}
+
+}  // namespace
+
 extern "C" int32_t resident_epoch_prefill_batch(void* engine, int32_t n_rows, const int32_t* rows,
                                                 const int32_t* generations, const int64_t* prompts,
                                                 const int32_t* prompt_lens, const int32_t* block_tables) {
   using namespace re;
   Engine* e = static_cast<Engine*>(engine);
-  if (e == nullptr || rows == nullptr || generations == nullptr || prompts == nullptr || prompt_lens == nullptr ||
-      block_tables == nullptr)
+  PrefillRequest req;
+  if (e == nullptr || !parse_prefill(e->dims, n_rows, rows, generations, prompts, prompt_lens, block_tables, req))
     return -1;
-  const Dims& d = e->dims;
-  if (n_rows < 1 || n_rows > d.batch) return -1;
-  std::vector<int> row_list(n_rows);
-  std::vector<int32_t> gens(generations, generations + n_rows);
-  std::vector<std::vector<int64_t>> prompt_list(n_rows);
-  std::vector<int32_t> tables(block_tables, block_tables + (size_t)n_rows * d.blocks_per_row);
-  std::vector<bool> seen(d.batch, false);
-  size_t at = 0;
-  for (int i = 0; i < n_rows; ++i) {
-    const int r = rows[i];
-    if (r < 0 || r >= d.batch || seen[r] || gens[i] <= 0) return -1;
-    seen[r] = true;
-    row_list[i] = r;
-    const int len = prompt_lens[i];
-    if (len < 1 || len > d.capacity || (len > 1 && (len - 2) / d.block_size >= d.blocks_per_row)) return -1;
-    prompt_list[i].assign(prompts + at, prompts + at + len);
-    at += len;
-    for (int64_t t : prompt_list[i])
-      if (t < 0 || t >= d.vocab) return -1;
-  }
-  for (int32_t blk : tables)
-    if (blk < 0 || blk >= d.physical_blocks) return -1;
   std::lock_guard<std::mutex> lock(e->execute_mutex);
-  return prefill_batch(*e, row_list, gens, prompt_list, tables);
+  return prefill_batch(*e, req.rows, req.gens, req.prompts, req.tables);
+}
+
+extern "C" int32_t resident_epoch_prefill_batch_noalloc(void* engine, int32_t n_rows, const int32_t* rows,
+                                                        const int32_t* generations, const int64_t* prompts,
+                                                        const int32_t* prompt_lens, const int32_t* block_tables) {
+  using namespace re;
+  Engine* e = static_cast<Engine*>(engine);
+  PrefillRequest req;
+  if (e == nullptr || !parse_prefill(e->dims, n_rows, rows, generations, prompts, prompt_lens, block_tables, req))
+    return -1;
+  uint8_t* scratch_ptr = noalloc_scratch(e->device);
+  if (scratch_ptr == nullptr) return -2;
+  std::lock_guard<std::mutex> lock(e->execute_mutex);
+  std::lock_guard<std::mutex> shared(g_noalloc_mutex);
+  return prefill_batch(*e, req.rows, req.gens, req.prompts, req.tables, scratch_ptr, kNoAllocScratchBytes);
 }
 
 namespace {

@@ -310,17 +310,19 @@ class ResidentEpochRuntime:
         if rc != 0:
             raise RuntimeError(f"resident_epoch_prefill failed: {rc}")
 
-    def prefill_batch(self, rows, generations, prompts, block_tables) -> None:
-        """Batched prefill of several rows at once (resident_epoch_prefill_batch):
-        ``prompts`` is a list of token lists, ``block_tables`` [len(rows), BPR]."""
+    def prefill_batch(self, rows, generations, prompts, block_tables, *, noalloc: bool = False) -> None:
+        """Batched prefill of several rows at once (resident_epoch_prefill_batch,
+        or with ``noalloc`` resident_epoch_prefill_batch_noalloc): ``prompts``
+        is a list of token lists, ``block_tables`` [len(rows), BPR]."""
         lens = np.asarray([len(p) for p in prompts], dtype=np.int32)
         flat = np.concatenate([np.asarray(p, dtype=np.int64) for p in prompts]) if len(prompts) else np.zeros(0, np.int64)
         args = [np.asarray(rows, dtype=np.int32), np.asarray(generations, dtype=np.int32), flat, lens,
                 np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32))]
         ptrs = [_ptr(a) for a in args]
-        rc = self.lib.resident_epoch_prefill_batch(self.handle, len(lens), *(p for p, _ in ptrs))
+        name = "resident_epoch_prefill_batch_noalloc" if noalloc else "resident_epoch_prefill_batch"
+        rc = getattr(self.lib, name)(self.handle, len(lens), *(p for p, _ in ptrs))
         if rc != 0:
-            raise RuntimeError(f"resident_epoch_prefill_batch failed: {rc}")
+            raise RuntimeError(f"{name} failed: {rc}")
 
     def execute(
         self,

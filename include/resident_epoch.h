@@ -156,6 +156,25 @@ int32_t resident_epoch_prefill_batch(void *engine, int32_t n_rows,
                                      const int32_t *prompt_lens,
                                      const int32_t *block_tables);
 
+/* resident_epoch_prefill_batch without device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and resulting state as resident_epoch_prefill_batch,
+ * but the pass's activations and token tables live in a fixed 64 MiB device
+ * array of the library (one per GPU, held until the process ends) instead of
+ * the engine's grown-on-demand buffer, and the projections always run on
+ * the hand-written GEMM (hipBLASLt keeps a workspace of its own).  Calls on
+ * one GPU share the array and are serialized; a call leaves its contents
+ * behind.  Return 0, -1 bad arguments, -2 HIP failure, -3 the pass does not
+ * fit the array (about 145 KB per prompt token at Qwen2.5-7B's shape, so
+ * some 460 tokens at most; prompts of one token need none). */
+int32_t resident_epoch_prefill_batch_noalloc(void *engine, int32_t n_rows,
+                                             const int32_t *rows,
+                                             const int32_t *generations,
+                                             const int64_t *prompts,
+                                             const int32_t *prompt_lens,
+                                             const int32_t *block_tables);
+
 /* Named state access (host or device buffers of exactly the named size).
  * Names: any weight of the bundle ("embedding", "layers_3_q_weight", ...),
  * "key_cache", "value_cache" (resident caches [L,P,bs,KVH,d]), "logits"
