@@ -90,6 +90,10 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int32,
         [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_float)],
     ),
+    "resident_epoch_time_layer_op": (
+        ctypes.c_int32,
+        [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_float)],
+    ),
 }
 
 _LIB: ctypes.CDLL | None = None

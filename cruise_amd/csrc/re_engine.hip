@@ -300,6 +300,8 @@ bool make_plan(Engine& e, const Json& cfg) {
   }
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
+    // "down_whole": 0 keeps the split-K down projection and its reduce launch
+    if (t->number_or("down_whole", 1) == 0) p.down_whole_grid = 0;
   }
   p.o_grid = (d.hidden / 2 + p.waves - 1) / p.waves;
   p.down_grid = p.o_grid;
@@ -623,13 +625,16 @@ std::array<int, 3> count_copies(hipGraph_t graph) {
     if (type != hipGraphNodeTypeMemcpy) continue;
     hipMemcpy3DParms p{};
     if (hipGraphMemcpyNodeGetParams(node, &p) != hipSuccess) return {{-1, -1, -1}};
-    const bool src_dev = is_device_ptr(p.srcPtr.ptr), dst_dev = is_device_ptr(p.dstPtr.ptr);
-    if (!src_dev && dst_dev)
-      ++c[0];
-    else if (src_dev && !dst_dev)
-      ++c[1];
-    else
-      ++c[2];
+    int dir = 2;
+    if (p.kind == hipMemcpyHostToDevice) {
+      dir = 0;
+    } else if (p.kind == hipMemcpyDeviceToHost) {
+      dir = 1;
+    } else if (p.kind == hipMemcpyDefault) {  // classify by where the pointers live
+      const bool src_dev = is_device_ptr(p.srcPtr.ptr), dst_dev = is_device_ptr(p.dstPtr.ptr);
+      dir = (!src_dev && dst_dev) ? 0 : (src_dev && !dst_dev) ? 1 : 2;
+    }
+    ++c[dir];
   }
   return c;
 }
@@ -1665,6 +1670,38 @@ extern "C" int32_t resident_epoch_time_ops(void* engine, int32_t begin, int32_t 
   float ms = 0.f;
   if (hipEventElapsedTime(&ms, e->ev_start, e->ev_stop) != hipSuccess) return -2;
   *avg_ms = ms / iters;
+  return 0;
+}
+
+extern "C" int32_t resident_epoch_time_layer_op(void* engine, int32_t which, int32_t passes, float* avg_ms) {
+  using namespace re;
+  Engine* e = static_cast<Engine*>(engine);
+  if (e == nullptr || avg_ms == nullptr || passes < 1) return -1;
+  std::lock_guard<std::mutex> lock(e->execute_mutex);
+  const KernelEnv env = e->env();
+  const int per_layer = (step_op_count(env) - 2) / e->dims.layers;
+  if (which < 0 || which >= per_layer) return -1;
+  if (e->dec_key == nullptr) {
+    if (hipMalloc(&e->dec_key, e->cache_bytes) != hipSuccess) return -2;
+    if (hipMalloc(&e->dec_value, e->cache_bytes) != hipSuccess) return -2;
+    if (hipMemset(e->dec_key, 0, e->cache_bytes) != hipSuccess) return -2;
+    if (hipMemset(e->dec_value, 0, e->cache_bytes) != hipSuccess) return -2;
+  }
+  StepPtrs sp = e->step_io;
+  sp.key_cache = e->dec_key;
+  sp.value_cache = e->dec_value;
+  sp.logits = e->logits;
+  sp.done = nullptr;
+  auto op = [&](int l) { return 1 + per_layer * l + which; };
+  if (launch_step_ops(env, sp, e->stream, op(0), op(0) + 1) != hipSuccess) return -2;  // warm
+  if (hipEventRecord(e->ev_start, e->stream) != hipSuccess) return -2;
+  for (int i = 0; i < passes; ++i)
+    for (int l = 0; l < e->dims.layers; ++l)
+      if (launch_step_ops(env, sp, e->stream, op(l), op(l) + 1) != hipSuccess) return -2;
+  if (hipEventRecord(e->ev_stop, e->stream) != hipSuccess || hipEventSynchronize(e->ev_stop) != hipSuccess) return -2;
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, e->ev_start, e->ev_stop) != hipSuccess) return -2;
+  *avg_ms = ms / (passes * e->dims.layers);
   return 0;
 }
 

@@ -136,6 +136,9 @@ struct LaunchPlan {
   int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
   int slot_w[4];   // their per-slot weights
   int gu_grid_eq, lm_grid_eq;  // the grids for equal ranges
+  // Down projection with the whole K in one workgroup (re_step.hip
+  // k_down_whole): 0 = split-K segments + reduce launch; else its grid.
+  int down_whole_grid;
 };
 
 // Arguments of the paged decode attention (re_attn.hip).

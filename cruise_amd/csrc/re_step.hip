@@ -152,11 +152,12 @@ __device__ __forceinline__ void proj_rows(const ProjArgs& a, int u, const T* W0,
 // pair's weights so the epilogue needs no further memory round trip.
 struct QkvEpi {
   float bias0, bias1, cos, sin;
+  int slot, active;  // the row's paged slot and active flag (key/value rows)
 };
 
 template <typename T>
 __device__ __forceinline__ QkvEpi qkv_epilogue_inputs(const ProjArgs& a, int u, int row0, int row1, int b) {
-  QkvEpi e{0.f, 0.f, 1.f, 0.f};
+  QkvEpi e{0.f, 0.f, 1.f, 0.f, -1, 0};
   const T* bias = static_cast<const T*>(a.w1);
   e.bias0 = Elt<T>::f(bias[row0]);
   e.bias1 = Elt<T>::f(bias[row1]);
@@ -165,6 +166,8 @@ __device__ __forceinline__ QkvEpi qkv_epilogue_inputs(const ProjArgs& a, int u, 
   const int bc = min(b, a.B - 1);
   e.cos = a.rope[((size_t)bc * half + j) * 2];
   e.sin = a.rope[((size_t)bc * half + j) * 2 + 1];
+  e.slot = a.slot[bc];
+  e.active = a.active[bc];
   return e;
 }
 
@@ -263,8 +266,8 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
         } else {
           // Paged slot write (batched_decoder_step.py:250-264): active rows only,
           // slots outside [0, P*bs) write nothing.
-          const int s = a.slot[b];
-          if (a.active[b] != 0 && s >= 0 && s < a.slots) {
+          const int s = epi.slot;
+          if (epi.active != 0 && s >= 0 && s < a.slots) {
             const bool is_key = hg < nq + nkv;
             const int kvh = is_key ? hg - nq : hg - nq - nkv;
             T* cache = static_cast<T*>(is_key ? a.key_cache : a.value_cache) + ((size_t)s * nkv + kvh) * a.head_dim;
@@ -414,6 +417,137 @@ __global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
     resid_segment<T, MB, WAVES, false>(a, xs, red, seg, len);
 }
 
+// ---------------------------------------------------------------------------
+// Down projection with the whole K in one workgroup (bf16, B <= 4):
+// h = T(h + T(x W^T)) (batched_decoder_step.py:399-403) with no fp32
+// partials in global memory and no reduce launch.  One workgroup of 16 waves
+// per CU; workgroup g owns the row pairs [g*ppw, (g+1)*ppw).  The activations
+// x [B, K] are staged into LDS once (4 x 18944 bf16 = 148 KB at Qwen2.5-7B's
+// shape: gfx950 gives a workgroup up to 160 KB).  For one row pair, wave w
+// covers elements [w*K/16, (w+1)*K/16) of both rows in up to three 512-element
+// loads per row; each lane dots its elements against the B rows and the
+// lanes of a wave are combined by the halving exchange into LDS.  After the
+// last pair, one thread per output adds the 16 wave totals in wave order and
+// the residual -- a fixed order, so the results do not depend on timing.
+// The next pair's weights are in flight while a pair is computed (two
+// register sets), and nothing else is requested inside the loop, so every
+// wait there is for the pair being computed; a request past the
+// workgroup's range reads one 16-byte line for the whole wave.
+// ---------------------------------------------------------------------------
+constexpr int kWholeWaves = 16;
+constexpr int kWholeLoads = 3;   // loads per row and wave: K <= 16 * 3 * 512
+constexpr int kWholeStage = 10;  // staged activation vectors per thread: B*K <= 4 * 20480
+
+struct DownWholeArgs {
+  const int32_t* done;
+  const void* x;  // bf16 [B, K]
+  const void* w;  // bf16 [N, K]
+  void* hidden;   // bf16 [B, N]
+  int B, N, K, pairs_per_wg;
+};
+
+// Requests the weights of row pair u (rows 2u, 2u+1) for this wave's K range.
+__device__ __forceinline__ void whole_issue(Vec8<bf16_t> (&w)[kWholeLoads][2], const bf16_t* W, int K, int u,
+                                            int u_end, int k_lo, int span, int lane) {
+  const bool real = u < u_end;
+#pragma unroll
+  for (int j = 0; j < kWholeLoads; ++j) {
+    const int k = min(j * kChunk + lane * 8, span - 8);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const size_t off = real ? (size_t)(2 * u + r) * K + k_lo + k : 0;
+      w[j][r] = Vec8<bf16_t>::load(W + off);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  constexpr int MB = 4;
+  bf16_t* xs = reinterpret_cast<bf16_t*>(smem_raw);  // [MB][K]
+  float* red = reinterpret_cast<float*>(smem_raw + (size_t)MB * a.K * sizeof(bf16_t));  // [ppw][16][8]
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int K = a.K, span = K / kWholeWaves, k_lo = wave * span;
+  const int units = a.N / 2;
+  const int u_begin = blockIdx.x * a.pairs_per_wg;
+  const int u_end = min(u_begin + a.pairs_per_wg, units);
+  if (u_begin >= u_end) return;  // the whole workgroup
+  const bf16_t* W = static_cast<const bf16_t*>(a.w);
+  const bf16_t* X = static_cast<const bf16_t*>(a.x);
+  bf16_t* Hd = static_cast<bf16_t*>(a.hidden);
+
+  // Issue order: the flag, the residual values of this workgroup's outputs
+  // (thread t < 8 x pairs: pair t/8, row (t/4)&1 of the pair, batch row t&3),
+  // the activations, then the first two pairs' weights.
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int nout = (u_end - u_begin) * 8;
+  const int ot = min(tid, nout - 1);
+  const int o_u = u_begin + ot / 8, o_r = (ot >> 2) & 1, o_m = ot & 3;
+  const bf16_t h = Hd[(size_t)min(o_m, a.B - 1) * a.N + 2 * o_u + o_r];
+  const int per_row = K / 8, nvec = MB * per_row;
+  Vec8<bf16_t> xv[kWholeStage];
+#pragma unroll
+  for (int i = 0; i < kWholeStage; ++i) {
+    const int idx = min(tid + 1024 * i, nvec - 1);
+    const int m = idx / per_row;
+    xv[i] = Vec8<bf16_t>::load_cached(X + (size_t)min(m, a.B - 1) * K + (idx - m * per_row) * 8);
+  }
+  Vec8<bf16_t> wa[kWholeLoads][2], wb[kWholeLoads][2];
+  whole_issue(wa, W, K, u_begin, u_end, k_lo, span, lane);
+  whole_issue(wb, W, K, u_begin + 1, u_end, k_lo, span, lane);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kWholeStage; ++i) {
+    const int idx = tid + 1024 * i;
+    if (idx < nvec) *reinterpret_cast<Vec8<bf16_t>*>(xs + idx * 8) = idx / per_row < a.B ? xv[i] : Vec8<bf16_t>{};
+  }
+  lds_barrier();
+  if (stop != 0) return;
+
+  // One pair: products over this wave's range, wave totals to LDS.
+  auto pair = [&](Vec8<bf16_t>(&w)[kWholeLoads][2], int u) {
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[2][MB];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kWholeLoads; ++j) {
+      const int k = j * kChunk + lane * 8;
+      if (k < span) {
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          const Vec8<bf16_t> x = Vec8<bf16_t>::load_cached(xs + m * K + k_lo + k);
+#pragma unroll
+          for (int r = 0; r < 2; ++r) acc[r][m] = dot8(w[j][r], x, acc[r][m]);
+        }
+      }
+    }
+    const int p = min(u, u_end - 1) - u_begin;  // a pair past the range overwrites the last one's totals
+    float totals[2][MB];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) totals[r][m] = u < u_end ? acc[r][m] : 0.f;
+    if (u < u_end) wave_totals<MB, 2>(totals, lane, red + (p * kWholeWaves + wave) * 8);
+  };
+  for (int u = u_begin; u < u_end; u += 2) {
+    pair(wa, u);
+    whole_issue(wa, W, K, u + 2, u_end, k_lo, span, lane);
+    pair(wb, u + 1);
+    whole_issue(wb, W, K, u + 3, u_end, k_lo, span, lane);
+  }
+  lds_barrier();
+  if (tid < nout && o_m < a.B) {
+    const float* t = red + (ot / 8) * kWholeWaves * 8 + o_r * MB + o_m;
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < kWholeWaves; ++q) s += t[q * 8];
+    Hd[(size_t)o_m * a.N + 2 * o_u + o_r] = f_to_bf16(bf16_to_f(h) + round_bf16(s));
+  }
+}
+
 // Sum of the segment partials in segment order, rounded to T, residual add.
 template <typename T>
 __global__ void k_resid_reduce(const int32_t* done, const float* partial, void* hidden, int B, int N,
@@ -434,6 +568,9 @@ __global__ void k_resid_reduce(const int32_t* done, const float* partial, void* 
 // ---------------------------------------------------------------------------
 size_t normed_lds_bytes(int mb, int hidden, int dtype_bytes, int waves) {
   return (size_t)mb * hidden * dtype_bytes + (3 * (size_t)waves * kRowsPerWave + 4) * mb * sizeof(float);
+}
+size_t down_whole_lds_bytes(int K, int pairs_per_wg) {
+  return (size_t)4 * K * sizeof(bf16_t) + (size_t)pairs_per_wg * kWholeWaves * 8 * sizeof(float);
 }
 size_t resid_lds_bytes(int mb, int dtype_bytes, int waves) {
   return (size_t)mb * kSeg * dtype_bytes + (size_t)waves * mb * kRowsPerWave * sizeof(float);
@@ -578,6 +715,24 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     set_slots(gu, p, p.gu_grid);
     if (want()) launch_proj<T, MB, WAVES, kGateUp>(gu, dim3(p.gu_grid, p.row_tiles), proj_smem, stream);
 
+    if constexpr (sizeof(T) == 2 && MB == 4) {
+      if (p.down_whole_grid > 0) {
+        DownWholeArgs dw{};
+        dw.done = st.done;
+        dw.x = sc.mlp;
+        dw.w = env.weights + lo.down_w;
+        dw.hidden = sc.hidden;
+        dw.B = B;
+        dw.N = d.hidden;
+        dw.K = d.intermediate;
+        dw.pairs_per_wg = (d.hidden / 2 + p.down_whole_grid - 1) / p.down_whole_grid;
+        if (want())
+          k_down_whole<<<p.down_whole_grid, kWholeWaves * 64, down_whole_lds_bytes(d.intermediate, dw.pairs_per_wg),
+                         stream>>>(dw);
+        (void)want();  // the reduce entry: nothing to reduce
+        continue;
+      }
+    }
     ResidArgs dn{};
     dn.done = st.done;
     dn.x = sc.mlp;
@@ -631,6 +786,7 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
   const bool full = d.hidden == kSeg;
   p.qkv_grid = fit(full ? k_proj<T, MB, WAVES, kQkv, true> : k_proj<T, MB, WAVES, kQkv, false>,
                    (d.qkv_rows() / 2 + WAVES - 1) / WAVES);
+  p.slot_cus = 0;
   p.gu_grid = fit(full ? k_proj<T, MB, WAVES, kGateUp, true> : k_proj<T, MB, WAVES, kGateUp, false>,
                   (d.intermediate + WAVES - 1) / WAVES);
   p.lm_grid = fit(full ? k_proj<T, MB, WAVES, kLmHead, true> : k_proj<T, MB, WAVES, kLmHead, false>,
@@ -639,7 +795,6 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
   // CU (bf16, one row tile): 1 : 1 : 0.9 : 0.8 measured best on MI355X.
   p.gu_grid_eq = p.gu_grid;
   p.lm_grid_eq = p.lm_grid;
-  p.slot_cus = 0;
   int per_cu = 0;
   if (sizeof(T) == 2 && p.row_tiles == 1 &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -653,6 +808,17 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
     p.lm_grid = 4 * cus;
   }
   p.lm_wg = p.lm_grid;
+  // The whole-K down projection: bf16, one row tile of at most four rows,
+  // K a multiple of 16 x 8 within three loads per wave, activations in LDS.
+  p.down_whole_grid = 0;
+  const int whole_grid = std::min(cus, d.hidden / 2);
+  const size_t whole_lds = down_whole_lds_bytes(d.intermediate, (d.hidden / 2 + whole_grid - 1) / whole_grid);
+  if (sizeof(T) == 2 && MB == 4 && p.row_tiles == 1 && d.intermediate % (kWholeWaves * 8) == 0 &&
+      d.intermediate / kWholeWaves <= kWholeLoads * kChunk && d.hidden % 2 == 0 && whole_lds <= 160 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k_down_whole), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(whole_lds)) == hipSuccess) {
+    p.down_whole_grid = whole_grid;
+  }
 }
 
 void plan_grids(LaunchPlan& p, const Dims& d, int cus) {

@@ -392,6 +392,17 @@ class ResidentEpochRuntime:
             raise RuntimeError(f"time_ops failed: {rc}")
         return float(out.value)
 
+    LAYER_OPS = ("qkv", "attention", "o_proj", "o_reduce", "gate_up", "down", "down_reduce")
+
+    def time_layer_op(self, which: str, passes: int = 2) -> float:
+        """Mean ms of one layer op launched for every layer in turn, back to
+        back (resident_epoch_time_layer_op: each launch streams cold weights)."""
+        out = ctypes.c_float(0.0)
+        rc = self.lib.resident_epoch_time_layer_op(self.handle, self.LAYER_OPS.index(which), passes, ctypes.byref(out))
+        if rc != 0:
+            raise RuntimeError(f"time_layer_op failed: {rc}")
+        return float(out.value)
+
     def op_index(self, layer: int, which: str) -> int:
         """Index of one launch in the step's launch list."""
         order = ("qkv", "attention", "o_proj", "o_reduce", "gate_up", "down", "down_reduce")

@@ -219,6 +219,17 @@ int32_t resident_epoch_read_kernel_timing(void *engine, float *ms, int32_t n);
  * Return 0, -1 bad arguments, -2 HIP failure. */
 int32_t resident_epoch_time_ops(void *engine, int32_t begin, int32_t end, int32_t iters, float *avg_ms);
 
+/* Microbenchmark with cold weights: launches op `which` of the per-layer
+ * launch list (0 qkv, 1 attention, 2 o-proj, 3 o-reduce, 4 gate/up, 5 down,
+ * 6 down-reduce) for layer 0, 1, ..., L-1 in turn, `passes` times, back to
+ * back on the engine stream between two HIP events, on the same inputs as
+ * resident_epoch_time_ops.  Each launch streams another layer's weights, so
+ * none of them is left in the memory-side cache by the launch before (at
+ * Qwen2.5-7B's shape a layer's gate/up weights are 272 MB, the cache 256 MB).
+ * *avg_ms receives the mean time per launch.  Return 0, -1 bad arguments,
+ * -2 HIP failure. */
+int32_t resident_epoch_time_layer_op(void *engine, int32_t which, int32_t passes, float *avg_ms);
+
 #ifdef __cplusplus
 }
 #endif
