@@ -195,10 +195,9 @@ int32_t resident_epoch_write_state(void *engine, const char *name,
  * "step_ops" (entries of a decoder step's launch list), "ops_per_layer",
  * "timing_layer", launch-plan sizes ("qkv_grid", "gateup_grid", "lm_grid",
  * "o_segments", "down_segments", "gemv_rows_per_pass"), "compute_units",
- * and the memory copies of the last epoch launched, counted from the nodes of
- * its captured graph(s): "epoch_h2d_copies", "epoch_d2h_copies",
- * "epoch_other_copies" (device-to-device copies and memsets; -1 before the
- * first epoch).  Return 0 or -1 for an unknown key. */
+ * and the nodes of the last epoch launched, counted from its captured
+ * graph(s): "epoch_memcpy_nodes", "epoch_memset_nodes", "epoch_kernel_nodes"
+ * (-1 before the first epoch).  Return 0 or -1 for an unknown key. */
 int32_t resident_epoch_info(void *engine, const char *key, int64_t *value);
 
 /* Kernel timing in the epoch: when enabled, each epoch runs as graph part 1,
