@@ -116,7 +116,16 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     return _LIB
 
 
-def _bind(path: Path) -> ctypes.CDLL:
+BRIDGE_SYMBOLS = ("resident_epoch_create", "resident_epoch_execute", "resident_epoch_destroy")
+
+
+def load_bridge(path: Path) -> ctypes.CDLL:
+    """A library that exports the three bridge entry points (the reference
+    bridge's whole C-ABI), bound without the engine's other symbols."""
+    return _bind(Path(path), BRIDGE_SYMBOLS)
+
+
+def _bind(path: Path, symbols=None) -> ctypes.CDLL:
     # PyTorch-ROCm ships its own libamdhip64.so.7.  Importing it first makes
     # the library bind that same HIP runtime (same soname), so torch tensors
     # and the engine share one runtime and one device context per process.
@@ -130,7 +139,8 @@ def _bind(path: Path) -> ctypes.CDLL:
             "or __graft_entry__.build() first"
         )
     lib = ctypes.CDLL(str(path))
-    for name, (restype, argtypes) in SIGNATURES.items():
+    for name in symbols or SIGNATURES:
+        restype, argtypes = SIGNATURES[name]
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes

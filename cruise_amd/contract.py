@@ -1,29 +1,38 @@
 """The scheduler <-> worker contract of a resident epoch.
 
-Mirrors src/vllm_ascend_resident_epoch/contract.py: the plan the scheduler
-attaches to its output (one request per resident row), the result the
-worker attaches to the model-runner output, the three commit states and the
-execution error that carries them.  Field names, validation rules and the
-wording of the rejections are the reference's, so its scheduler, worker and
-tests read these objects unchanged.
+Interface kept from src/vllm_ascend_resident_epoch/contract.py so that a
+scheduler, worker or test written against the reference reads these objects
+unchanged: the attribute names the plan and the result travel under
+(contract.py:7-8), the three commit states (13-16), the execution error and
+its ``input_preserving`` property (19-33), and the field names of the
+request, plan and result records (36-136).  The same conditions are
+rejected, always with ValueError (contract.py:75-112 for a plan, 138-214 for
+a result).
+
+The rules themselves are data here: each is a named predicate in an ordered
+table, ``validate`` reports the first one broken as a ContractViolation (a
+ValueError) whose ``rule`` attribute names it, and ``violations`` lists every
+broken rule at once for diagnostics.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
 from enum import IntEnum
-from typing import Any, Literal
+from typing import Any, Callable, Iterator, Literal
 
 from .version import PYTHON_CONTRACT_VERSION
 
 PLAN_ATTR = "_ascend_resident_epoch_plan"
 RESULT_ATTR = "_ascend_resident_epoch_result"
 CONTRACT_VERSION = PYTHON_CONTRACT_VERSION
+GRAPH_BATCH_SIZES = (1, 2, 4)
+TRANSFER_MODES = ("none", "host_snapshot", "device_ipc")
 
 
 class EpochCommitState(IntEnum):
-    """How far an epoch got (contract.py:13-16): PREPARED means nothing
-    reached the device, EXECUTING that the device may have run, COMMITTED
-    that the outputs were fetched and unpacked."""
+    """How far an epoch got.  PREPARED: nothing reached the device, the host
+    state is intact.  EXECUTING: the device may have run.  COMMITTED: the
+    outputs were fetched and unpacked."""
 
     PREPARED = 0
     EXECUTING = 1
@@ -31,9 +40,9 @@ class EpochCommitState(IntEnum):
 
 
 class ResidentEpochExecutionError(RuntimeError):
-    """An epoch failure together with the commit state it reached
-    (contract.py:19-33).  Only a PREPARED failure leaves the host state
-    intact, so only it may be replayed on the host."""
+    """An epoch failure and the commit state it reached.  Only a PREPARED
+    failure leaves the host's copy of the requests valid, so only it may be
+    replayed on the host."""
 
     def __init__(self, message: str, *, commit_state: EpochCommitState, status: int | None = None) -> None:
         super().__init__(message)
@@ -45,14 +54,31 @@ class ResidentEpochExecutionError(RuntimeError):
         return self.commit_state == EpochCommitState.PREPARED
 
 
-def _check(condition: bool, message: str) -> None:
-    if not condition:
-        raise ValueError(message)
+class ContractViolation(ValueError):
+    """A broken contract rule; ``rule`` is its name in the rule tables."""
+
+    def __init__(self, rule: str, detail: str) -> None:
+        super().__init__(f"[{rule}] {detail}")
+        self.rule = rule
+
+
+# A rule: (name, predicate that holds for a valid record, what a violation means).
+Rule = tuple[str, Callable[..., bool], str]
+
+
+def _broken(rules: tuple[Rule, ...], *record: Any) -> Iterator[ContractViolation]:
+    """The violations of ``rules`` in table order.  A rule is only evaluated
+    once every earlier one holds, so later predicates may rely on them; the
+    iteration therefore stops at the first violation."""
+    for name, holds, detail in rules:
+        if not holds(*record):
+            yield ContractViolation(name, detail)
+            return
 
 
 @dataclass(frozen=True)
 class ResidentEpochRequest:
-    """One resident row of a plan (contract.py:36-48)."""
+    """One resident row of a plan."""
 
     req_id: str
     row: int
@@ -67,9 +93,54 @@ class ResidentEpochRequest:
     kv_import_required: bool = False
 
 
+def _distinct(values) -> bool:
+    values = list(values)
+    return len(set(values)) == len(values)
+
+
+def _occupancy(plan: "ResidentEpochPlan") -> tuple[int, ...]:
+    rows = {r.row for r in plan.requests}
+    return tuple(int(row in rows) for row in range(plan.graph_batch_size))
+
+
+PLAN_RULES: tuple[Rule, ...] = (
+    ("contract-version", lambda p: p.version == CONTRACT_VERSION,
+     f"the plan is not written for contract version {CONTRACT_VERSION}"),
+    ("graph-batch", lambda p: p.graph_batch_size in GRAPH_BATCH_SIZES,
+     f"graph batch size must be one of {GRAPH_BATCH_SIZES}"),
+    ("request-count", lambda p: 0 < len(p.requests) <= p.graph_batch_size,
+     "a plan carries between one request and one request per graph row"),
+    ("mask-length", lambda p: len(p.active_mask) == p.graph_batch_size,
+     "the active mask needs one entry per graph row"),
+    ("mask-binary", lambda p: set(p.active_mask) <= {0, 1},
+     "active mask entries are 0 or 1"),
+    ("request-ids", lambda p: _distinct(p.req_ids),
+     "a request appears at most once in a plan"),
+    ("row-ids", lambda p: _distinct(r.row for r in p.requests),
+     "two requests of a plan share a resident row"),
+    ("generation-positive", lambda p: all(r.generation > 0 for r in p.requests),
+     "resident generations start at 1"),
+    ("generation-ids", lambda p: _distinct(r.generation for r in p.requests),
+     "two requests of a plan share a generation"),
+    ("row-range", lambda p: all(0 <= r.row < p.graph_batch_size for r in p.requests),
+     "a request's row lies outside the graph"),
+    ("length-position", lambda p: all(r.sequence_length == r.position + 1 for r in p.requests),
+     "a request's sequence length must be its position plus one"),
+    ("state-owner", lambda p: all(r.state_owner in ("host", "device") for r in p.requests),
+     "state_owner is 'host' or 'device'"),
+    ("import-owner", lambda p: all(r.state_owner == "host" for r in p.requests if r.kv_import_required),
+     "only a request whose state the host still owns can have its KV imported"),
+    ("capacity", lambda p: all(r.position + p.max_steps <= p.logical_capacity for r in p.requests),
+     "position + max_steps exceeds the logical capacity of a row"),
+    ("mask-rows", lambda p: _occupancy(p) == tuple(p.active_mask),
+     "the active mask must mark exactly the rows the requests occupy"),
+)
+
+
 @dataclass(frozen=True)
 class ResidentEpochPlan:
-    """What one epoch must do (contract.py:51-112)."""
+    """What one epoch must do: K = ``max_steps`` decoder steps over the
+    requests, each on its own row of a ``graph_batch_size``-row graph."""
 
     version: int
     graph_batch_size: Literal[1, 2, 4]
@@ -94,32 +165,94 @@ class ResidentEpochPlan:
     def host_replay_safe(self) -> bool:
         return all(r.state_owner == "host" for r in self.requests)
 
+    def violations(self) -> list[ContractViolation]:
+        return list(_broken(PLAN_RULES, self))
+
     def validate(self) -> None:
-        _check(self.version == CONTRACT_VERSION, f"unsupported resident epoch contract {self.version}")
-        _check(self.graph_batch_size in (1, 2, 4), "graph batch size must be 1, 2, or 4")
-        _check(1 <= len(self.requests) <= self.graph_batch_size, "request count does not fit the static graph")
-        _check(len(self.active_mask) == self.graph_batch_size, "active mask does not match graph batch size")
-        _check(all(v in (0, 1) for v in self.active_mask), "active mask must contain only zero or one")
-        _check(len(set(self.req_ids)) == len(self.requests), "request IDs must be unique")
-        rows = [r.row for r in self.requests]
-        _check(len(set(rows)) == len(rows), "resident rows must be unique")
-        gens = [r.generation for r in self.requests]
-        _check(all(g > 0 for g in gens), "resident generations must be positive")
-        _check(len(set(gens)) == len(gens), "resident generations must be unique")
-        occupied = [0] * self.graph_batch_size
-        for r in self.requests:
-            _check(0 <= r.row < self.graph_batch_size, "resident row is outside the static graph")
-            occupied[r.row] = 1
-            _check(r.sequence_length == r.position + 1, "sequence length and position disagree")
-            _check(r.state_owner in ("host", "device"), "resident request has an invalid state owner")
-            _check(not r.kv_import_required or r.state_owner == "host", "KV import requires Host-owned request state")
-            _check(r.position + self.max_steps <= self.logical_capacity, "epoch exceeds logical capacity")
-        _check(tuple(occupied) == tuple(self.active_mask), "active mask does not match resident rows")
+        for violation in _broken(PLAN_RULES, self):
+            raise violation
+
+
+def _steps_ok(res, plan, tokens) -> bool:
+    return all(1 <= res.computed_steps[r.req_id] <= plan.max_steps for r in plan.requests)
+
+
+def _counts_ok(res, plan, tokens) -> bool:
+    return all(len(tokens[r.req_id]) == res.computed_steps[r.req_id] for r in plan.requests)
+
+
+def _short_rows_end_at_eos(res, plan, tokens) -> bool:
+    """A device row that ran fewer than K steps stopped because it sampled
+    its EOS token."""
+    for r in plan.requests:
+        if res.computed_steps[r.req_id] < plan.max_steps:
+            row_tokens = tokens[r.req_id]
+            if not row_tokens or row_tokens[-1] != r.eos_token_id:
+                return False
+    return True
+
+
+def _device(rule: Callable[..., bool]) -> Callable[..., bool]:
+    return lambda res, plan, tokens: res.route != "device" or rule(res, plan, tokens)
+
+
+def _fallback(rule: Callable[..., bool]) -> Callable[..., bool]:
+    return lambda res, plan, tokens: res.route != "host_fallback" or rule(res, plan, tokens)
+
+
+RESULT_RULES: tuple[Rule, ...] = (
+    # what the result is about
+    ("result-version", lambda res, plan, tok: res.version == plan.version,
+     "the result answers a different contract version than the plan"),
+    ("result-requests", lambda res, plan, tok: set(res.computed_steps) == set(plan.req_ids),
+     "computed_steps must name exactly the plan's requests"),
+    ("output-requests", lambda res, plan, tok: set(tok) == set(plan.req_ids),
+     "the sampled tokens must name exactly the plan's requests"),
+    # a device epoch: one complete, committed run of the planned rows
+    ("device-status", _device(lambda res, plan, tok: res.status == 0),
+     "a device epoch with a non-zero status cannot be committed"),
+    ("device-committed", _device(lambda res, plan, tok: res.commit_state == EpochCommitState.COMMITTED),
+     "a device epoch's result must be in the COMMITTED state"),
+    ("device-round-trip", _device(lambda res, plan, tok: (res.feed_calls, res.fetch_calls) == (1, 1)),
+     "a device epoch is one feed and one fetch"),
+    ("device-generations", _device(lambda res, plan, tok: tuple(res.row_generations) == plan.row_generations),
+     "the generations the device acknowledged differ from the plan's"),
+    ("device-import", _device(lambda res, plan, tok: res.kv_imported
+                              or not any(r.kv_import_required for r in plan.requests)),
+     "the plan asked for a KV import that the device did not perform"),
+    # an imported KV transfer must prove itself
+    ("import-proof", lambda res, plan, tok: not res.kv_imported
+     or (res.kv_import_checksum != 0 and res.transfer_mode in ("host_snapshot", "device_ipc")),
+     "an imported KV transfer needs a non-zero checksum and a transfer mode"),
+    ("snapshot-proof", lambda res, plan, tok: not (res.kv_imported and res.transfer_mode == "host_snapshot")
+     or (res.kv_snapshot_checksum != 0 and res.kv_import_checksum == res.kv_snapshot_checksum),
+     "the checksum of the imported KV differs from the host snapshot's"),
+    ("transfer-without-import", lambda res, plan, tok: res.kv_imported or res.transfer_mode == "none",
+     "a transfer mode is set although nothing was imported"),
+    # a host fallback: nothing reached the device and the host may replay
+    ("fallback-declared", _fallback(lambda res, plan, tok: res.fallback_safe),
+     "a host fallback must be declared input-preserving"),
+    ("fallback-prepared", _fallback(lambda res, plan, tok: res.commit_state == EpochCommitState.PREPARED),
+     "a host fallback is only possible from the PREPARED state"),
+    ("fallback-host-owned", _fallback(lambda res, plan, tok: plan.host_replay_safe),
+     "a host fallback needs every request's state on the host"),
+    ("fallback-no-dataflow", _fallback(lambda res, plan, tok: (res.feed_calls, res.fetch_calls) == (0, 0)),
+     "a host fallback performed no feed or fetch"),
+    # per request
+    ("steps-range", _steps_ok, "each request runs between 1 and max_steps steps"),
+    ("steps-tokens", _counts_ok, "each request samples one token per computed step"),
+    ("fallback-one-step", _fallback(lambda res, plan, tok: set(res.computed_steps.values()) == {1}),
+     "a host fallback keeps vLLM's one step per request"),
+    ("short-row-eos", _device(_short_rows_end_at_eos),
+     "a device row that stopped before K steps must end with its EOS token"),
+    ("device-model-calls", _device(lambda res, plan, tok: res.model_calls == max(res.computed_steps.values())),
+     "the device's decoder-step count must equal the longest row's steps"),
+)
 
 
 @dataclass(frozen=True)
 class ResidentEpochResult:
-    """What an epoch did (contract.py:115-214)."""
+    """What an epoch did, attached to the model-runner output."""
 
     version: int
     route: Literal["device", "host_fallback"]
@@ -142,54 +275,22 @@ class ResidentEpochResult:
     kv_snapshot_checksum: int = 0
     kv_transfer_mode: Literal["none", "host_snapshot", "device_ipc"] = "none"
 
+    @property
+    def transfer_mode(self) -> str:
+        """The transfer mode in effect: an import recorded without a mode
+        came from a host snapshot."""
+        if self.kv_imported and self.kv_transfer_mode == "none":
+            return "host_snapshot"
+        return self.kv_transfer_mode
+
+    def violations(self, plan: ResidentEpochPlan, sampled_token_ids: dict[str, list[int]]) -> list[ContractViolation]:
+        return list(_broken(RESULT_RULES, self, plan, sampled_token_ids))
+
     def validate_against(self, plan: ResidentEpochPlan, sampled_token_ids: dict[str, list[int]]) -> None:
-        """Every rule a committed or host-replayed epoch must satisfy before
-        the scheduler advances its accounting (contract.py:138-214)."""
-        device = self.route == "device"
-        fallback = self.route == "host_fallback"
-        _check(self.version == plan.version, "resident epoch result version mismatch")
-        _check(set(self.computed_steps) == set(plan.req_ids), "resident epoch result request set mismatch")
-        _check(set(sampled_token_ids) == set(plan.req_ids), "resident epoch output request set mismatch")
-        if device:
-            _check(self.status == 0, "failed device execution cannot be committed")
-            _check(self.commit_state == EpochCommitState.COMMITTED, "device execution result is not committed")
-            _check(self.feed_calls == 1 and self.fetch_calls == 1, "device epoch must use exactly one Feed and one Fetch")
-            _check(self.row_generations == plan.row_generations, "device resident generations disagree with the plan")
-            importing = any(r.kv_import_required for r in plan.requests)
-            _check(not importing or self.kv_imported, "device result did not commit the requested KV import")
-        # A result that imported without naming a mode came from a host snapshot.
-        mode = "host_snapshot" if self.kv_imported and self.kv_transfer_mode == "none" else self.kv_transfer_mode
-        if self.kv_imported:
-            _check(
-                self.kv_import_checksum != 0 and mode in ("host_snapshot", "device_ipc"),
-                "device result did not prove an imported KV transfer",
-            )
-            if mode == "host_snapshot":
-                _check(
-                    self.kv_snapshot_checksum != 0 and self.kv_import_checksum == self.kv_snapshot_checksum,
-                    "device result did not prove equivalent imported KV from the Host snapshot",
-                )
-        else:
-            _check(mode == "none", "KV transfer mode is set without an import")
-        if fallback:
-            _check(self.fallback_safe, "host fallback must be declared input-preserving")
-            _check(self.commit_state == EpochCommitState.PREPARED, "host fallback requires a prepared device state")
-            _check(plan.host_replay_safe, "Host no longer owns every request state")
-            _check(self.feed_calls == 0 and self.fetch_calls == 0, "Host fallback result cannot claim DataFlow calls")
-        for r in plan.requests:
-            steps = self.computed_steps[r.req_id]
-            tokens = sampled_token_ids[r.req_id]
-            _check(1 <= steps <= plan.max_steps, "computed step count is outside the epoch")
-            _check(len(tokens) == steps, "sampled token count and computed steps disagree")
-            if fallback:
-                _check(steps == 1, "host fallback must retain one-step vLLM semantics")
-            if device and steps < plan.max_steps:
-                _check(bool(tokens) and tokens[-1] == r.eos_token_id, "a short device epoch must terminate at EOS")
-        if device:
-            _check(
-                self.model_calls == max(self.computed_steps.values()),
-                "device model-call count disagrees with executed steps",
-            )
+        """Every rule an epoch result must satisfy before the scheduler
+        advances its accounting; raises the first violation."""
+        for violation in _broken(RESULT_RULES, self, plan, sampled_token_ids):
+            raise violation
 
 
 def attach_plan(scheduler_output: Any, plan: ResidentEpochPlan) -> None:
@@ -198,10 +299,7 @@ def attach_plan(scheduler_output: Any, plan: ResidentEpochPlan) -> None:
 
 
 def get_plan(scheduler_output: Any) -> ResidentEpochPlan | None:
-    plan = getattr(scheduler_output, PLAN_ATTR, None)
-    if plan is not None and not isinstance(plan, ResidentEpochPlan):
-        raise TypeError("invalid resident epoch plan attached to SchedulerOutput")
-    return plan
+    return _typed_attr(scheduler_output, PLAN_ATTR, ResidentEpochPlan, "SchedulerOutput")
 
 
 def attach_result(model_runner_output: Any, result: ResidentEpochResult) -> None:
@@ -209,7 +307,11 @@ def attach_result(model_runner_output: Any, result: ResidentEpochResult) -> None
 
 
 def get_result(model_runner_output: Any) -> ResidentEpochResult | None:
-    result = getattr(model_runner_output, RESULT_ATTR, None)
-    if result is not None and not isinstance(result, ResidentEpochResult):
-        raise TypeError("invalid resident epoch result attached to ModelRunnerOutput")
-    return result
+    return _typed_attr(model_runner_output, RESULT_ATTR, ResidentEpochResult, "ModelRunnerOutput")
+
+
+def _typed_attr(holder: Any, attr: str, kind: type, holder_name: str):
+    value = getattr(holder, attr, None)
+    if value is not None and not isinstance(value, kind):
+        raise TypeError(f"{holder_name}.{attr} holds a {type(value).__name__}, not a {kind.__name__}")
+    return value

@@ -1,14 +1,33 @@
-"""Sidecar engine: the resident epoch served by ``resident_epoch_server`` in
-its own process, driven over a Unix socket.
+"""Sidecar engine: the resident epoch served by ``resident_epoch_server`` in a
+process of its own, driven over a Unix stream socket.
 
-Mirrors src/vllm_ascend_resident_epoch/sidecar_backend.py:23-466: the same
-environment variables, wire records (136-byte request ``<IHHiiQ4q4q4i4i4i``,
-352-byte response ``<Iiiiiiii4q4i4i32q``, protocol 7), operations, warm-up
-request, startup handshake and shutdown escalation.  The server binary
-defaults to the one built into this package (cruise_amd/lib/
-resident_epoch_server) when VLLM_ASCEND_RESIDENT_EPOCH_SERVER is unset.
-The reference's Ascend-only child settings (custom operator path, memcpy
-trace preload) have no MI355X counterpart and are not read.
+Interface kept from src/vllm_ascend_resident_epoch/sidecar_backend.py so the
+reference's worker configuration works unchanged:
+
+* the wire records (protocol 7): a 136-byte request ``<IHHiiQ4q4q4i4i4i``
+  (magic 0x71317131, version, operation, request count, K, transfer id, then
+  token/position/length/EOS/generation per row) and a 352-byte response
+  ``<Iiiiiiii4q4i4i32q`` (magic 0x71327132, transport status, device status,
+  model calls, feeds, fetches, commit state, checksum, wall/CPU microseconds,
+  declared bytes, executed and generations per row, token history), with
+  operations 1 execute, 2 warm-up, 3 shutdown, 4 import-execute, 5
+  device-IPC execute (whose request is followed by the 4,088-byte IPC
+  record) (sidecar_backend.py:23-36);
+* the startup handshake: the server answers a response with transport
+  status 0, or 100 + its create status, before taking requests;
+* the environment: VLLM_ASCEND_RESIDENT_EPOCH_{SERVER, AIR, GRAPH_CONFIG,
+  FUNC_CONFIG, TILING, EXTERNAL_WEIGHTS, SOCKET, CHILD_LIBRARY_PATH,
+  STARTUP_TIMEOUT}; the socket, the weights and the KV transfer file live
+  under /dev/shm.  SERVER defaults to the server built into this package.
+  The Ascend-only child settings (custom operator path, memcpy trace
+  preload) have no counterpart on this platform and are not read.
+
+Structure: ``SidecarLaunch`` resolves the environment into a launch
+description, ``SidecarLink`` frames records over the socket, and
+``SidecarDataFlowEngine`` spawns the server and turns plans into records
+through the shared feed/fetch codec (epoch_io.py).  Any failure between
+sending a request and reading its whole answer is EXECUTING: the device may
+or may not have run.
 """
 from __future__ import annotations
 
@@ -17,289 +36,269 @@ import socket
 import struct
 import subprocess
 import time
+from dataclasses import dataclass
 from pathlib import Path
 
 from .backend import NativeEpochOutput, NativeWarmupOutput
 from .contract import EpochCommitState, ResidentEpochExecutionError, ResidentEpochPlan
+from .epoch_io import (
+    DEFAULT_EOS,
+    MAX_EPOCH_STEPS,
+    ROWS,
+    WARMUP_GENERATION,
+    WARMUP_TOKEN,
+    EpochFeed,
+    EpochFetch,
+    check_transfer,
+)
 from .kv_transfer import IPC_METADATA_BYTES, DeviceKVTransfer, ResidentKVSnapshot, write_kv_snapshot
 from .version import SIDECAR_PROTOCOL_VERSION
 
 REQUEST_MAGIC = 0x71317131
 RESPONSE_MAGIC = 0x71327132
 PROTOCOL_VERSION = SIDECAR_PROTOCOL_VERSION
-EXECUTE = 1
-WARM_UP = 2
-SHUTDOWN = 3
-IMPORT_EXECUTE = 4
-DEVICE_IPC_EXECUTE = 5
-GRAPH_BATCH_SIZE = 4
-MAX_EPOCH_STEPS = 8
-WARMUP_GENERATION = 2**31 - 1
-WARMUP_TOKEN = 11690
-DEFAULT_EOS = 151645
+EXECUTE, WARM_UP, SHUTDOWN, IMPORT_EXECUTE, DEVICE_IPC_EXECUTE = 1, 2, 3, 4, 5
+GRAPH_BATCH_SIZE = ROWS
 REQUEST = struct.Struct("<IHHiiQ4q4q4i4i4i")
 RESPONSE = struct.Struct("<Iiiiiiii4q4i4i32q")
 
 DEFAULT_SERVER = Path(__file__).resolve().parent / "lib" / "resident_epoch_server"
+SHM = "/dev/shm/"
+ENV = "VLLM_ASCEND_RESIDENT_EPOCH_"
 
-# Response field positions (RESPONSE.unpack order).
-_TRANSPORT, _DEVICE, _CALLS, _FEEDS, _FETCHES, _COMMIT, _CHECKSUM = 1, 2, 3, 4, 5, 6, 7
-_WALL, _CPU, _IN_BYTES, _OUT_BYTES = 8, 9, 10, 11
-_EXECUTED = slice(12, 16)
-_GENERATIONS = slice(16, 20)
-_TOKENS = slice(20, 20 + GRAPH_BATCH_SIZE * MAX_EPOCH_STEPS)
-
-
-def _commit_state(value: int) -> EpochCommitState:
-    try:
-        return EpochCommitState(value)
-    except ValueError as exc:
-        raise ResidentEpochExecutionError(
-            f"sidecar returned invalid commit state {value}", commit_state=EpochCommitState.EXECUTING
-        ) from exc
+__all__ = [
+    "DEFAULT_EOS", "DEVICE_IPC_EXECUTE", "EXECUTE", "GRAPH_BATCH_SIZE", "IMPORT_EXECUTE", "MAX_EPOCH_STEPS",
+    "PROTOCOL_VERSION", "REQUEST", "REQUEST_MAGIC", "RESPONSE", "RESPONSE_MAGIC", "SHUTDOWN", "WARMUP_GENERATION",
+    "WARMUP_TOKEN", "WARM_UP", "SidecarDataFlowEngine", "SidecarLaunch", "SidecarLink", "create_sidecar_engine",
+    "decode_response", "encode_request",
+]
 
 
-def _env_path(name: str, *, directory: bool = False, default: Path | None = None) -> Path:
-    raw = os.getenv(name)
+def encode_request(operation: int, feed: EpochFeed, transfer_id: int = 0) -> bytes:
+    return REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION, operation, feed.request_count, feed.max_steps, transfer_id,
+                        *feed.tokens, *feed.positions, *feed.lengths, *feed.eos, *feed.generations)
+
+
+def decode_response(record: bytes) -> EpochFetch:
+    v = RESPONSE.unpack(record)
+    if v[0] != RESPONSE_MAGIC:
+        raise RuntimeError(f"sidecar response starts with {v[0]:#010x}, not the response magic")
+    return EpochFetch(
+        transport_status=v[1], device_status=v[2], model_calls=v[3], feed_calls=v[4], fetch_calls=v[5],
+        commit_code=v[6], checksum=v[7], wall_us=v[8], native_cpu_us=v[9], declared_input_bytes=v[10],
+        declared_output_bytes=v[11], executed=tuple(v[12:16]), generations=tuple(v[16:20]),
+        history=tuple(v[20:20 + ROWS * MAX_EPOCH_STEPS]), source="resident epoch sidecar",
+    )
+
+
+def _existing(name: str, *, directory: bool = False, default: Path | None = None) -> Path:
+    raw = os.getenv(ENV + name)
     if not raw and default is None:
-        raise RuntimeError(f"{name} is required by the resident epoch sidecar")
+        raise RuntimeError(f"{ENV}{name} must be set for the resident epoch sidecar")
     path = Path(raw).resolve() if raw else default
     if not (path.is_dir() if directory else path.is_file()):
-        raise RuntimeError(f"{name} must name an existing {'directory' if directory else 'file'}: {path}")
+        raise RuntimeError(f"{ENV}{name}: {path} is not an existing {'directory' if directory else 'file'}")
     return path
 
 
-def _by_row(plan: ResidentEpochPlan, field: str, fill: int) -> list[int]:
-    values = [fill] * GRAPH_BATCH_SIZE
-    for r in plan.requests:
-        values[r.row] = int(getattr(r, field))
-    return values
+@dataclass(frozen=True)
+class SidecarLaunch:
+    """Everything needed to start the server: its argv (socket, then the
+    five create arguments), its environment and the startup timeout."""
+
+    server: Path
+    socket_path: Path
+    create_args: tuple[Path, ...]
+    env: dict
+    startup_timeout: float
+
+    @property
+    def transfer_path(self) -> Path:
+        """The host-snapshot file of import-execute requests, beside the
+        socket."""
+        return self.socket_path.with_name(self.socket_path.name + ".kv-transfer")
+
+    @property
+    def argv(self) -> list[str]:
+        return [str(self.server), str(self.socket_path), *map(str, self.create_args)]
+
+    @classmethod
+    def from_env(cls) -> "SidecarLaunch":
+        server = _existing("SERVER", default=DEFAULT_SERVER)
+        create_args = (_existing("AIR"), _existing("GRAPH_CONFIG"), _existing("FUNC_CONFIG"),
+                       _existing("EXTERNAL_WEIGHTS", directory=True), _existing("TILING"))
+        raw_socket = os.getenv(ENV + "SOCKET")
+        if not raw_socket:
+            raise RuntimeError(f"{ENV}SOCKET must name the sidecar's socket")
+        socket_path = Path(raw_socket).resolve()
+        env = dict(os.environ)
+        extra = os.getenv(ENV + "CHILD_LIBRARY_PATH")
+        if extra:
+            roots = [Path(p).resolve() for p in extra.split(":")]
+            missing = [str(p) for p in roots if not p.is_dir()]
+            if missing:
+                raise RuntimeError(f"{ENV}CHILD_LIBRARY_PATH names missing directories: {missing}")
+            env["LD_LIBRARY_PATH"] = ":".join([*map(str, roots), *filter(None, [env.get("LD_LIBRARY_PATH")])])
+        launch = cls(server, socket_path, create_args, env,
+                     float(os.getenv(ENV + "STARTUP_TIMEOUT", "3600")))
+        for what, path in (("socket", socket_path), ("external weight directory", create_args[3]),
+                           ("KV transfer file", launch.transfer_path)):
+            if not str(path).startswith(SHM):
+                raise RuntimeError(f"the sidecar's {what} must be under {SHM}, got {path}")
+        return launch
 
 
-def _request(operation: int, count: int, steps: int, transfer_id: int, tokens, positions, lengths, eos, gens) -> bytes:
-    return REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION, operation, count, steps, transfer_id,
-                        *tokens, *positions, *lengths, *eos, *gens)
+class SidecarLink:
+    """A connected control socket carrying whole records."""
+
+    def __init__(self, sock: socket.socket, peer: subprocess.Popen) -> None:
+        self.sock = sock
+        self.peer = peer
+
+    @classmethod
+    def connect(cls, path: Path, peer: subprocess.Popen, deadline: float) -> "SidecarLink | None":
+        """Connect once the server listens; None at the deadline.  Raises if
+        the server exits first."""
+        while time.monotonic() < deadline:
+            if peer.poll() is not None:
+                raise RuntimeError(f"the resident epoch sidecar exited during startup with status {peer.returncode}")
+            if path.exists():
+                sock = socket.socket(socket.AF_UNIX, socket.SOCK_STREAM)
+                try:
+                    sock.connect(str(path))
+                    return cls(sock, peer)
+                except OSError:
+                    sock.close()
+            time.sleep(0.05)
+        return None
+
+    def read_record(self) -> EpochFetch:
+        data = bytearray()
+        while len(data) < RESPONSE.size:
+            chunk = self.sock.recv(RESPONSE.size - len(data))
+            if not chunk:
+                raise RuntimeError(f"the resident epoch sidecar closed its socket (server status {self.peer.poll()})")
+            data += chunk
+        return decode_response(bytes(data))
+
+    def exchange(self, record: bytes) -> EpochFetch:
+        self.sock.sendall(record)
+        return self.read_record()
+
+    def close(self) -> None:
+        self.sock.close()
 
 
 class SidecarDataFlowEngine:
-    """Spawns the server, waits for its startup response, then runs epochs."""
+    """Starts the server, waits for its startup response, then serves the
+    NativeEpochEngine protocol over the socket."""
 
     warmup_token = WARMUP_TOKEN
     warmup_eos = DEFAULT_EOS
 
     def __init__(self) -> None:
-        server = _env_path("VLLM_ASCEND_RESIDENT_EPOCH_SERVER", default=DEFAULT_SERVER)
-        air = _env_path("VLLM_ASCEND_RESIDENT_EPOCH_AIR")
-        graph_config = _env_path("VLLM_ASCEND_RESIDENT_EPOCH_GRAPH_CONFIG")
-        func_config = _env_path("VLLM_ASCEND_RESIDENT_EPOCH_FUNC_CONFIG")
-        tiling = _env_path("VLLM_ASCEND_RESIDENT_EPOCH_TILING")
-        weights = _env_path("VLLM_ASCEND_RESIDENT_EPOCH_EXTERNAL_WEIGHTS", directory=True)
-        raw_socket = os.getenv("VLLM_ASCEND_RESIDENT_EPOCH_SOCKET")
-        if not raw_socket:
-            raise RuntimeError("VLLM_ASCEND_RESIDENT_EPOCH_SOCKET is required")
-        self.socket_path = Path(raw_socket).resolve()
-        self.transfer_path = self.socket_path.with_name(self.socket_path.name + ".kv-transfer")
-        for what, p in (("socket", self.socket_path), ("external weights", weights), ("KV transfer file", self.transfer_path)):
-            if not str(p).startswith("/dev/shm/"):
-                raise RuntimeError(f"resident epoch {what} must be under /dev/shm")
-
-        env = os.environ.copy()
-        extra_libs = os.getenv("VLLM_ASCEND_RESIDENT_EPOCH_CHILD_LIBRARY_PATH")
-        if extra_libs:
-            roots = [Path(p).resolve() for p in extra_libs.split(":")]
-            if not all(p.is_dir() for p in roots):
-                raise RuntimeError("resident sidecar library path is invalid")
-            inherited = env.get("LD_LIBRARY_PATH")
-            env["LD_LIBRARY_PATH"] = ":".join([*map(str, roots), *([inherited] if inherited else [])])
-
-        try:
-            self.socket_path.unlink(missing_ok=True)
-            self.transfer_path.unlink(missing_ok=True)
-        except OSError as exc:
-            raise RuntimeError(f"cannot reset sidecar socket: {exc}") from exc
-        argv = [str(server), str(self.socket_path), str(air), str(graph_config), str(func_config), str(weights), str(tiling)]
-        self.process = subprocess.Popen(argv, close_fds=True, env=env)
-        self.socket: socket.socket | None = None
-        timeout = int(os.getenv("VLLM_ASCEND_RESIDENT_EPOCH_STARTUP_TIMEOUT", "3600"))
-        self.socket = self._connect(time.monotonic() + timeout)
-        if self.socket is None:
+        self.launch = SidecarLaunch.from_env()
+        self.socket_path = self.launch.socket_path
+        self.transfer_path = self.launch.transfer_path
+        self._remove_files(strict=True)
+        self.link: SidecarLink | None = None
+        self.process = subprocess.Popen(self.launch.argv, close_fds=True, env=self.launch.env)
+        self.link = SidecarLink.connect(self.socket_path, self.process,
+                                        time.monotonic() + self.launch.startup_timeout)
+        if self.link is None:
             self._stop_process()
-            raise TimeoutError("resident epoch sidecar socket startup timed out")
-        self.socket.settimeout(timeout)
-        startup = self._receive_response()
-        if startup[_TRANSPORT] != 0:
-            status = startup[_TRANSPORT]
+            raise TimeoutError(f"the resident epoch sidecar did not open {self.socket_path} in time")
+        self.link.sock.settimeout(self.launch.startup_timeout)
+        startup = self.link.read_record()
+        if startup.transport_status != 0:
             self.close(force=True)
-            raise RuntimeError(f"resident epoch sidecar native initialization failed: {status}")
+            raise RuntimeError(f"the sidecar's native initialization failed: {startup.transport_status}")
 
-    def _connect(self, deadline: float) -> socket.socket | None:
-        while time.monotonic() < deadline:
-            if self.process.poll() is not None:
-                raise RuntimeError(f"resident epoch sidecar exited during startup with status {self.process.returncode}")
-            if self.socket_path.exists():
-                s = socket.socket(socket.AF_UNIX, socket.SOCK_STREAM)
-                try:
-                    s.connect(str(self.socket_path))
-                    return s
-                except OSError:
-                    s.close()
-            time.sleep(0.05)
-        return None
-
-    # -- wire ------------------------------------------------------------------
-    def _receive_exact(self, size: int) -> bytes:
-        assert self.socket is not None
-        buf = bytearray()
-        while len(buf) < size:
-            chunk = self.socket.recv(size - len(buf))
-            if not chunk:
-                raise RuntimeError(f"resident epoch sidecar closed the control socket (status={self.process.poll()})")
-            buf += chunk
-        return bytes(buf)
-
-    def _receive_response(self) -> tuple[int, ...]:
-        values = RESPONSE.unpack(self._receive_exact(RESPONSE.size))
-        if values[0] != RESPONSE_MAGIC:
-            raise RuntimeError("resident epoch sidecar response magic mismatch")
-        return values
-
-    # -- operations --------------------------------------------------------------
+    # -- the engine protocol -------------------------------------------------
     def warm_up(self) -> NativeWarmupOutput:
-        """One decoder step of one row under the reserved generation
-        (sidecar_backend.py:218-272)."""
-        if self.socket is None:
-            raise RuntimeError("resident epoch sidecar is closed")
-        self.socket.sendall(
-            _request(WARM_UP, 1, 1, 0, [self.warmup_token, 0, 0, 0], [0] * 4, [1, 0, 0, 0],
-                     [self.warmup_eos] * 4, [WARMUP_GENERATION, 0, 0, 0])
-        )
-        v = self._receive_response()
-        commit = _commit_state(v[_COMMIT])
-        if v[_TRANSPORT] != 0:
-            raise ResidentEpochExecutionError(
-                f"resident epoch warmup failed: {v[_TRANSPORT]}", commit_state=commit, status=v[_TRANSPORT]
-            )
-        if v[_EXECUTED] != (1, 0, 0, 0):
-            raise RuntimeError("resident epoch warmup did not execute exactly one row")
-        if v[_GENERATIONS] != (WARMUP_GENERATION, 0, 0, 0):
-            raise RuntimeError("resident epoch warmup generation acknowledgement failed")
-        return NativeWarmupOutput(
-            status=v[_DEVICE], model_calls=v[_CALLS], feed_calls=v[_FEEDS], fetch_calls=v[_FETCHES],
-            commit_state=commit, wall_us=v[_WALL], native_cpu_us=v[_CPU],
-            declared_input_bytes=v[_IN_BYTES], declared_output_bytes=v[_OUT_BYTES],
-        )
+        if self.link is None:
+            raise RuntimeError("the resident epoch sidecar is closed")
+        feed = EpochFeed.warm_up(self.warmup_token, self.warmup_eos)
+        return self.link.exchange(encode_request(WARM_UP, feed)).warmup_output()
 
     def execute(self, plan: ResidentEpochPlan) -> NativeEpochOutput:
-        return self._execute(plan, operation=EXECUTE, transfer_id=0)
-
-    @staticmethod
-    def _import_check(plan: ResidentEpochPlan, mask: int, generations, what: str) -> None:
-        rows = [r for r in plan.requests if r.kv_import_required]
-        if mask != sum(1 << r.row for r in rows):
-            raise ValueError(f"{what} mask does not match the resident plan")
-        expected = [0] * GRAPH_BATCH_SIZE
-        for r in rows:
-            expected[r.row] = r.generation
-        if tuple(generations) != tuple(expected):
-            raise ValueError(f"{what} generations do not match the resident plan")
+        return self._run(plan, EXECUTE, 0, b"", "none")
 
     def execute_with_import(self, plan: ResidentEpochPlan, snapshot: ResidentKVSnapshot) -> NativeEpochOutput:
         snapshot.validate()
-        self._import_check(plan, snapshot.import_mask, snapshot.row_generations, "KV snapshot")
+        check_transfer(plan, snapshot.import_mask, snapshot.row_generations, "KV snapshot")
         write_kv_snapshot(self.transfer_path, snapshot)
         try:
-            return self._execute(plan, operation=IMPORT_EXECUTE, transfer_id=snapshot.transfer_id)
+            return self._run(plan, IMPORT_EXECUTE, snapshot.transfer_id, b"", "host_snapshot")
         finally:
             self.transfer_path.unlink(missing_ok=True)
 
     def execute_with_device_transfer(self, plan: ResidentEpochPlan, transfer: DeviceKVTransfer) -> NativeEpochOutput:
         transfer.validate()
-        self._import_check(plan, transfer.import_mask, transfer.row_generations, "device KV transfer")
-        return self._execute(plan, operation=DEVICE_IPC_EXECUTE, transfer_id=transfer.transfer_id,
-                             ipc_metadata=transfer.wire_bytes())
+        check_transfer(plan, transfer.import_mask, transfer.row_generations, "device KV transfer")
+        record = transfer.wire_bytes()
+        if len(record) != IPC_METADATA_BYTES:
+            raise ValueError(f"a device IPC record is {IPC_METADATA_BYTES} bytes, not {len(record)}")
+        return self._run(plan, DEVICE_IPC_EXECUTE, transfer.transfer_id, record, "device_ipc")
 
-    def _execute(self, plan: ResidentEpochPlan, *, operation: int, transfer_id: int,
-                 ipc_metadata: bytes | None = None) -> NativeEpochOutput:
-        if self.socket is None:
-            raise ResidentEpochExecutionError("resident epoch sidecar is closed", commit_state=EpochCommitState.PREPARED)
-        if plan.graph_batch_size != GRAPH_BATCH_SIZE:
-            raise ValueError("the sidecar backend owns only the static B=4 graph")
-        payload = _request(operation, len(plan.requests), plan.max_steps, transfer_id,
-                           _by_row(plan, "token_id", 0), _by_row(plan, "position", 0),
-                           _by_row(plan, "sequence_length", 0), _by_row(plan, "eos_token_id", DEFAULT_EOS),
-                           plan.row_generations)
-        if operation == DEVICE_IPC_EXECUTE:
-            if ipc_metadata is None or len(ipc_metadata) != IPC_METADATA_BYTES:
-                raise ValueError("direct Device KV operation has invalid metadata")
-            payload += ipc_metadata
+    def _run(self, plan: ResidentEpochPlan, operation: int, transfer_id: int, trailer: bytes,
+             mode: str) -> NativeEpochOutput:
+        if self.link is None:
+            raise ResidentEpochExecutionError("the resident epoch sidecar is closed",
+                                              commit_state=EpochCommitState.PREPARED)
+        record = encode_request(operation, EpochFeed.from_plan(plan), transfer_id) + trailer
         try:
-            self.socket.sendall(payload)
-            v = self._receive_response()
+            fetch = self.link.exchange(record)
         except Exception as exc:
-            # The request may or may not have reached the device.
-            raise ResidentEpochExecutionError(
-                f"resident epoch response is ambiguous: {exc}", commit_state=EpochCommitState.EXECUTING
-            ) from exc
-        commit = _commit_state(v[_COMMIT])
-        if v[_TRANSPORT] != 0:
-            raise ResidentEpochExecutionError(
-                f"resident epoch sidecar execute failed: {v[_TRANSPORT]}", commit_state=commit, status=v[_TRANSPORT]
-            )
-        executed = v[_EXECUTED]
-        history = v[_TOKENS]
-        tokens: dict[str, list[int]] = {}
-        for r in plan.requests:
-            n = executed[r.row]
-            if not 0 <= n <= plan.max_steps:
-                raise ResidentEpochExecutionError("sidecar returned an invalid executed count", commit_state=commit)
-            tokens[r.req_id] = list(history[r.row * MAX_EPOCH_STEPS : r.row * MAX_EPOCH_STEPS + n])
-        imported = operation in (IMPORT_EXECUTE, DEVICE_IPC_EXECUTE)
-        return NativeEpochOutput(
-            status=v[_DEVICE], model_calls=v[_CALLS], token_ids=tokens, row_generations=tuple(v[_GENERATIONS]),
-            commit_state=commit, feed_calls=v[_FEEDS], fetch_calls=v[_FETCHES], wall_us=v[_WALL],
-            native_cpu_us=v[_CPU], declared_input_bytes=v[_IN_BYTES], declared_output_bytes=v[_OUT_BYTES],
-            kv_imported=imported, kv_import_checksum=v[_CHECKSUM] & 0xFFFFFFFF,
-            kv_transfer_mode=("device_ipc" if operation == DEVICE_IPC_EXECUTE else "host_snapshot") if imported else "none",
-        )
+            raise ResidentEpochExecutionError(f"no complete answer from the sidecar: {exc}",
+                                              commit_state=EpochCommitState.EXECUTING) from exc
+        return fetch.native_output(plan, mode)
 
-    # -- lifecycle ---------------------------------------------------------------
+    # -- lifecycle -----------------------------------------------------------
+    def _remove_files(self, strict: bool = False) -> None:
+        for path in (self.socket_path, self.transfer_path):
+            try:
+                path.unlink(missing_ok=True)
+            except OSError as exc:
+                if strict:
+                    raise RuntimeError(f"cannot remove the stale sidecar file {path}: {exc}") from exc
+
     def _stop_process(self) -> None:
-        if self.process.poll() is None:
-            self.process.terminate()
+        """Terminate, then kill, waiting up to a minute for each."""
+        for signal_process in (self.process.terminate, self.process.kill):
+            if self.process.poll() is not None:
+                return
+            signal_process()
             try:
                 self.process.wait(timeout=60)
+                return
             except subprocess.TimeoutExpired:
-                self.process.kill()
-                self.process.wait(timeout=60)
+                continue
 
     def close(self, *, force: bool = False) -> None:
-        """Graceful SHUTDOWN when the server still runs, else (or if that
-        fails) terminate, then kill (sidecar_backend.py:416-456)."""
-        if self.socket is not None:
+        """Ask a running server to shut down; if that fails, or with
+        ``force``, stop its process instead."""
+        if self.link is not None:
             if not force and self.process.poll() is None:
                 try:
-                    self.socket.sendall(_request(SHUTDOWN, 0, 0, 0, [0] * 4, [0] * 4, [0] * 4, [0] * 4, [0] * 4))
-                    self._receive_response()
+                    self.link.exchange(encode_request(SHUTDOWN, EpochFeed.empty()))
                 except (OSError, RuntimeError):
                     force = True
-            self.socket.close()
-            self.socket = None
-        if force:
-            self._stop_process()
-        else:
+            self.link.close()
+            self.link = None
+        if not force:
             try:
                 self.process.wait(timeout=300)
             except subprocess.TimeoutExpired:
-                self._stop_process()
-        for p in (self.socket_path, self.transfer_path):
-            try:
-                p.unlink(missing_ok=True)
-            except OSError:
-                pass
+                force = True
+        if force:
+            self._stop_process()
+        self._remove_files()
 
     def __del__(self) -> None:
         try:
-            self.close(force=True)
+            if getattr(self, "process", None) is not None:
+                self.close(force=True)
         except Exception:
             pass
 

@@ -88,7 +88,7 @@ def test_import_modes_are_proven():
     out = ResidentEpochBackend(eng).execute(p, device_transfer=transfer(0b0010, (0, 3, 0, 0), (0, 1, 0, 0)))
     assert get_result(out).kv_transfer_mode == "device_ipc"
     assert eng.calls == ["import", "ipc"]
-    with pytest.raises(ValueError, match="two KV transfer modes"):
+    with pytest.raises(ValueError, match="one source"):
         ResidentEpochBackend(eng).execute(p, snapshot=snapshot(0b0010, (0, 3, 0, 0)),
                                           device_transfer=transfer(0b0010, (0, 3, 0, 0), (0, 1, 0, 0)))
 
@@ -96,11 +96,11 @@ def test_import_modes_are_proven():
 @pytest.mark.parametrize(
     ("override", "state", "message"),
     [
-        ({"status": 207}, EpochCommitState.COMMITTED, "returned status 207"),
-        ({"commit_state": EpochCommitState.EXECUTING}, EpochCommitState.EXECUTING, "was not committed"),
-        ({"token_ids": {"rX": [1]}}, EpochCommitState.COMMITTED, "wrong request set"),
-        ({"model_calls": 9}, EpochCommitState.COMMITTED, "result is invalid"),
-        ({"feed_calls": 2}, EpochCommitState.COMMITTED, "result is invalid"),
+        ({"status": 207}, EpochCommitState.COMMITTED, "fell back with status 207"),
+        ({"commit_state": EpochCommitState.EXECUTING}, EpochCommitState.EXECUTING, "did not commit"),
+        ({"token_ids": {"rX": [1]}}, EpochCommitState.COMMITTED, "answered for"),
+        ({"model_calls": 9}, EpochCommitState.COMMITTED, "output is invalid"),
+        ({"feed_calls": 2}, EpochCommitState.COMMITTED, "device-round-trip"),
     ],
 )
 def test_failures_carry_their_commit_state(override, state, message):
@@ -111,10 +111,10 @@ def test_failures_carry_their_commit_state(override, state, message):
 
 def test_snapshot_checksum_disagreement_is_committed_failure():
     p = plan(req(1, 3, imp=True))
-    with pytest.raises(ResidentEpochExecutionError, match="disagrees with the Host snapshot") as err:
+    with pytest.raises(ResidentEpochExecutionError, match="disagrees with the host") as err:
         ResidentEpochBackend(Engine(kv_import_checksum=5)).execute(p, snapshot=snapshot(0b0010, (0, 3, 0, 0)))
     assert err.value.commit_state == EpochCommitState.COMMITTED
-    with pytest.raises(ResidentEpochExecutionError, match="did not return an import checksum"):
+    with pytest.raises(ResidentEpochExecutionError, match="returned no checksum"):
         ResidentEpochBackend(Engine(kv_import_checksum=0)).execute(
             p, device_transfer=transfer(0b0010, (0, 3, 0, 0), (0, 1, 0, 0)))
 
@@ -122,7 +122,7 @@ def test_snapshot_checksum_disagreement_is_committed_failure():
 def test_invalid_plan_is_prepared_failure():
     bad = ResidentEpochPlan(CONTRACT_VERSION, 4, 4, 8, (req(0, 1),), (1, 1, 0, 0))
     eng = Engine()
-    with pytest.raises(ResidentEpochExecutionError, match="plan validation failed") as err:
+    with pytest.raises(ResidentEpochExecutionError, match="rejected before execution") as err:
         ResidentEpochBackend(eng).execute(bad)
     assert err.value.input_preserving and eng.calls == []
 
@@ -132,9 +132,20 @@ def test_engine_exception_is_executing_failure():
         def execute(self, p):
             raise OSError("socket reset")
 
-    with pytest.raises(ResidentEpochExecutionError, match="without commit-state proof") as err:
+    with pytest.raises(ResidentEpochExecutionError, match="without proof of its commit state") as err:
         ResidentEpochBackend(Broken()).execute(plan(req(0, 1)))
     assert err.value.commit_state == EpochCommitState.EXECUTING
+
+
+def test_engine_errors_with_a_commit_state_pass_through():
+    class Declared(Engine):
+        def execute(self, p):
+            raise ResidentEpochExecutionError("socket closed before send", commit_state=EpochCommitState.PREPARED,
+                                              status=13)
+
+    with pytest.raises(ResidentEpochExecutionError, match="socket closed before send") as err:
+        ResidentEpochBackend(Declared()).execute(plan(req(0, 1)))
+    assert err.value.input_preserving and err.value.status == 13
 
 
 def test_missing_import_support_is_prepared_failure():
@@ -142,7 +153,7 @@ def test_missing_import_support_is_prepared_failure():
         def execute(self, p):
             raise AssertionError
 
-    with pytest.raises(ResidentEpochExecutionError, match="does not support KV import") as err:
+    with pytest.raises(ResidentEpochExecutionError, match="no execute_with_import") as err:
         ResidentEpochBackend(Plain()).execute(plan(req(1, 3, imp=True)), snapshot=snapshot(0b0010, (0, 3, 0, 0)))
     assert err.value.input_preserving
 

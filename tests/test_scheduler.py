@@ -32,7 +32,7 @@ from cruise_amd.contract import (
     get_plan,
 )
 from cruise_amd.eligibility import request_rejection_reason
-from cruise_amd.scheduler import ResidentEpochSchedulerMixin, epoch_steps_for
+from cruise_amd.scheduler import ResidentEpochSchedulerMixin, ResidentRowTable, epoch_steps_for, host_lane_reason
 from fake_vllm import EOS_TOKEN_ID, FakeScheduler, Request, RequestStatus, greedy_params, qwen7b_vllm_config
 
 
@@ -88,27 +88,39 @@ def test_epoch_length_is_largest_power_within_budget(max_steps, remaining, k):
     assert epoch_steps_for(max_steps, remaining) == k
 
 
+def rows_of(table):
+    return {rid: seat.row for rid, seat in table.seats.items()}
+
+
+def generations_of(table):
+    return {rid: seat.generation for rid, seat in table.seats.items()}
+
+
 def test_rows_are_lowest_free_and_generations_fresh():
-    s = make_scheduler(4)
-    s._ensure_test_config()
-    s._assign_resident_rows(("a", "b", "c"))
-    assert s._resident_epoch_rows == {"a": 0, "b": 1, "c": 2}
-    assert s._resident_epoch_generations == {"a": 1, "b": 2, "c": 3}
-    s._resident_epoch_device_owned.add("b")
-    s._assign_resident_rows(("a", "c", "d", "e"))  # b leaves: its row is reused first
-    assert s._resident_epoch_rows == {"a": 0, "c": 2, "d": 1, "e": 3}
-    assert s._resident_epoch_generations["d"] == 4 and s._resident_epoch_generations["e"] == 5
-    assert "b" not in s._resident_epoch_device_owned
+    t = ResidentRowTable(4)
+    t.seat_exactly(("a", "b", "c"))
+    assert rows_of(t) == {"a": 0, "b": 1, "c": 2}
+    assert generations_of(t) == {"a": 1, "b": 2, "c": 3}
+    t.device_owned.add("b")
+    t.seat_exactly(("a", "c", "d", "e"))  # b leaves: its row is reused first
+    assert rows_of(t) == {"a": 0, "c": 2, "d": 1, "e": 3}
+    assert generations_of(t)["d"] == 4 and generations_of(t)["e"] == 5
+    assert "b" not in t.device_owned
     with pytest.raises(RuntimeError, match="exhausted"):
-        s._assign_resident_rows(("a", "c", "d", "e", "f"))
+        t.seat_exactly(("a", "c", "d", "e", "f"))
 
 
 def test_generation_space_is_bounded():
-    s = make_scheduler(4)
-    s._ensure_test_config()
-    s._resident_epoch_next_generation = 2**31
+    t = ResidentRowTable(4, first_generation=2**31 - 1)
+    assert t.admit("last").generation == 2**31 - 1
     with pytest.raises(RuntimeError, match="generation space exhausted"):
-        s._assign_resident_rows(("x",))
+        t.admit("x")
+
+
+def test_scheduler_without_init_gets_default_state():
+    s = Scheduler.__new__(Scheduler)
+    config, table = s._resident_state()
+    assert config == ResidentEpochConfig() and table.rows == 4 and s._resident_epoch_device_owned == set()
 
 
 # ---------------------------------------------------------------------------
@@ -270,9 +282,8 @@ def test_running_prefill_is_isolated_from_device_owned_requests():
     prefill = prefill_request("prefill", [9707, 11, 358], 4)
     prefill.num_computed_tokens = 1
     s.running = [device_req, prefill]
-    s._ensure_test_config()
-    assert s._host_isolation_reason((device_req,)) == "host-prefill-admission"
-    assert s._host_isolation_reason(()) is None
+    assert host_lane_reason(s, [device_req]) == "host-prefill-admission"
+    assert host_lane_reason(s, []) is None
 
 
 def test_device_owned_request_is_never_sent_to_the_host():
@@ -282,7 +293,7 @@ def test_device_owned_request_is_never_sent_to_the_host():
     out = s2.schedule()
     commit_device_epoch(s2, out, {"0": list(range(1, 9))})
     s2.block_size = 64
-    with pytest.raises(RuntimeError, match="refusing Host execution for Device-owned"):
+    with pytest.raises(RuntimeError, match="device-owned requests cannot run on the host: 0"):
         s2.schedule()
     assert r.request_id in s2._resident_epoch_device_owned
 
@@ -355,16 +366,16 @@ def test_host_fallback_retains_normal_one_step_accounting():
 def test_constructor_rejects_unsupported_deployments(monkeypatch):
     monkeypatch.delenv("VLLM_ASCEND_RESIDENT_EPOCH_STEPS", raising=False)
     Scheduler(vllm_config=qwen7b_vllm_config())
-    with pytest.raises(ValueError, match="native graph mismatch: hidden_size=4096"):
+    with pytest.raises(ValueError, match="hidden_size=3584.*has 4096"):
         Scheduler(vllm_config=qwen7b_vllm_config(hidden_size=4096))
-    with pytest.raises(ValueError, match="synchronous scheduling"):
+    with pytest.raises(ValueError, match="need synchronous scheduling"):
         Scheduler(async_scheduling=True)
     cfg = qwen7b_vllm_config()
     cfg.parallel_config.tensor_parallel_size = 2
-    with pytest.raises(ValueError, match="tensor parallel size 1"):
+    with pytest.raises(ValueError, match="tensor and pipeline parallel size"):
         Scheduler(vllm_config=cfg)
     monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_STEPS", "3")
-    with pytest.raises(ValueError, match="one of 1, 2, 4, 8"):
+    with pytest.raises(ValueError, match=r"max_steps=3 is not one of \(1, 2, 4, 8\)"):
         Scheduler()
 
 
@@ -401,13 +412,23 @@ def test_unsupported_semantics_are_rejected(field, value, reason):
     assert request_rejection_reason(eligible_request(**{field: value})) == reason
 
 
+def test_config_geometry_and_mapping():
+    c = ResidentEpochConfig(logical_capacity=256)
+    assert [c.row_blocks(r) for r in range(4)] == [(0, 1), (2, 3), (4, 5), (6, 7)]
+    assert [c.epoch_steps(b) for b in (1, 2, 3, 5, 8, 100)] == [1, 2, 2, 4, 8, 8]
+    with pytest.raises(ValueError):
+        c.epoch_steps(0)
+    assert ResidentEpochConfig.from_env({"VLLM_ASCEND_RESIDENT_EPOCH_STEPS": "2"}).max_steps == 2
+    assert len(ResidentEpochConfig(max_steps=3, logical_capacity=1, max_batch_size=2).problems()) == 3
+
+
 def test_config_from_env(monkeypatch):
     monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_STEPS", "4")
     monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_CAPACITY", "256")
     assert ResidentEpochConfig.from_env() == ResidentEpochConfig(max_steps=4, logical_capacity=256)
     monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_CAPACITY", "2")
-    with pytest.raises(ValueError, match="at least max_steps"):
+    with pytest.raises(ValueError, match="cannot hold an epoch of 4 steps"):
         ResidentEpochConfig.from_env()
     monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_CAPACITY", "x")
-    with pytest.raises(ValueError, match="must be an integer"):
+    with pytest.raises(ValueError, match="is not an integer"):
         ResidentEpochConfig.from_env()

@@ -36,6 +36,7 @@ from cruise_amd.kv_transfer import (
     ResidentKVSnapshot,
     kv_payload_checksum,
 )
+from cruise_amd.ctypes_backend import CtypesDataFlowEngine
 from cruise_amd.sidecar_backend import (
     DEVICE_IPC_EXECUTE,
     EXECUTE,
@@ -48,6 +49,7 @@ from cruise_amd.sidecar_backend import (
     WARM_UP,
     WARMUP_GENERATION,
     SidecarDataFlowEngine,
+    decode_response,
 )
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -84,59 +86,110 @@ def test_record_sizes_and_field_order():
     assert v[20:] == tuple(range(32))
 
 
-def test_warmup_request_uses_the_reserved_generation():
-    sent = []
+class FakeLink:
+    """Stands in for the socket: records what is sent and answers with one
+    fixed response record."""
 
-    class Recorder:
-        def sendall(self, data):
-            sent.append(data)
+    def __init__(self, *response):
+        self.sent = []
+        self.response = RESPONSE.pack(*response)
 
+    def exchange(self, record):
+        self.sent.append(record)
+        return decode_response(self.response)
+
+    def close(self):
+        pass
+
+
+def engine_with(link):
     eng = SidecarDataFlowEngine.__new__(SidecarDataFlowEngine)
-    eng.socket = Recorder()
-    eng._receive_response = lambda: RESPONSE.unpack(
-        RESPONSE.pack(RESPONSE_MAGIC, 0, 0, 1, 1, 1, 2, 0, 7, 3, 260, 368, 1, 0, 0, 0,
-                      WARMUP_GENERATION, 0, 0, 0, 12, *([-1] * 31))
-    )
-    out = eng.warm_up()
-    fields = REQUEST.unpack(sent[0])
+    eng.link = link
+    return eng
+
+
+def test_warmup_request_uses_the_reserved_generation():
+    link = FakeLink(RESPONSE_MAGIC, 0, 0, 1, 1, 1, 2, 0, 7, 3, 260, 368, 1, 0, 0, 0,
+                    WARMUP_GENERATION, 0, 0, 0, 12, *([-1] * 31))
+    out = engine_with(link).warm_up()
+    fields = REQUEST.unpack(link.sent[0])
     assert fields[:5] == (REQUEST_MAGIC, PROTOCOL_VERSION, WARM_UP, 1, 1)
     assert fields[6:10] == (11690, 0, 0, 0)
     assert fields[-GRAPH_BATCH_SIZE:] == (WARMUP_GENERATION, 0, 0, 0)
     assert (out.status, out.model_calls, out.feed_calls, out.fetch_calls) == (0, 1, 1, 1)
 
 
+def test_warmup_must_run_exactly_row_zero():
+    link = FakeLink(RESPONSE_MAGIC, 0, 0, 1, 1, 1, 2, 0, 7, 3, 260, 368, 1, 1, 0, 0,
+                    WARMUP_GENERATION, 0, 0, 0, *([-1] * 32))
+    with pytest.raises(RuntimeError, match="instead of one step on row 0"):
+        engine_with(link).warm_up()
+
+
+def test_plan_rows_are_laid_out_on_the_graph_rows():
+    link = FakeLink(RESPONSE_MAGIC, 0, 0, 4, 1, 1, 2, 0, 0, 0, 260, 368, 0, 4, 0, 4, 0, 3, 0, 4, *([-1] * 32))
+    plan = plan_of(request(1, 3, 500, 2), request(3, 4, 600, 0))
+    engine_with(link).execute(plan)
+    fields = REQUEST.unpack(link.sent[0])
+    assert fields[3:5] == (2, 4)  # request count, K
+    assert fields[6:10] == (0, 500, 0, 600)  # tokens
+    assert fields[10:14] == (0, 2, 0, 0)  # positions
+    assert fields[14:18] == (0, 3, 0, 1)  # lengths
+    assert fields[18:22] == (151645,) * 4  # EOS: the plan's, default elsewhere
+    assert fields[22:26] == (0, 3, 0, 4)  # generations
+
+
 def test_device_ipc_execute_is_reported_as_kv_import():
-    sent = []
-
-    class Recorder:
-        def sendall(self, data):
-            sent.append(data)
-
-    eng = SidecarDataFlowEngine.__new__(SidecarDataFlowEngine)
-    eng.socket = Recorder()
-    eng._receive_response = lambda: RESPONSE.unpack(
-        RESPONSE.pack(RESPONSE_MAGIC, 0, 0, 1, 1, 1, EpochCommitState.COMMITTED, 0x12345678, 123, 45, 3776, 368,
-                      1, 0, 0, 0, 7, 0, 0, 0, 42, *([-1] * 31))
-    )
+    link = FakeLink(RESPONSE_MAGIC, 0, 0, 1, 1, 1, EpochCommitState.COMMITTED, 0x12345678, 123, 45, 3776, 368,
+                    1, 0, 0, 0, 7, 0, 0, 0, 42, *([-1] * 31))
     plan = plan_of(request(0, 7, 11, 1, imp=True), steps=1)
     metadata = b"\0" * IPC_METADATA_BYTES
-    out = eng._execute(plan, operation=DEVICE_IPC_EXECUTE, transfer_id=9, ipc_metadata=metadata)
-    assert out.kv_imported is True
+    out = engine_with(link)._run(plan, DEVICE_IPC_EXECUTE, 9, metadata, "device_ipc")
+    assert out.kv_imported is True and out.kv_transfer_mode == "device_ipc"
     assert out.kv_import_checksum == 0x12345678
     assert out.token_ids == {"r0": [42]}
-    assert len(sent) == 1 and sent[0][REQUEST.size:] == metadata
-    assert REQUEST.unpack(sent[0][: REQUEST.size])[2] == DEVICE_IPC_EXECUTE
+    assert len(link.sent) == 1 and link.sent[0][REQUEST.size:] == metadata
+    assert REQUEST.unpack(link.sent[0][: REQUEST.size])[2] == DEVICE_IPC_EXECUTE
 
 
 def test_invalid_commit_state_is_ambiguous():
-    eng = SidecarDataFlowEngine.__new__(SidecarDataFlowEngine)
-    eng.socket = type("S", (), {"sendall": lambda self, d: None})()
-    eng._receive_response = lambda: RESPONSE.unpack(
-        RESPONSE.pack(RESPONSE_MAGIC, 0, 0, 1, 1, 1, 9, 0, 0, 0, 0, 0, *([0] * 8), *([-1] * 32))
-    )
+    link = FakeLink(RESPONSE_MAGIC, 0, 0, 1, 1, 1, 9, 0, 0, 0, 0, 0, *([0] * 8), *([-1] * 32))
     with pytest.raises(ResidentEpochExecutionError) as err:
-        eng.execute(plan_of(request(0, 1, 5, 0)))
+        engine_with(link).execute(plan_of(request(0, 1, 5, 0)))
     assert err.value.commit_state == EpochCommitState.EXECUTING
+
+
+def test_executed_count_beyond_the_epoch_is_rejected():
+    link = FakeLink(RESPONSE_MAGIC, 0, 0, 4, 1, 1, 2, 0, 0, 0, 0, 0, 9, 0, 0, 0, 1, 0, 0, 0, *([-1] * 32))
+    with pytest.raises(ResidentEpochExecutionError, match="9 executed steps") as err:
+        engine_with(link).execute(plan_of(request(0, 1, 5, 0)))
+    assert err.value.commit_state == EpochCommitState.COMMITTED
+
+
+def test_a_broken_socket_is_an_executing_failure():
+    class Dead:
+        def exchange(self, record):
+            raise ConnectionResetError("peer reset")
+
+    with pytest.raises(ResidentEpochExecutionError, match="no complete answer") as err:
+        engine_with(Dead()).execute(plan_of(request(0, 1, 5, 0)))
+    assert err.value.commit_state == EpochCommitState.EXECUTING
+    closed = engine_with(None)
+    with pytest.raises(ResidentEpochExecutionError) as err:
+        closed.execute(plan_of(request(0, 1, 5, 0)))
+    assert err.value.input_preserving
+
+
+def test_transfer_must_match_the_plan():
+    link = FakeLink(RESPONSE_MAGIC, *([0] * 19), *([-1] * 32))
+    eng = engine_with(link)
+    eng.transfer_path = Path("/nonexistent/never-written")
+    plan = plan_of(request(1, 5, 7, 2, imp=True), steps=2)
+    with pytest.raises(ValueError, match="import mask"):
+        eng.execute_with_import(plan, small_snapshot(0b0001, (5, 0, 0, 0)))
+    with pytest.raises(ValueError, match="row generations"):
+        eng.execute_with_import(plan, small_snapshot(0b0010, (0, 6, 0, 0)))
+    assert link.sent == []
 
 
 # ---------------------------------------------------------------------------
@@ -238,24 +291,22 @@ def test_transport_errors_keep_the_connection(sidecar_env):
     eng = SidecarDataFlowEngine()
     try:
         # request count that disagrees with the rows: the engine's status 12
-        eng.socket.sendall(REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION, EXECUTE, 2, 2, 0, *([0] * 4), *([0] * 4),
-                                        1, 0, 0, 0, *([151645] * 4), 1, 0, 0, 0))
-        assert eng._receive_response()[1] == 12
+        link = eng.link
+        assert link.exchange(REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION, EXECUTE, 2, 2, 0, *([0] * 4), *([0] * 4),
+                                          1, 0, 0, 0, *([151645] * 4), 1, 0, 0, 0)).transport_status == 12
         # wrong magic, wrong version, unknown operation
-        eng.socket.sendall(REQUEST.pack(0x1234, PROTOCOL_VERSION, EXECUTE, *([0] * 23)))
-        assert eng._receive_response()[1] == 69
-        eng.socket.sendall(REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION + 1, EXECUTE, *([0] * 23)))
-        assert eng._receive_response()[1] == 69
-        eng.socket.sendall(REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION, 9, *([0] * 23)))
-        assert eng._receive_response()[1] == 71
+        assert link.exchange(REQUEST.pack(0x1234, PROTOCOL_VERSION, EXECUTE, *([0] * 23))).transport_status == 69
+        assert link.exchange(REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION + 1, EXECUTE,
+                                          *([0] * 23))).transport_status == 69
+        assert link.exchange(REQUEST.pack(REQUEST_MAGIC, PROTOCOL_VERSION, 9, *([0] * 23))).transport_status == 71
         # the session still serves epochs
         out = eng.execute(plan_of(request(0, 1, 5, 0), steps=2))
         assert out.token_ids == {"r0": [6, 7]}
         # an engine-side rejection (the double's 35 for a zero IPC magic) is an
         # error in PREPARED state: nothing reached the device
         with pytest.raises(ResidentEpochExecutionError) as err:
-            eng._execute(ResidentEpochPlan(CONTRACT_VERSION, 4, 1, 8, (request(0, 1, 5, 0),), (1, 0, 0, 0)),
-                         operation=DEVICE_IPC_EXECUTE, transfer_id=3, ipc_metadata=b"\0" * IPC_METADATA_BYTES)
+            eng._run(ResidentEpochPlan(CONTRACT_VERSION, 4, 1, 8, (request(0, 1, 5, 0),), (1, 0, 0, 0)),
+                     DEVICE_IPC_EXECUTE, 3, b"\0" * IPC_METADATA_BYTES, "device_ipc")
         assert err.value.status == 35 and err.value.commit_state == EpochCommitState.PREPARED
     finally:
         eng.close()
@@ -279,8 +330,8 @@ def test_startup_refuses_an_engine_that_is_not_four_rows(sidecar_env, monkeypatc
 
 def test_server_exits_when_the_client_goes_away(sidecar_env):
     eng = SidecarDataFlowEngine()
-    eng.socket.close()
-    eng.socket = None
+    eng.link.close()
+    eng.link = None
     assert eng.process.wait(timeout=30) == 68
     eng.close(force=True)
 
@@ -289,3 +340,27 @@ def test_server_rejects_a_socket_outside_dev_shm(stub_server, tmp_path):
     rc = subprocess.run([str(stub_server), str(tmp_path / "s.sock"), "a", "b", "c", "d", "e"]).returncode
     assert rc == 65
     assert subprocess.run([str(stub_server)]).returncode == 64
+
+
+def test_in_process_engine_decodes_like_the_sidecar(sidecar_env, stub_server, monkeypatch):
+    """The ctypes engine over the same C-ABI double returns what the sidecar
+    returns for the same plans: both go through one feed/fetch codec."""
+    monkeypatch.setenv("VLLM_ASCEND_RESIDENT_EPOCH_LIBRARY", str(stub_server.parent / "libresident_epoch.so"))
+    plans = [plan_of(request(0, 1, 100, 0), request(2, 2, 200, 3)), plan_of(request(3, 4, 9, 5), steps=2)]
+    local = CtypesDataFlowEngine()
+    try:
+        warm_local = local.warm_up()
+        out_local = [local.execute(p) for p in plans]
+        snap = small_snapshot(0b0010, (0, 5, 0, 0))
+        imported = local.execute_with_import(plan_of(request(1, 5, 7, 2, imp=True), steps=2), snap)
+    finally:
+        local.close()
+    assert imported.kv_imported and imported.kv_import_checksum == snap.checksum
+    assert imported.kv_transfer_mode == "host_snapshot" and imported.token_ids == {"r1": [8, 9]}
+    remote = SidecarDataFlowEngine()
+    try:
+        assert remote.warm_up() == warm_local
+        assert [remote.execute(p) for p in plans] == out_local
+    finally:
+        remote.close()
+    assert out_local[0].token_ids == {"r0": [101, 102, 103, 104], "r2": [201, 202, 203, 204]}
