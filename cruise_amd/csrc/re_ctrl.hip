@@ -70,21 +70,32 @@ __device__ FeedView feed_view(const uint8_t* feed, int B, int bpr, bool importin
   return f;
 }
 
+// Row-parallel controller kernels: one workgroup, thread r owns batch row r
+// (rows strided by the block size).  A check the reference runs row by row
+// and stops at the first failing row becomes a per-row code plus the lowest
+// failing row, found with an LDS atomicMin over the key (row << 8) | (status -
+// 200); the row's code is the status, and the side effects of the rows before
+// it are applied exactly as the sequential loop applies them.
+constexpr int kCtrlThreads = 1024;
+constexpr int kNoFailure = 0x7fffffff;
+// Block-uniqueness bitmap: pools up to 32 x 15360 = 491,520 blocks are checked
+// in LDS; larger pools compare pairs in global memory.
+constexpr int kBitmapWords = 15360;
+
+__device__ __forceinline__ int fail_key(int row, int32_t status) { return (row << 8) | (status - 200); }
+__device__ __forceinline__ int fail_row(int key) { return key == kNoFailure ? 0x7fffffff : key >> 8; }
+__device__ __forceinline__ int32_t fail_status(int key) { return (key & 0xff) + 200; }
+
 // Validation, import bookkeeping, generation continuity (CTRL:204-471) and the
-// loop's initial state (CTRL:473-483).  Single thread: B rows of integer work.
-__global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// loop's initial state (CTRL:473-483), in the reference's order of checks:
+// feed form, K / sampling / variant (335-340), EOS ids (341-345), block table
+// range and uniqueness (346-353), per-row metadata and slots (354-385), import
+// mask and rows (387-429), generation continuity (448-464).
+__global__ void __launch_bounds__(kCtrlThreads) k_ctrl_init(CtrlArgs a, long long payload_bytes) {
+  __shared__ unsigned seen[kBitmapWords];
+  __shared__ int eos_bad, block_bad, meta_key, import_key, cont_key, active_count, any_adopted;
   StatePtrs& s = a.st;
-  if (threadIdx.x == 0) {  // import checksum accumulators, summed by k_import_checksum
-    s.import_sum[0] = 0;
-    s.import_sum[1] = 0;
-  }
-  const int B = a.B;
-  // The control vector sits at the same place in both feed forms; read the
-  // variant first to learn the form (CTRL:209-217).
-  const FeedView plain = feed_view(s.feed, B, a.bpr, false, 0);
-  const int32_t* ctl_plain = plain.control;  // valid only for the plain form
-  (void)ctl_plain;
+  const int B = a.B, tid = threadIdx.x, T = blockDim.x;
   // In import mode the payload precedes everything and the slot input is
   // absent, so the control offset differs; the host tells us the form.
   const bool importing = a.has_payload != 0;
@@ -96,22 +107,24 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
   const int32_t graph_variant = flagged ? (encoded_variant & ~(kImportGraphFlag | 0xF)) : encoded_variant;
   const int32_t max_steps = ctl[0];
   const int32_t sampling = ctl[1 + B];
-  s.misc[0] = max_steps;
-  s.misc[1] = sampling;
-  s.misc[2] = graph_variant;
-  s.misc[3] = flagged ? 1 : 0;
-  s.misc[4] = import_mask;
-  s.misc[5] = 0;  // 1 once the import is complete (every masked row adopted)
-  s.misc[6] = 0;  // 1 once at least one masked row is adopted (its copy runs)
-  *s.model_calls = 0;
-  *s.status = kStatusOk;
-  *s.done = 0;
+  const int nent = B * a.bpr;
+  const bool bitmap = a.physical_blocks <= kBitmapWords * 32;
+  if (tid == 0) {
+    eos_bad = 0;
+    block_bad = 0;
+    meta_key = kNoFailure;
+    import_key = kNoFailure;
+    cont_key = kNoFailure;
+    active_count = 0;
+    any_adopted = 0;
+  }
+  if (bitmap)
+    for (int i = tid; i < (a.physical_blocks + 31) / 32; i += T) seen[i] = 0u;
   int64_t* history = reinterpret_cast<int64_t*>(s.fetch);
-  for (int i = 0; i < kMaxEpochSteps * B; ++i) history[i] = -1;
-  for (int r = 0; r < B; ++r) {
+  for (int i = tid; i < kMaxEpochSteps * B; i += T) history[i] = -1;
+  for (int i = tid; i < nent; i += T) s.table[i] = f.table[i];
+  for (int r = tid; r < B; r += T) {
     s.executed[r] = 0;
-    s.reason[r] = kFinishNone;
-    s.clear_row[r] = 0;
     s.eos[r] = ctl[1 + r];
     s.initial_active[r] = f.active[r];
     s.generation[r] = ctl[3 + B + r];
@@ -119,101 +132,115 @@ __global__ void k_ctrl_init(CtrlArgs a, long long payload_bytes) {
     s.cur_pos[r] = f.pos[r];
     s.cur_len[r] = f.len[r];
     s.cur_active[r] = f.active[r];
+    s.cur_slot[r] = f.slot ? f.slot[r] : compute_slot(f.table, a, r, f.pos[r]);
   }
-  for (int i = 0; i < B * a.bpr; ++i) s.table[i] = f.table[i];
-  for (int r = 0; r < B; ++r) s.cur_slot[r] = f.slot ? f.slot[r] : compute_slot(s.table, a, r, f.pos[r]);
+  __syncthreads();
+
+  // Every check evaluated in parallel; which one decides is settled below.
+  for (int r = tid; r < B; r += T)
+    if (ctl[1 + r] < 0 || ctl[1 + r] >= a.vocab) atomicOr(&eos_bad, 1);
+  for (int i = tid; i < nent; i += T) {
+    const int blk = f.table[i];
+    bool bad = blk < 0 || blk >= a.physical_blocks;
+    if (!bad && bitmap) {
+      bad = (atomicOr(&seen[blk >> 5], 1u << (blk & 31)) >> (blk & 31)) & 1u;
+    } else if (!bad) {
+      for (int j = 0; j < i && !bad; ++j) bad = f.table[j] == blk;
+    }
+    if (bad) atomicOr(&block_bad, 1);
+  }
+  for (int r = tid; r < B; r += T) {
+    const int32_t act = f.active[r], len = f.len[r], gen = ctl[3 + B + r];
+    const int64_t tok = f.token[r], pos = f.pos[r];
+    int32_t code = kStatusOk;
+    if ((act != 0 && act != 1) || tok < 0 || tok >= a.vocab || pos < 0 || pos >= a.capacity) {
+      code = kStatusInvalidMetadata;
+    } else if (act == 1) {
+      if (gen <= 0 || len != pos + 1) code = kStatusInvalidMetadata;
+      else if (pos + max_steps > a.capacity) code = kStatusCapacityExceeded;
+    } else if (len == 0) {
+      if (gen != 0) code = kStatusInvalidMetadata;
+    } else if (len != pos + 1) {
+      code = kStatusInvalidMetadata;
+    }
+    if (code == kStatusOk && compute_slot(f.table, a, r, pos) != (f.slot ? f.slot[r] : compute_slot(f.table, a, r, pos)))
+      code = kStatusSlotMismatch;
+    if (code != kStatusOk) atomicMin(&meta_key, fail_key(r, code));
+    if (importing && r < 31 && ((import_mask >> r) & 1) != 0 && (act != 1 || gen <= 0))
+      atomicMin(&import_key, fail_key(r, kStatusInvalidMetadata));
+    const bool imported = importing && r < 31 && ((import_mask >> r) & 1) != 0;
+    if (act == 1 && !imported) {
+      // A row adopted by the import matches its resident record by construction.
+      const bool same_gen = s.res_gen[r] == gen;
+      const bool ok = same_gen ? (s.res_valid[r] != 0 && s.res_token[r] == tok && s.res_pos[r] == pos &&
+                                  s.res_len[r] == len)
+                               : (pos == 0 && len == 1);
+      if (!ok) atomicMin(&cont_key, fail_key(r, kStatusResidentContinuity));
+    }
+  }
+  __syncthreads();
 
   int32_t status = kStatusOk;
+  bool import_reached = false;  // every earlier check passed: the import loop runs
   if (flagged != importing) {
     status = kStatusInvalidMetadata;  // feed form and flag disagree
   } else if (max_steps < 1 || max_steps > kMaxEpochSteps || sampling != 0 || graph_variant != 0) {
-    // CTRL:335-340
     status = sampling != 0 ? kStatusUnsupportedSampling
              : graph_variant != 0 ? kStatusUnsupportedGraph
                                   : kStatusInvalidMetadata;
+  } else if (eos_bad) {
+    status = kStatusInvalidMetadata;
+  } else if (block_bad) {
+    status = kStatusInvalidBlockTable;
+  } else if (meta_key != kNoFailure) {
+    status = fail_status(meta_key);
+  } else if (importing && (import_mask <= 0 || (B < 31 && import_mask >= (1 << B)))) {
+    status = kStatusInvalidMetadata;
+  } else {
+    import_reached = importing;
+    if (importing && import_key != kNoFailure) status = kStatusInvalidMetadata;
+    else if (cont_key != kNoFailure) status = kStatusResidentContinuity;
   }
-  if (status == kStatusOk) {
-    for (int r = 0; r < B; ++r)
-      if (s.eos[r] < 0 || s.eos[r] >= a.vocab) { status = kStatusInvalidMetadata; break; }  // 341-345
-  }
-  if (status == kStatusOk) {  // 346-353: blocks in range and unique
-    for (int i = 0; i < B * a.bpr && status == kStatusOk; ++i) {
-      const int blk = s.table[i];
-      if (blk < 0 || blk >= a.physical_blocks) { status = kStatusInvalidBlockTable; break; }
-      for (int j = 0; j < i; ++j)
-        if (s.table[j] == blk) { status = kStatusInvalidBlockTable; break; }
-    }
-  }
-  if (status == kStatusOk) {  // 354-385
-    for (int r = 0; r < B; ++r) {
-      const int32_t act = f.active[r];
-      const int64_t tok = f.token[r], pos = f.pos[r];
-      const int32_t len = f.len[r];
-      if ((act != 0 && act != 1) || tok < 0 || tok >= a.vocab || pos < 0 || pos >= a.capacity) {
-        status = kStatusInvalidMetadata;
-        break;
-      }
-      if (act == 1) {
-        if (s.generation[r] <= 0 || len != pos + 1) { status = kStatusInvalidMetadata; break; }
-        if (pos + max_steps > a.capacity) { status = kStatusCapacityExceeded; break; }
-      } else if (len == 0) {
-        if (s.generation[r] != 0) { status = kStatusInvalidMetadata; break; }
-        s.reason[r] = kFinishEmpty;
-      } else if (len == pos + 1) {
-        s.reason[r] = kFinishAlreadyFinished;
-      } else {
-        status = kStatusInvalidMetadata;
-        break;
-      }
-      if (compute_slot(s.table, a, r, pos) != s.cur_slot[r]) { status = kStatusSlotMismatch; break; }
-    }
-  }
-  if (status == kStatusOk && importing) {  // 387-429 (the copy itself runs in k_clear_rows)
-    if (import_mask <= 0 || import_mask >= (1 << B)) status = kStatusInvalidMetadata;
-    for (int r = 0; r < B && status == kStatusOk; ++r) {
-      if ((import_mask & (1 << r)) == 0) continue;
-      if (f.active[r] != 1 || s.generation[r] <= 0) { status = kStatusInvalidMetadata; break; }
-      s.clear_row[r] = 2;  // clear, then import block 0 of the row
-      s.misc[6] = 1;
-      s.res_gen[r] = s.generation[r];
+  // The import loop adopts rows in order up to its first failing row; they
+  // keep their copied blocks even when the epoch then falls back.
+  const int adopt_below = import_reached ? (import_key == kNoFailure ? B : fail_row(import_key)) : 0;
+  for (int r = tid; r < B; r += T) {
+    const bool adopted = r < adopt_below && r < 31 && ((import_mask >> r) & 1) != 0;
+    if (adopted) {
+      atomicOr(&any_adopted, 1);
+      s.res_gen[r] = ctl[3 + B + r];
       s.res_token[r] = f.token[r];
       s.res_pos[r] = f.pos[r];
       s.res_len[r] = f.len[r];
       s.res_valid[r] = 1;
     }
-    if (status == kStatusOk) s.misc[5] = 1;
-  }
-  if (status == kStatusOk) {  // 448-464
-    for (int r = 0; r < B; ++r) {
-      if (f.active[r] == 0) continue;
-      if (s.res_gen[r] == s.generation[r]) {
-        if (s.res_valid[r] == 0 || s.res_token[r] != f.token[r] || s.res_pos[r] != f.pos[r] ||
-            s.res_len[r] != f.len[r]) {
-          status = kStatusResidentContinuity;
-          break;
-        }
-      } else {
-        if (f.pos[r] != 0 || f.len[r] != 1) { status = kStatusResidentContinuity; break; }
-        s.clear_row[r] = 1;
-      }
+    int32_t reason = kFinishFallback, clear = adopted ? 2 : 0;
+    if (status == kStatusOk) {
+      const int32_t act = f.active[r];
+      reason = act == 1 ? kFinishNone : (f.len[r] == 0 ? kFinishEmpty : kFinishAlreadyFinished);
+      if (act == 1 && !adopted && s.res_gen[r] != ctl[3 + B + r]) clear = 1;  // a new generation
+      if (act != 0) atomicAdd(&active_count, 1);
     }
+    s.reason[r] = reason;
+    s.clear_row[r] = clear;
   }
-  if (status != kStatusOk) {
-    // Rows the import loop adopted before the fallback stay adopted with
-    // their blocks copied, as CTRL:402-428 copies each row before it checks
-    // the next one.  The checksum runs only for a complete import (misc[5]):
-    // CTRL:430-445 is reached only after the whole mask.  The
-    // new-generation clears are dropped.
-    for (int r = 0; r < B; ++r) {
-      s.reason[r] = kFinishFallback;
-      if (s.misc[6] == 0 || s.clear_row[r] != 2) s.clear_row[r] = 0;
-    }
+  __syncthreads();
+  if (tid == 0) {
+    s.import_sum[0] = 0;  // accumulators of k_import_checksum
+    s.import_sum[1] = 0;
+    s.misc[0] = max_steps;
+    s.misc[1] = sampling;
+    s.misc[2] = graph_variant;
+    s.misc[3] = flagged ? 1 : 0;
+    s.misc[4] = import_mask;
+    // the whole mask adopted: the checksum is emitted even when the
+    // continuity check after the import then falls back (CTRL:430-464)
+    s.misc[5] = import_reached && import_key == kNoFailure ? 1 : 0;
+    s.misc[6] = any_adopted;  // some masked row adopted: its copy runs
+    *s.model_calls = 0;
     *s.status = status;
-    *s.done = 1;
-  } else {
-    int count = 0;
-    for (int r = 0; r < B; ++r) count += s.cur_active[r] != 0;
-    if (count == 0) *s.done = 1;  // the loop runs no step (CTRL:488)
+    // the loop runs no step after a fallback or with no active row (CTRL:488)
+    *s.done = (status != kStatusOk || active_count == 0) ? 1 : 0;
   }
 }
 
@@ -265,8 +292,9 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   StatePtrs& s = a.st;
   if (*s.done != 0) return;
   const int B = a.B;
-  __shared__ int tok_s[64 * 4];
-  __shared__ int bad_s[64 * 4];
+  __shared__ int tok_s[256];
+  __shared__ int bad_s[256];
+  __shared__ int fail_at, active_count;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
   // Final argmax over the LM head's workgroup partials (CTRL:99-119): one wave
   // per batch row; each lane requests its strided share of the partials at
@@ -312,47 +340,66 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
       bad_s[b] = bb;
     }
   }
+  if (tid == 0) {
+    fail_at = kNoFailure;
+    active_count = 0;
+  }
+  const int call = *s.model_calls + 1;  // read by every thread before thread 0 stores it
   __syncthreads();
-  if (tid != 0) return;
-  const int call = ++(*s.model_calls);
   int64_t* history = reinterpret_cast<int64_t*>(s.fetch);
-  int32_t status = kStatusOk;
-  // next_position = where(active, pos + 1, pos) (batched_decoder_step.py:409-411)
-  for (int r = 0; r < B; ++r) {
-    const int64_t next_pos = s.cur_active[r] != 0 ? s.cur_pos[r] + 1 : s.cur_pos[r];
-    if (s.cur_active[r] == 0) {
-      if (next_pos != s.cur_pos[r]) { status = kStatusPositionProgress; break; }
-      continue;
+  // The row update (CTRL:546-581).  Row r fails with NonFinite (bad logits),
+  // PositionProgress (never, with next_position = where(active, pos + 1,
+  // pos), batched_decoder_step.py:409-411) or CapacityExceeded (no slot for
+  // the next position: checked after the row's history, count, position,
+  // token and length are updated).  The rows before the first failing row are
+  // updated in full, as the sequential loop does before it stops.
+  // B <= 256 < blockDim.x: thread r owns row r.
+  const int r = tid;
+  const bool live = r < B && s.cur_active[r] != 0;
+  int32_t code = kStatusOk;
+  int slot_next = -1;
+  if (live) {
+    const int64_t next_pos = s.cur_pos[r] + 1;
+    if (bad_s[r] != 0 || tok_s[r] < 0) {
+      code = kStatusNonFiniteLogits;
+    } else if (next_pos != a.capacity) {
+      slot_next = compute_slot(s.table, a, r, next_pos);
+      if (slot_next < 0) code = kStatusCapacityExceeded;
     }
-    if (bad_s[r] != 0 || tok_s[r] < 0) { status = kStatusNonFiniteLogits; break; }
+    if (code != kStatusOk) atomicMin(&fail_at, fail_key(r, code));
+  }
+  __syncthreads();
+  const int first = fail_row(fail_at);  // uniform
+  if (live && (r < first || (r == first && code == kStatusCapacityExceeded))) {
     const int64_t tok = tok_s[r];
-    if (next_pos != s.cur_pos[r] + 1) { status = kStatusPositionProgress; break; }
+    const int64_t next_pos = s.cur_pos[r] + 1;
     history[(call - 1) * B + r] = tok;
     s.executed[r] += 1;
     s.cur_pos[r] = next_pos;
     s.cur_token[r] = tok;
     s.cur_len[r] = static_cast<int32_t>(next_pos + 1);
-    if (next_pos == a.capacity) {
-      s.cur_slot[r] = -1;
-    } else {
-      const int slot = compute_slot(s.table, a, r, next_pos);
-      if (slot < 0) { status = kStatusCapacityExceeded; break; }
-      s.cur_slot[r] = slot;
-    }
-    if (tok == s.eos[r]) {
-      s.cur_active[r] = 0;
-      s.reason[r] = kFinishEos;
+    if (r < first) {
+      s.cur_slot[r] = slot_next;  // -1 at the capacity
+      if (tok == s.eos[r]) {
+        s.cur_active[r] = 0;
+        s.reason[r] = kFinishEos;
+      } else {
+        atomicAdd(&active_count, 1);
+      }
     }
   }
-  if (status != kStatusOk) {
-    for (int r = 0; r < B; ++r) s.reason[r] = kFinishFallback;
-    *s.status = status;
-    *s.done = 1;
-    return;
+  const bool failed = first != 0x7fffffff;
+  if (failed && r < B) s.reason[r] = kFinishFallback;  // the same thread wrote any EOS reason above
+  __syncthreads();
+  if (tid == 0) {
+    *s.model_calls = call;
+    if (failed) {
+      *s.status = fail_status(fail_at);
+      *s.done = 1;
+    } else if (active_count == 0) {
+      *s.done = 1;
+    }
   }
-  int count = 0;
-  for (int r = 0; r < B; ++r) count += s.cur_active[r] != 0;
-  if (count == 0) *s.done = 1;
 }
 
 // Adler-32 of the imported blocks as they sit in the resident caches, in the
@@ -432,28 +479,47 @@ __global__ void __launch_bounds__(256) k_import_checksum(ImportSumArgs a) {
   }
 }
 
-// Finish reasons, resident save and emit (CTRL:296-324, 592-621).
-__global__ void k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
+// Finish reasons, resident save and emit (CTRL:296-324, 592-621), one thread
+// per row.
+__global__ void __launch_bounds__(256) k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
   (void)import_checksum_unused;
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  __shared__ int initial, final_count, nsel;
   StatePtrs& s = a.st;
-  const int B = a.B;
+  const int B = a.B, tid = threadIdx.x;
   const int32_t status = *s.status;
   const bool fallback = status != kStatusOk;
-  if (!fallback) {
-    for (int r = 0; r < B; ++r)
-      if (s.initial_active[r] == 1 && s.reason[r] == kFinishNone) s.reason[r] = kFinishMaxSteps;
-    for (int r = 0; r < B; ++r) {
-      if (s.initial_active[r] == 0) continue;
+  const bool importing = s.misc[3] != 0;
+  const int32_t mask = s.misc[4];
+  int32_t* control = reinterpret_cast<int32_t*>(s.fetch + 8 * kMaxEpochSteps * B);
+  if (tid == 0) {
+    initial = 0;
+    final_count = 0;
+    nsel = 0;
+  }
+  __syncthreads();
+  for (int r = tid; r < B; r += blockDim.x) {
+    const int32_t init = s.initial_active[r];
+    int32_t reason = s.reason[r];
+    if (!fallback && init == 1 && reason == kFinishNone) reason = kFinishMaxSteps;
+    if (!fallback && init != 0) {
+      s.reason[r] = reason;
       s.res_gen[r] = s.generation[r];
       s.res_token[r] = s.cur_token[r];
       s.res_pos[r] = s.cur_pos[r];
       s.res_len[r] = s.cur_len[r];
       s.res_valid[r] = 1;
     }
+    control[6 + r] = s.eos[r];
+    control[6 + B + r] = init;
+    control[6 + 2 * B + r] = s.executed[r];
+    control[6 + 3 * B + r] = reason;
+    control[6 + 4 * B + 2 + r] = init == 1 ? s.generation[r] : 0;
+    if (init != 0) atomicAdd(&initial, 1);
+    if ((fallback ? init : s.cur_active[r]) != 0) atomicAdd(&final_count, 1);
+    if (r < 31 && ((mask >> r) & 1) != 0) atomicAdd(&nsel, 1);
   }
-  int32_t* control = reinterpret_cast<int32_t*>(s.fetch + 8 * kMaxEpochSteps * B);
-  const bool importing = s.misc[3] != 0;
+  __syncthreads();
+  if (tid != 0) return;
   control[0] = s.misc[0];
   control[1] = s.misc[1];
   control[2] = s.misc[2];
@@ -461,8 +527,6 @@ __global__ void k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
   control[4] = *s.model_calls;
   if (importing && s.misc[5] != 0) {
     // CTRL:301-303: the import checksum; see k_import_checksum for the sums
-    int nsel = 0;
-    for (int r = 0; r < B; ++r) nsel += (s.misc[4] >> r) & 1;
     const unsigned long long n =
         2ULL * a.layers * nsel * (unsigned long long)a.block_size * a.kv_dim * a.elem_bytes;
     const unsigned first = static_cast<unsigned>((1 + s.import_sum[0]) % kAdlerModulus);
@@ -470,16 +534,6 @@ __global__ void k_ctrl_finish(CtrlArgs a, uint32_t import_checksum_unused) {
     control[5] = static_cast<int32_t>((second << 16) | first);
   } else {
     control[5] = importing ? 0 : (fallback ? 1 : 0);  // import rejected before the copy: 0
-  }
-  int initial = 0, final_count = 0;
-  for (int r = 0; r < B; ++r) {
-    control[6 + r] = s.eos[r];
-    control[6 + B + r] = s.initial_active[r];
-    control[6 + 2 * B + r] = s.executed[r];
-    control[6 + 3 * B + r] = s.reason[r];
-    control[6 + 4 * B + 2 + r] = s.initial_active[r] == 1 ? s.generation[r] : 0;
-    initial += s.initial_active[r] != 0;
-    final_count += (fallback ? s.initial_active[r] : s.cur_active[r]) != 0;
   }
   control[6 + 4 * B] = initial;
   control[6 + 4 * B + 1] = final_count;
@@ -538,7 +592,7 @@ static long long payload_bytes_of(const Dims& d) {
 hipError_t launch_ctrl_init(const KernelEnv& env, const StatePtrs& st, int has_payload, hipStream_t stream) {
   CtrlArgs a = ctrl_args(env, st);
   a.has_payload = has_payload;
-  k_ctrl_init<<<1, 64, 0, stream>>>(a, has_payload ? payload_bytes_of(env.dims) : 0);
+  k_ctrl_init<<<1, kCtrlThreads, 0, stream>>>(a, has_payload ? payload_bytes_of(env.dims) : 0);
   return hipGetLastError();
 }
 
@@ -607,7 +661,7 @@ hipError_t launch_ctrl_step(const KernelEnv& env, const StatePtrs& st, hipStream
 }
 
 hipError_t launch_ctrl_finish(const KernelEnv& env, const StatePtrs& st, hipStream_t stream) {
-  k_ctrl_finish<<<1, 64, 0, stream>>>(ctrl_args(env, st), 0u);
+  k_ctrl_finish<<<1, 256, 0, stream>>>(ctrl_args(env, st), 0u);
   return hipGetLastError();
 }
 
