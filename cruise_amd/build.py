@@ -20,7 +20,7 @@ LIBRARY = LIBDIR / "libresident_epoch.so"
 SERVER = LIBDIR / "resident_epoch_server"
 SERVER_SOURCE = "re_server.cpp"
 INCLUDE = PACKAGE.parent / "include"
-SOURCES = ("re_step.hip", "re_attn.hip", "re_ctrl.hip", "re_prefill.hip", "re_blas.hip", "re_engine.hip")
+SOURCES = ("re_step.hip", "re_attn.hip", "re_ctrl.hip", "re_prefill.hip", "re_blas.hip", "re_mfma.hip", "re_engine.hip")
 LINK_LIBS = ("-lhipblaslt",)  # batched-prefill GEMMs (re_blas.hip)
 
 HIPCC_FLAGS = [

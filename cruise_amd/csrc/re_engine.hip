@@ -298,6 +298,14 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));
     p.lm_wg = p.lm_grid;
   }
+  // 64 bf16 rows of Qwen2.5-7B's shape: projections on the matrix cores
+  // ("tuning": {"mfma": 0} keeps the row-tiled kernels)
+  const Json* tune = cfg.get("tuning");
+  p.mfma = 0;
+  if (mfma_step_supported(d) && (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
+    p.mfma = 1;
+    p.lm_wg = mfma_lm_partials(d);
+  }
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
     // "down_whole": 0 keeps the split-K down projection and its reduce launch
@@ -424,6 +432,7 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.am_bad), (size_t)p.lm_wg * B * sizeof(int32_t)},
       {reinterpret_cast<void**>(&e.scratch.inv_freq), (size_t)d.head_dim / 2 * sizeof(float)},
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
+      {&e.scratch.xn, p.mfma ? (size_t)B * d.hidden * T : 0},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},
   };

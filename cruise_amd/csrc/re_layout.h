@@ -124,6 +124,7 @@ struct Scratch {
   int32_t* am_bad;    // non-finite flags [nwg, B]
   float* inv_freq;    // fp32 [d/2]
   float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
+  void* xn;           // T [B, H] normalized rows (matrix-core projections)
 };
 
 struct LaunchPlan {
@@ -139,6 +140,8 @@ struct LaunchPlan {
   // Down projection with the whole K in one workgroup (re_step.hip
   // k_down_whole): 0 = split-K segments + reduce launch; else its grid.
   int down_whole_grid;
+  // 1: the projections run on the matrix cores (re_mfma.hip, 64 rows)
+  int mfma;
 };
 
 // Arguments of the paged decode attention (re_attn.hip).
@@ -185,6 +188,13 @@ int step_op_count(const KernelEnv& env);
 int timed_op_index(const KernelEnv& env, int layer);
 // Grid sizes of the grid-stride projections from the kernels' occupancy.
 void plan_grids(LaunchPlan& p, const Dims& d, int cus);
+// Decode projections on the matrix cores at 64 batch rows (re_mfma.hip):
+// the RMSNorm (where the projection has one) and the projection of one op.
+enum class MfmaOp { kQkv, kO, kGateUp, kDown, kLmHead };
+bool mfma_step_supported(const Dims& d);
+int mfma_lm_partials(const Dims& d);
+hipError_t prepare_mfma();
+hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, int layer, hipStream_t stream);
 // Controller kernels.
 hipError_t launch_ctrl_init(const KernelEnv& env, const StatePtrs& st, int has_payload,
                             hipStream_t stream);

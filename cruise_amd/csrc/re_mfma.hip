@@ -1,0 +1,425 @@
+// Decode projections of the resident epoch on the matrix cores (gfx950), for
+// 64 batch rows (the scaled-batch configuration): Y[B, N] = X[B, K] W[N, K]^T
+// with v_mfma_f32_16x16x32_bf16, the weights streamed from HBM once per step.
+//
+// Work layout.  A workgroup owns 16 output columns per strip (one strip, or two:
+// gate and up, or two adjacent column groups of the LM head) and splits K
+// evenly over its waves.  Each wave streams its K range of the strip's rows:
+// lane l holds row l % 16 of the strip and elements 8 (l / 16) ..+8 of each
+// 32-wide k step (a 64-byte run per row per load instruction), and the
+// matching activation fragments of the four 16-row batch tiles (read through
+// the cache: every workgroup reads the same activations).  The whole K range
+// is unrolled at compile time: weights are requested kRing steps ahead and
+// activations kXRing steps ahead, with no branch inside the loop.  At the end
+// the waves' accumulators meet in LDS and wave 0 adds them in wave order (a
+// fixed order: results do not depend on timing) and applies the projection's
+// epilogue -- the same operations and roundings as the four-row kernels of
+// re_step.hip:
+//   qkv     + bias, RoPE of q and k (the partner element j + d/2 sits in lane
+//           l ^ 8: a strip holds 8 pairs), q out, k and v to the paged slots
+//   gate/up silu(gate) * up
+//   resid   h + T(y) for the o and down projections
+//   LM head logits (T(y) as fp32) and per-workgroup argmax partials
+// MFMA result layout: value v of lane l is row 4 (l / 16) + v of the tile,
+// column l % 16.
+//
+// The RMSNorm before qkv, gate/up and the LM head runs as its own kernel
+// (one workgroup per row) into a normalized copy of the rows.
+#include "re_device.h"
+#include "re_layout.h"
+
+namespace re {
+namespace {
+
+typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfRows = 64;   // batch rows of the configuration
+constexpr int kMfTiles = kMfRows / 16;
+constexpr int kMfK = 32;      // k per MFMA step
+constexpr int kRing = 8;      // weight steps in flight per wave
+// activation steps in flight per wave: 4, or 2 at 16 waves (128 registers)
+template <int WAVES>
+constexpr int x_ring() { return WAVES >= 16 ? 2 : 4; }
+// Qwen2.5-7B's shape, the one these instantiations are compiled for
+constexpr int kMfHidden = 3584;
+constexpr int kMfInter = 18944;
+
+enum MfKind { kMfQkv = 0, kMfGateUp = 1, kMfLm = 2, kMfResid = 3 };
+
+struct MfArgs {
+  const int32_t* done;
+  const bf16_t* x;   // [B, K]
+  const bf16_t* w0;  // [rows, K]
+  const bf16_t* w1;  // gate/up: up weights; qkv: bias [rows]
+  int B, K;
+  // qkv
+  bf16_t* q;
+  bf16_t* key_cache;
+  bf16_t* value_cache;
+  const float* rope;
+  const int32_t* slot;
+  const int32_t* active;
+  long long slots;
+  int heads, kv_heads, head_dim;
+  // gate/up output, residual stream
+  bf16_t* out;
+  bf16_t* hidden;
+  int hidden_dim;
+  // LM head
+  float* logits;
+  float* am_val;
+  int32_t* am_idx;
+  int32_t* am_bad;
+  int vocab;
+};
+
+// Weight row of column c (0..15) of strip j in workgroup g.
+template <int KIND>
+__device__ __forceinline__ int strip_row(const MfArgs& a, int g, int j, int c) {
+  if constexpr (KIND == kMfQkv) {
+    // strip g: head g / (d / 16), pairs 8 t ..+8 of that head; columns 0..7
+    // are elements j of the pairs, columns 8..15 their partners j + d/2
+    const int half = a.head_dim >> 1, per_head = half >> 3;
+    const int head = g / per_head, t = g - head * per_head;
+    return head * a.head_dim + 8 * t + (c & 7) + (c >= 8 ? half : 0);
+  } else if constexpr (KIND == kMfLm) {
+    return g * 32 + j * 16 + c;
+  } else {
+    return g * 16 + c;  // gate/up: both strips are the same columns
+  }
+}
+
+template <int NS, int WAVES, int KIND, int STEPS>
+__global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
+  constexpr int kXRing = x_ring<WAVES>();
+  extern __shared__ __align__(16) float mf_red[];  // [WAVES - 1][NS * kMfTiles * 4][64]
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int g = blockIdx.x;
+  const int c = lane & 15, kq = (lane >> 4) * 8;
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  if (stop != 0) return;  // uniform
+
+  const int kbase = wave * STEPS * kMfK + kq;
+  const bf16_t* wp[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const bf16_t* base = (KIND == kMfGateUp && j == 1) ? a.w1 : a.w0;
+    wp[j] = base + (size_t)strip_row<KIND>(a, g, j, c) * a.K + kbase;
+  }
+  const bf16_t* xp[kMfTiles];
+#pragma unroll
+  for (int t = 0; t < kMfTiles; ++t) xp[t] = a.x + (size_t)min(t * 16 + c, a.B - 1) * a.K + kbase;
+
+  mf_f32x4 acc[NS][kMfTiles];
+#pragma unroll
+  for (int j = 0; j < NS; ++j)
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t) acc[j][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  re_u32x4 wr[kRing][NS];
+  re_u32x4 xr[kXRing][kMfTiles];
+#pragma unroll
+  for (int s = 0; s < kRing && s < STEPS; ++s)
+#pragma unroll
+    for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * kMfK));
+#pragma unroll
+  for (int s = 0; s < kXRing && s < STEPS; ++s)
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t) xr[s][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + s * kMfK);
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int rw = s % kRing, rx = s % kXRing;
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t)
+        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8, xr[rx][t]),
+                                                            __builtin_bit_cast(mf_bf16x8, wr[rw][j]), acc[j][t], 0,
+                                                            0, 0);
+    if (s + kRing < STEPS) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+        wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + (s + kRing) * kMfK));
+    }
+    if (s + kXRing < STEPS) {
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t) xr[rx][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + (s + kXRing) * kMfK);
+    }
+  }
+
+  // The waves' partial sums, added by wave 0 in wave order.
+  constexpr int R = NS * kMfTiles * 4;
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) mf_red[((wave - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane] = acc[j][t][v];
+  }
+  lds_barrier();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w)
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[j][t][v] += mf_red[((w - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane];
+
+  const int mrow = 4 * (lane >> 4);  // + 16 t + v
+  if constexpr (KIND == kMfQkv) {
+    const int row = strip_row<KIND>(a, g, 0, c);
+    const int half = a.head_dim >> 1;
+    const int head = row / a.head_dim, jj = row - head * a.head_dim;  // jj < half for c < 8
+    const int jpair = c < 8 ? jj : jj - half;
+    const float bias = Elt<bf16_t>::f(a.w1[row]);
+    const bool roped = head < a.heads + a.kv_heads;
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = t * 16 + mrow + v;
+        // F.linear with bias: fp32 sum + bias, one rounding (g4a_linear_t_bias.py:18-21)
+        const float y = Elt<bf16_t>::r(acc[0][t][v] + bias);
+        const float p = __shfl_xor(y, 8, 64);
+        if (m >= a.B) continue;
+        float o = y;
+        if (roped) {
+          // q' = q*cos + rotate_half(q)*sin, each product and the sum rounded
+          // (batched_decoder_step.py:231-240, 323-324)
+          const float cs = a.rope[((size_t)m * half + jpair) * 2], sn = a.rope[((size_t)m * half + jpair) * 2 + 1];
+          o = c < 8 ? Elt<bf16_t>::r(Elt<bf16_t>::r(y * cs) + Elt<bf16_t>::r(-p * sn))
+                    : Elt<bf16_t>::r(Elt<bf16_t>::r(y * cs) + Elt<bf16_t>::r(p * sn));
+        }
+        if (head < a.heads) {
+          a.q[((size_t)m * a.heads + head) * a.head_dim + jj] = Elt<bf16_t>::t(o);
+        } else {
+          // paged slot write, active rows only (batched_decoder_step.py:250-264)
+          const int s = a.slot[m];
+          if (a.active[m] != 0 && s >= 0 && s < a.slots) {
+            const bool is_key = head < a.heads + a.kv_heads;
+            const int kvh = is_key ? head - a.heads : head - a.heads - a.kv_heads;
+            bf16_t* cache = is_key ? a.key_cache : a.value_cache;
+            cache[((size_t)s * a.kv_heads + kvh) * a.head_dim + jj] = Elt<bf16_t>::t(o);
+          }
+        }
+      }
+  } else if constexpr (KIND == kMfGateUp) {
+    const int n = strip_row<KIND>(a, g, 0, c);
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = t * 16 + mrow + v;
+        if (m >= a.B) continue;
+        // silu(gate) * up, each result rounded (batched_decoder_step.py:391-398)
+        const float gt = Elt<bf16_t>::r(acc[0][t][v]);
+        const float up = Elt<bf16_t>::r(acc[1][t][v]);
+        const float sg = Elt<bf16_t>::r(gt / (1.0f + expf(-gt)));
+        a.out[(size_t)m * a.hidden_dim + n] = Elt<bf16_t>::t(Elt<bf16_t>::r(sg * up));
+      }
+  } else if constexpr (KIND == kMfResid) {
+    const int n = strip_row<KIND>(a, g, 0, c);
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = t * 16 + mrow + v;
+        if (m >= a.B) continue;
+        bf16_t* h = a.hidden + (size_t)m * a.hidden_dim + n;
+        *h = f_to_bf16(bf16_to_f(*h) + round_bf16(acc[0][t][v]));
+      }
+  } else {
+    // LM head in T, then .float() (batched_decoder_step.py:405-408); the
+    // first index of the maximum over this workgroup's 32 columns (CTRL:99-119)
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = t * 16 + mrow + v;
+        const int n0 = strip_row<KIND>(a, g, 0, c), n1 = n0 + 16;
+        const float l0 = Elt<bf16_t>::r(acc[0][t][v]), l1 = Elt<bf16_t>::r(acc[1][t][v]);
+        const bool mine = m < a.B;
+        if (mine) {
+          a.logits[(size_t)m * a.vocab + n0] = l0;
+          a.logits[(size_t)m * a.vocab + n1] = l1;
+        }
+        int bad = (!isfinite(l0) || !isfinite(l1)) ? 1 : 0;
+        float bv = l0;
+        int bi = n0;
+        if (l1 > bv) {
+          bv = l1;
+          bi = n1;
+        }
+#pragma unroll
+        for (int x = 1; x < 16; x <<= 1) {
+          const float ov = __shfl_xor(bv, x, 64);
+          const int oi = __shfl_xor(bi, x, 64);
+          bad |= __shfl_xor(bad, x, 64);
+          if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (mine && c == 0) {
+          a.am_val[(size_t)g * a.B + m] = bv;
+          a.am_idx[(size_t)g * a.B + m] = bi;
+          a.am_bad[(size_t)g * a.B + m] = bad;
+        }
+      }
+  }
+}
+
+template <int NS, int WAVES>
+constexpr size_t mgemv_lds() {
+  return (size_t)(WAVES - 1) * NS * kMfTiles * 4 * 64 * sizeof(float);
+}
+
+// RMSNorm of each row into a normalized copy: T(T(h * rs) * w) with rs =
+// rsqrt(mean(h^2) + eps) in fp32 (batched_decoder_step.py:224-229).
+__global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, const bf16_t* h, const bf16_t* w, bf16_t* y,
+                                               int H, float eps) {
+  __shared__ float red[4];
+  if (done != nullptr && __builtin_nontemporal_load(done) != 0) return;
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const bf16_t* hr = h + (size_t)m * H;
+  constexpr int kMaxChunks = 4;  // H <= 4 * 256 * 8
+  Vec8<bf16_t> hv[kMaxChunks];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int ch = tid + 256 * i;
+    hv[i] = ch * 8 < H ? Vec8<bf16_t>::load_cached(hr + ch * 8) : Vec8<bf16_t>{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = fmaf(hv[i].get(e), hv[i].get(e), s);
+  }
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  const float rs = rsqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int ch = tid + 256 * i;
+    if (ch * 8 >= H) continue;
+    const Vec8<bf16_t> wv = Vec8<bf16_t>::load_cached(w + ch * 8);
+    float out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = round_bf16(round_bf16(hv[i].get(e) * rs) * wv.get(e));
+    *reinterpret_cast<Vec8<bf16_t>*>(y + (size_t)m * H + ch * 8) = Vec8<bf16_t>::from_floats(out);
+  }
+}
+
+// The launches of one projection: (strips per workgroup, waves per
+// workgroup, kind, k steps per wave).
+constexpr int kQkvWaves = 8, kOWaves = 8, kGuWaves = 4, kDownWaves = 8, kLmWaves = 4;
+constexpr int kHidSteps(int waves) { return kMfHidden / kMfK / waves; }
+constexpr int kInterSteps = kMfInter / kMfK / kDownWaves;
+
+template <int NS, int WAVES, int KIND, int STEPS>
+hipError_t mgemv_prepare() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_mgemv<NS, WAVES, KIND, STEPS>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mgemv_lds<NS, WAVES>()));
+}
+
+template <int NS, int WAVES, int KIND, int STEPS>
+void mgemv_launch(const MfArgs& a, int grid, hipStream_t stream) {
+  k_mgemv<NS, WAVES, KIND, STEPS><<<grid, WAVES * 64, mgemv_lds<NS, WAVES>(), stream>>>(a);
+}
+
+}  // namespace
+
+bool mfma_step_supported(const Dims& d) {
+  return d.dtype_bytes == 2 && d.batch == kMfRows && d.hidden == kMfHidden && d.q_dim() == kMfHidden &&
+         d.intermediate == kMfInter && d.head_dim % 16 == 0 && d.qkv_rows() % 16 == 0 && d.vocab % 32 == 0 &&
+         d.hidden % 16 == 0;
+}
+
+int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
+
+hipError_t prepare_mfma() {
+  hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves)>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves)>();
+  if (e == hipSuccess) e = mgemv_prepare<2, kGuWaves, kMfGateUp, kHidSteps(kGuWaves)>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kDownWaves, kMfResid, kInterSteps>();
+  if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidSteps(kLmWaves)>();
+  return e;
+}
+
+hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, int layer, hipStream_t stream) {
+  const Dims& d = env.dims;
+  const Scratch& sc = env.scratch;
+  MfArgs a{};
+  a.done = st.done;
+  a.B = d.batch;
+  a.hidden_dim = d.hidden;
+  auto wt = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.weights + off); };
+  if (op == MfmaOp::kLmHead) {
+    k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(env.final_norm_off),
+                                           static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
+    a.x = static_cast<const bf16_t*>(sc.xn);
+    a.w0 = wt(env.lm_head_off);
+    a.K = d.hidden;
+    a.logits = st.logits;
+    a.am_val = sc.am_val;
+    a.am_idx = sc.am_idx;
+    a.am_bad = sc.am_bad;
+    a.vocab = d.vocab;
+    mgemv_launch<2, kLmWaves, kMfLm, kHidSteps(kLmWaves)>(a, d.vocab / 32, stream);
+    return hipGetLastError();
+  }
+  const LayerOffsets& lo = env.layer_off[layer];
+  const size_t cache_layer_elems = (size_t)d.slots() * d.kv_dim();
+  switch (op) {
+    case MfmaOp::kQkv:
+      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.input_norm),
+                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
+      a.x = static_cast<const bf16_t*>(sc.xn);
+      a.w0 = wt(lo.qkv_w);
+      a.w1 = wt(lo.qkv_b);
+      a.K = d.hidden;
+      a.q = static_cast<bf16_t*>(sc.q);
+      a.key_cache = static_cast<bf16_t*>(st.key_cache) + layer * cache_layer_elems;
+      a.value_cache = static_cast<bf16_t*>(st.value_cache) + layer * cache_layer_elems;
+      a.rope = sc.rope;
+      a.slot = st.slot;
+      a.active = st.active;
+      a.slots = d.slots();
+      a.heads = d.heads;
+      a.kv_heads = d.kv_heads;
+      a.head_dim = d.head_dim;
+      mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves)>(a, d.qkv_rows() / 16, stream);
+      break;
+    case MfmaOp::kO:
+      a.x = static_cast<const bf16_t*>(sc.attn);
+      a.w0 = wt(lo.o_w);
+      a.K = d.q_dim();
+      a.hidden = static_cast<bf16_t*>(sc.hidden);
+      mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves)>(a, d.hidden / 16, stream);
+      break;
+    case MfmaOp::kGateUp:
+      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.post_norm),
+                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
+      a.x = static_cast<const bf16_t*>(sc.xn);
+      a.w0 = wt(lo.gate_w);
+      a.w1 = wt(lo.up_w);
+      a.K = d.hidden;
+      a.out = static_cast<bf16_t*>(sc.mlp);
+      a.hidden_dim = d.intermediate;
+      mgemv_launch<2, kGuWaves, kMfGateUp, kHidSteps(kGuWaves)>(a, d.intermediate / 16, stream);
+      break;
+    case MfmaOp::kDown:
+      a.x = static_cast<const bf16_t*>(sc.mlp);
+      a.w0 = wt(lo.down_w);
+      a.K = d.intermediate;
+      a.hidden = static_cast<bf16_t*>(sc.hidden);
+      mgemv_launch<1, kDownWaves, kMfResid, kInterSteps>(a, d.hidden / 16, stream);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace re

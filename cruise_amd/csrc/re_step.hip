@@ -661,7 +661,14 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     q.kv_heads = d.kv_heads;
     q.head_dim = d.head_dim;
     q.eps = d.rms_eps;
-    if (want()) launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
+    if (want()) {
+      if (p.mfma) {
+        const hipError_t err = launch_mfma_op(MfmaOp::kQkv, env, st, l, stream);
+        if (err != hipSuccess) return err;
+      } else {
+        launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
+      }
+    }
 
     AttnArgs at{};
     at.done = st.done;
@@ -695,9 +702,15 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     o.N = d.hidden;
     o.K = d.q_dim();
     o.segments = p.o_segments;
-    if (want())
-      k_resid<T, MB, WAVES><<<dim3(p.o_grid, p.o_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(o);
-    if (want() && p.o_segments > 1)
+    if (want()) {
+      if (p.mfma) {
+        const hipError_t err = launch_mfma_op(MfmaOp::kO, env, st, l, stream);
+        if (err != hipSuccess) return err;
+      } else {
+        k_resid<T, MB, WAVES><<<dim3(p.o_grid, p.o_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(o);
+      }
+    }
+    if (want() && p.o_segments > 1 && !p.mfma)
       k_resid_reduce<T><<<reduce_blocks, 256, 0, stream>>>(st.done, sc.partial, sc.hidden, B, d.hidden,
                                                             p.o_segments);
 
@@ -713,7 +726,22 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     gu.units = d.intermediate;
     gu.eps = d.rms_eps;
     set_slots(gu, p, p.gu_grid);
-    if (want()) launch_proj<T, MB, WAVES, kGateUp>(gu, dim3(p.gu_grid, p.row_tiles), proj_smem, stream);
+    if (want()) {
+      if (p.mfma) {
+        const hipError_t err = launch_mfma_op(MfmaOp::kGateUp, env, st, l, stream);
+        if (err != hipSuccess) return err;
+      } else {
+        launch_proj<T, MB, WAVES, kGateUp>(gu, dim3(p.gu_grid, p.row_tiles), proj_smem, stream);
+      }
+    }
+    if (p.mfma) {
+      if (want()) {
+        const hipError_t err = launch_mfma_op(MfmaOp::kDown, env, st, l, stream);
+        if (err != hipSuccess) return err;
+      }
+      (void)want();  // the reduce entry: nothing to reduce
+      continue;
+    }
 
     if constexpr (sizeof(T) == 2 && MB == 4) {
       if (p.down_whole_grid > 0) {
@@ -763,7 +791,10 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
   lm.units = d.vocab / 2;
   lm.eps = d.rms_eps;
   set_slots(lm, p, p.lm_grid);
-  if (want()) launch_proj<T, MB, WAVES, kLmHead>(lm, dim3(p.lm_grid, p.row_tiles), proj_smem, stream);
+  if (want()) {
+    if (p.mfma) return launch_mfma_op(MfmaOp::kLmHead, env, st, 0, stream);
+    launch_proj<T, MB, WAVES, kLmHead>(lm, dim3(p.lm_grid, p.row_tiles), proj_smem, stream);
+  }
   return hipGetLastError();
 }
 
