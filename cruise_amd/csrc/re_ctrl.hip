@@ -575,7 +575,7 @@ static CtrlArgs ctrl_args(const KernelEnv& env, const StatePtrs& st) {
   a.block_size = env.dims.block_size;
   a.capacity = env.dims.capacity;
   a.vocab = env.dims.vocab;
-  a.lm_wg = env.plan.lm_wg;
+  a.lm_wg = env.plan.argmax_parts;
   a.layers = env.dims.layers;
   a.kv_dim = env.dims.kv_dim();
   a.elem_bytes = env.dims.dtype_bytes;

@@ -114,6 +114,10 @@ struct Engine {
   size_t embedding_off = 0, final_norm_off = 0, lm_head_off = 0;
   std::map<std::string, WeightSlot> weight_slots;
   std::vector<std::string> weight_order;
+  // the matrix-core copy (plan.mfma): the matrices packed into 1 KB tiles
+  uint8_t* packed = nullptr;
+  std::vector<PackedOffsets> packed_off;
+  size_t packed_lm_off = 0;
 
   // resident caches and state
   void* key_cache = nullptr;
@@ -178,6 +182,9 @@ struct Engine {
     e.final_norm_off = final_norm_off;
     e.lm_head_off = lm_head_off;
     e.scratch = scratch;
+    e.packed = packed;
+    e.packed_off = packed_off.data();
+    e.packed_lm_off = packed_lm_off;
     return e;
   }
 };
@@ -306,6 +313,8 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.mfma = 1;
     p.lm_wg = mfma_lm_partials(d);
   }
+  // the matrix-core LM head folds its partials to one per row itself
+  p.argmax_parts = p.mfma ? 1 : p.lm_wg;
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
     // "down_whole": 0 keeps the split-K down projection and its reduce launch
@@ -367,6 +376,44 @@ void layout_weights(Engine& e) {
   e.final_norm_off = add("final_norm", d.hidden, true);
   e.lm_head_off = add("lm_head", (long long)d.vocab * d.hidden, true);
   e.weight_bytes = off;
+}
+
+// The packed copy of the matrix a weight slot belongs to, refreshed after the
+// slot is written (matrix-core plan only; other slots have no copy).
+hipError_t repack_slot(Engine& e, const std::string& name) {
+  if (!e.plan.mfma) return hipSuccess;
+  const Dims& d = e.dims;
+  if (name == "lm_head")
+    return mfma_pack_matrix(e.weights + e.lm_head_off, e.packed + e.packed_lm_off, d.vocab, d.hidden, 0, e.stream);
+  if (name.rfind("layers_", 0) != 0) return hipSuccess;
+  const size_t us = name.find('_', 7);
+  if (us == std::string::npos) return hipSuccess;
+  const int l = std::atoi(name.substr(7, us - 7).c_str());
+  if (l < 0 || l >= d.layers) return hipSuccess;
+  const std::string what = name.substr(us + 1);
+  const LayerOffsets& lo = e.layer_off[l];
+  const PackedOffsets& po = e.packed_off[l];
+  if (what == "q_weight" || what == "k_weight" || what == "v_weight")
+    return mfma_pack_matrix(e.weights + lo.qkv_w, e.packed + po.qkv, d.qkv_rows(), d.hidden, d.head_dim, e.stream);
+  if (what == "o_weight")
+    return mfma_pack_matrix(e.weights + lo.o_w, e.packed + po.o, d.hidden, d.q_dim(), 0, e.stream);
+  if (what == "gate_weight")
+    return mfma_pack_matrix(e.weights + lo.gate_w, e.packed + po.gate, d.intermediate, d.hidden, 0, e.stream);
+  if (what == "up_weight")
+    return mfma_pack_matrix(e.weights + lo.up_w, e.packed + po.up, d.intermediate, d.hidden, 0, e.stream);
+  if (what == "down_weight")
+    return mfma_pack_matrix(e.weights + lo.down_w, e.packed + po.down, d.hidden, d.intermediate, 0, e.stream);
+  return hipSuccess;
+}
+
+bool repack_all(Engine& e) {
+  if (!e.plan.mfma) return true;
+  for (int l = 0; l < e.dims.layers; ++l) {
+    const std::string p = "layers_" + std::to_string(l) + "_";
+    for (const char* w : {"q_weight", "o_weight", "gate_weight", "up_weight", "down_weight"})
+      if (repack_slot(e, p + w) != hipSuccess) return false;
+  }
+  return repack_slot(e, "lm_head") == hipSuccess && hipStreamSynchronize(e.stream) == hipSuccess;
 }
 
 bool alloc_state(Engine& e) {
@@ -662,6 +709,7 @@ void free_engine(Engine* e) {
   if (e->ev_start) (void)hipEventDestroy(e->ev_start);
   if (e->ev_stop) (void)hipEventDestroy(e->ev_stop);
   if (e->weights) (void)hipFree(e->weights);
+  if (e->packed) (void)hipFree(e->packed);
   if (e->key_cache) (void)hipFree(e->key_cache);
   if (e->value_cache) (void)hipFree(e->value_cache);
   if (e->state_mem) (void)hipFree(e->state_mem);
@@ -940,6 +988,14 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     *status = kCreateDevice;
     return nullptr;
   }
+  if (e->plan.mfma) {
+    e->packed_off.resize(e->dims.layers);
+    const size_t packed_bytes = mfma_packed_layout(e->dims, e->packed_off.data(), &e->packed_lm_off);
+    if (hipMalloc(&e->packed, packed_bytes) != hipSuccess) {
+      *status = kCreateDevice;
+      return nullptr;
+    }
+  }
   const Json* w = cfg.get("weights");
   const std::string source = w ? w->string_or("source", "bundle") : "bundle";
   bool loaded = false;
@@ -951,7 +1007,7 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
   } else if (source == "upload") {
     loaded = true;
   }
-  if (!loaded) {
+  if (!loaded || !repack_all(*e)) {
     *status = kCreateWeights;
     return nullptr;
   }
@@ -1567,9 +1623,14 @@ int32_t state_access(Engine* e, const char* name, void* buf, int64_t bytes, Acce
   }
   if (static_cast<size_t>(bytes) != size) return -1;
   if (hipStreamSynchronize(e->stream) != hipSuccess) return -2;
-  const hipError_t err = mode == Access::kRead ? hipMemcpy(buf, dev, size, hipMemcpyDefault)
-                                               : hipMemcpy(dev, buf, size, hipMemcpyDefault);
-  return err == hipSuccess ? 0 : -2;
+  // On the engine's stream (which does not wait for the null stream), so the
+  // repack of a written matrix sees the new values, and complete on return
+  // (a device-to-device hipMemcpy may return before the copy has finished).
+  const hipError_t err = mode == Access::kRead ? hipMemcpyAsync(buf, dev, size, hipMemcpyDefault, e->stream)
+                                               : hipMemcpyAsync(dev, buf, size, hipMemcpyDefault, e->stream);
+  if (err != hipSuccess) return -2;
+  if (mode == Access::kWrite && repack_slot(*e, n) != hipSuccess) return -2;
+  return hipStreamSynchronize(e->stream) == hipSuccess ? 0 : -2;
 }
 }  // namespace
 

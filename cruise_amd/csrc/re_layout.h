@@ -60,6 +60,13 @@ struct LayerOffsets {
   size_t input_norm, post_norm, qkv_w, qkv_b, o_w, gate_w, up_w, down_w;
 };
 
+// Byte offsets of one layer's matrices in the packed copy the matrix-core
+// projections stream (re_mfma.hip): each matrix as 16-row strips of 32-wide k
+// steps, one 1 KB tile per (strip, step) in the order the wave's lanes read it.
+struct PackedOffsets {
+  size_t qkv, o, gate, up, down;
+};
+
 // The epoch's device state.  Feed and fetch are contiguous byte buffers in
 // the ABI order so one copy moves each; the rest persists across epochs.
 struct StatePtrs {
@@ -134,6 +141,7 @@ struct LaunchPlan {
   int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)
+  int argmax_parts;  // partial rows k_ctrl_step reduces: lm_wg, or 1 once folded
   int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
   int slot_w[4];   // their per-slot weights
   int gu_grid_eq, lm_grid_eq;  // the grids for equal ranges
@@ -176,6 +184,9 @@ struct KernelEnv {
   const LayerOffsets* layer_off;  // host array [layers]
   size_t embedding_off, final_norm_off, lm_head_off;
   Scratch scratch;
+  const uint8_t* packed;               // matrix-core copy of the matrices (plan.mfma)
+  const PackedOffsets* packed_off;     // host array [layers]
+  size_t packed_lm_off;
 };
 
 // One decoder step: embedding, L layers, final norm + LM head with argmax
@@ -194,6 +205,11 @@ enum class MfmaOp { kQkv, kO, kGateUp, kDown, kLmHead };
 bool mfma_step_supported(const Dims& d);
 int mfma_lm_partials(const Dims& d);
 hipError_t prepare_mfma();
+// Layout of the packed copy; returns its bytes.
+size_t mfma_packed_layout(const Dims& d, PackedOffsets* layers, size_t* lm_off);
+// Pack one [rows, K] matrix (qkv_head_dim > 0: the stacked qkv matrix, whose
+// strips hold RoPE pairs of heads of that size).
+hipError_t mfma_pack_matrix(const void* src, void* dst, int rows, int K, int qkv_head_dim, hipStream_t stream);
 hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, int layer, hipStream_t stream);
 // Controller kernels.
 hipError_t launch_ctrl_init(const KernelEnv& env, const StatePtrs& st, int has_payload,

@@ -50,8 +50,9 @@ enum MfKind { kMfQkv = 0, kMfGateUp = 1, kMfLm = 2, kMfResid = 3 };
 struct MfArgs {
   const int32_t* done;
   const bf16_t* x;   // [B, K]
-  const bf16_t* w0;  // [rows, K]
-  const bf16_t* w1;  // gate/up: up weights; qkv: bias [rows]
+  const bf16_t* p0;  // packed weights (gate/up: gate)
+  const bf16_t* p1;  // gate/up: packed up weights
+  const bf16_t* w1;  // qkv: bias [rows]
   int B, K;
   // qkv
   bf16_t* q;
@@ -74,15 +75,20 @@ struct MfArgs {
   int vocab;
 };
 
+// Row of column c (0..15) of qkv strip g: head g / (d / 16), pairs 8 t ..+8 of
+// that head; columns 0..7 are elements j of the pairs, columns 8..15 their
+// partners j + d/2.
+__device__ __forceinline__ int qkv_strip_row(int head_dim, int g, int c) {
+  const int half = head_dim >> 1, per_head = half >> 3;
+  const int head = g / per_head, t = g - head * per_head;
+  return head * head_dim + 8 * t + (c & 7) + (c >= 8 ? half : 0);
+}
+
 // Weight row of column c (0..15) of strip j in workgroup g.
 template <int KIND>
 __device__ __forceinline__ int strip_row(const MfArgs& a, int g, int j, int c) {
   if constexpr (KIND == kMfQkv) {
-    // strip g: head g / (d / 16), pairs 8 t ..+8 of that head; columns 0..7
-    // are elements j of the pairs, columns 8..15 their partners j + d/2
-    const int half = a.head_dim >> 1, per_head = half >> 3;
-    const int head = g / per_head, t = g - head * per_head;
-    return head * a.head_dim + 8 * t + (c & 7) + (c >= 8 ? half : 0);
+    return qkv_strip_row(a.head_dim, g, c);
   } else if constexpr (KIND == kMfLm) {
     return g * 32 + j * 16 + c;
   } else {
@@ -101,11 +107,13 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
   if (stop != 0) return;  // uniform
 
   const int kbase = wave * STEPS * kMfK + kq;
+  // packed weights: tile (strip, step) at ((strip * K/32 + step) * 64 + lane) * 8
   const bf16_t* wp[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
-    const bf16_t* base = (KIND == kMfGateUp && j == 1) ? a.w1 : a.w0;
-    wp[j] = base + (size_t)strip_row<KIND>(a, g, j, c) * a.K + kbase;
+    const bf16_t* base = (KIND == kMfGateUp && j == 1) ? a.p1 : a.p0;
+    const int strip = KIND == kMfLm ? 2 * g + j : g;
+    wp[j] = base + ((size_t)strip * (a.K / kMfK) + wave * STEPS) * 512 + lane * 8;
   }
   const bf16_t* xp[kMfTiles];
 #pragma unroll
@@ -121,7 +129,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
 #pragma unroll
   for (int s = 0; s < kRing && s < STEPS; ++s)
 #pragma unroll
-    for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * kMfK));
+    for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * 512));
 #pragma unroll
   for (int s = 0; s < kXRing && s < STEPS; ++s)
 #pragma unroll
@@ -139,7 +147,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
     if (s + kRing < STEPS) {
 #pragma unroll
       for (int j = 0; j < NS; ++j)
-        wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + (s + kRing) * kMfK));
+        wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + (s + kRing) * 512));
     }
     if (s + kXRing < STEPS) {
 #pragma unroll
@@ -311,6 +319,74 @@ __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, const bf16
   }
 }
 
+// The LM head's per-workgroup argmax partials folded to one per row, written
+// over partial 0 of the row: the first index of the maximum (CTRL:99-119),
+// any non-finite flag kept.  One workgroup per row; every partial is read
+// before thread 0 overwrites the first.
+__global__ void __launch_bounds__(256) k_mf_fold(const int32_t* done, float* val, int32_t* idx, int32_t* bad,
+                                               int parts, int B) {
+  __shared__ float sv[4];
+  __shared__ int si[4], sb[4];
+  if (done != nullptr && __builtin_nontemporal_load(done) != 0) return;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  float bv = 0.f;
+  int bi = -1, bb = 0;
+  for (int w = tid; w < parts; w += 256) {
+    const float v = val[(size_t)w * B + b];
+    const int i = idx[(size_t)w * B + b];
+    bb |= bad[(size_t)w * B + b];
+    if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    bb |= __shfl_xor(bb, m, 64);
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+    sb[wave] = bb;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  for (int w = 1; w < 4; ++w) {
+    bb |= sb[w];
+    if (si[w] >= 0 && (bi < 0 || sv[w] > bv || (sv[w] == bv && si[w] < bi))) {
+      bv = sv[w];
+      bi = si[w];
+    }
+  }
+  val[b] = bv;
+  idx[b] = bi;
+  bad[b] = bb;
+}
+
+// The packed copy of one [rows, K] matrix: 16-byte unit u = (strip * K/32 +
+// step) * 64 + lane holds row strip_row(strip, lane % 16), elements
+// step * 32 + 8 (lane / 16) ..+8.
+__global__ void k_mf_pack(const bf16_t* src, bf16_t* dst, int rows, int K, int qkv_head_dim) {
+  const long long units = (long long)rows / 16 * (K / kMfK) * 64;
+  for (long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x; u < units;
+       u += (long long)gridDim.x * blockDim.x) {
+    const int lane = static_cast<int>(u & 63);
+    const long long tile = u >> 6;
+    const int steps = K / kMfK;
+    const int strip = static_cast<int>(tile / steps), step = static_cast<int>(tile - (long long)strip * steps);
+    const int c = lane & 15;
+    const int row = qkv_head_dim > 0 ? qkv_strip_row(qkv_head_dim, strip, c) : strip * 16 + c;
+    const re_u32x4 v = *reinterpret_cast<const re_u32x4*>(src + (size_t)row * K + step * kMfK + (lane >> 4) * 8);
+    *reinterpret_cast<re_u32x4*>(dst + u * 8) = v;
+  }
+}
+
 // The launches of one projection: (strips per workgroup, waves per
 // workgroup, kind, k steps per wave).
 constexpr int kQkvWaves = 8, kOWaves = 8, kGuWaves = 4, kDownWaves = 8, kLmWaves = 4;
@@ -338,6 +414,32 @@ bool mfma_step_supported(const Dims& d) {
 
 int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
 
+size_t mfma_packed_layout(const Dims& d, PackedOffsets* layers, size_t* lm_off) {
+  size_t off = 0;
+  auto add = [&](long long rows, long long k) {
+    const size_t at = off;
+    off += (size_t)rows * k * sizeof(bf16_t);
+    off = (off + 255) & ~size_t(255);
+    return at;
+  };
+  for (int l = 0; l < d.layers; ++l) {
+    layers[l].qkv = add(d.qkv_rows(), d.hidden);
+    layers[l].o = add(d.hidden, d.q_dim());
+    layers[l].gate = add(d.intermediate, d.hidden);
+    layers[l].up = add(d.intermediate, d.hidden);
+    layers[l].down = add(d.hidden, d.intermediate);
+  }
+  *lm_off = add(d.vocab, d.hidden);
+  return off;
+}
+
+hipError_t mfma_pack_matrix(const void* src, void* dst, int rows, int K, int qkv_head_dim, hipStream_t stream) {
+  if (rows % 16 != 0 || K % kMfK != 0 || (qkv_head_dim > 0 && qkv_head_dim % 16 != 0)) return hipErrorInvalidValue;
+  k_mf_pack<<<2048, 256, 0, stream>>>(static_cast<const bf16_t*>(src), static_cast<bf16_t*>(dst), rows, K,
+                                      qkv_head_dim);
+  return hipGetLastError();
+}
+
 hipError_t prepare_mfma() {
   hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves)>();
   if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves)>();
@@ -355,11 +457,12 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
   a.B = d.batch;
   a.hidden_dim = d.hidden;
   auto wt = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.weights + off); };
+  auto pk = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.packed + off); };
   if (op == MfmaOp::kLmHead) {
     k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(env.final_norm_off),
                                            static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
     a.x = static_cast<const bf16_t*>(sc.xn);
-    a.w0 = wt(env.lm_head_off);
+    a.p0 = pk(env.packed_lm_off);
     a.K = d.hidden;
     a.logits = st.logits;
     a.am_val = sc.am_val;
@@ -367,16 +470,18 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
     a.am_bad = sc.am_bad;
     a.vocab = d.vocab;
     mgemv_launch<2, kLmWaves, kMfLm, kHidSteps(kLmWaves)>(a, d.vocab / 32, stream);
+    k_mf_fold<<<d.batch, 256, 0, stream>>>(st.done, sc.am_val, sc.am_idx, sc.am_bad, d.vocab / 32, d.batch);
     return hipGetLastError();
   }
   const LayerOffsets& lo = env.layer_off[layer];
+  const PackedOffsets& po = env.packed_off[layer];
   const size_t cache_layer_elems = (size_t)d.slots() * d.kv_dim();
   switch (op) {
     case MfmaOp::kQkv:
       k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.input_norm),
                                              static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
       a.x = static_cast<const bf16_t*>(sc.xn);
-      a.w0 = wt(lo.qkv_w);
+      a.p0 = pk(po.qkv);
       a.w1 = wt(lo.qkv_b);
       a.K = d.hidden;
       a.q = static_cast<bf16_t*>(sc.q);
@@ -393,7 +498,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       break;
     case MfmaOp::kO:
       a.x = static_cast<const bf16_t*>(sc.attn);
-      a.w0 = wt(lo.o_w);
+      a.p0 = pk(po.o);
       a.K = d.q_dim();
       a.hidden = static_cast<bf16_t*>(sc.hidden);
       mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves)>(a, d.hidden / 16, stream);
@@ -402,8 +507,8 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.post_norm),
                                              static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
       a.x = static_cast<const bf16_t*>(sc.xn);
-      a.w0 = wt(lo.gate_w);
-      a.w1 = wt(lo.up_w);
+      a.p0 = pk(po.gate);
+      a.p1 = pk(po.up);
       a.K = d.hidden;
       a.out = static_cast<bf16_t*>(sc.mlp);
       a.hidden_dim = d.intermediate;
@@ -411,7 +516,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       break;
     case MfmaOp::kDown:
       a.x = static_cast<const bf16_t*>(sc.mlp);
-      a.w0 = wt(lo.down_w);
+      a.p0 = pk(po.down);
       a.K = d.intermediate;
       a.hidden = static_cast<bf16_t*>(sc.hidden);
       mgemv_launch<1, kDownWaves, kMfResid, kInterSteps>(a, d.hidden / 16, stream);
