@@ -96,28 +96,49 @@ __device__ __forceinline__ int strip_row(const MfArgs& a, int g, int j, int c) {
   }
 }
 
-template <int NS, int WAVES, int KIND, int STEPS>
+// Packed activations (XP): row m, element k at ((m/16 * K/32 + k/32) * 64 +
+// (m%16 + 16 (k%32)/8)) * 8 + k%8, so a wave's fragment of one 16-row tile and
+// one k step is 1 KB contiguous, like the packed weights.
+__device__ __forceinline__ size_t xpack_index(int m, int k, int K) {
+  return ((size_t)((m >> 4) * (K >> 5) + (k >> 5)) * 64 + (m & 15) + 16 * ((k & 31) >> 3)) * 8 + (k & 7);
+}
+
+// Waves of a workgroup split K (KSPLIT: qkv, o and down, whose few column
+// strips would not fill the chip otherwise) or N (gate/up and the LM head:
+// every wave owns its columns over the whole K, and the waves of a workgroup
+// read the same activation fragments at about the same time, which the L1
+// cache then serves once).
+template <int KIND>
+constexpr bool k_split() { return KIND == kMfQkv || KIND == kMfResid; }
+
+template <int NS, int WAVES, int KIND, int STEPS, bool XP>
 __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
   constexpr int kXRing = x_ring<WAVES>();
-  extern __shared__ __align__(16) float mf_red[];  // [WAVES - 1][NS * kMfTiles * 4][64]
+  constexpr bool KSPLIT = k_split<KIND>();
+  extern __shared__ __align__(16) float mf_red[];  // KSPLIT: [WAVES - 1][NS * kMfTiles * 4][64]
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  const int g = blockIdx.x;
   const int c = lane & 15, kq = (lane >> 4) * 8;
+  // column group of this wave: the workgroup's (KSPLIT) or the wave's own
+  const int g = KSPLIT ? blockIdx.x : blockIdx.x * WAVES + wave;
+  const int kstep0 = KSPLIT ? wave * STEPS : 0;  // first k step of this wave
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
   if (stop != 0) return;  // uniform
 
-  const int kbase = wave * STEPS * kMfK + kq;
+  const int kbase = kstep0 * kMfK + kq;
   // packed weights: tile (strip, step) at ((strip * K/32 + step) * 64 + lane) * 8
   const bf16_t* wp[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const bf16_t* base = (KIND == kMfGateUp && j == 1) ? a.p1 : a.p0;
     const int strip = KIND == kMfLm ? 2 * g + j : g;
-    wp[j] = base + ((size_t)strip * (a.K / kMfK) + wave * STEPS) * 512 + lane * 8;
+    wp[j] = base + ((size_t)strip * (a.K / kMfK) + kstep0) * 512 + lane * 8;
   }
   const bf16_t* xp[kMfTiles];
+  constexpr int kXStep = XP ? 512 : kMfK;  // elements between a fragment's consecutive k steps
 #pragma unroll
-  for (int t = 0; t < kMfTiles; ++t) xp[t] = a.x + (size_t)min(t * 16 + c, a.B - 1) * a.K + kbase;
+  for (int t = 0; t < kMfTiles; ++t)
+    xp[t] = XP ? a.x + ((size_t)t * (a.K / kMfK) + kstep0) * 512 + lane * 8
+               : a.x + (size_t)min(t * 16 + c, a.B - 1) * a.K + kbase;
 
   mf_f32x4 acc[NS][kMfTiles];
 #pragma unroll
@@ -133,7 +154,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
 #pragma unroll
   for (int s = 0; s < kXRing && s < STEPS; ++s)
 #pragma unroll
-    for (int t = 0; t < kMfTiles; ++t) xr[s][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + s * kMfK);
+    for (int t = 0; t < kMfTiles; ++t) xr[s][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + s * kXStep);
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int rw = s % kRing, rx = s % kXRing;
@@ -151,30 +172,35 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
     }
     if (s + kXRing < STEPS) {
 #pragma unroll
-      for (int t = 0; t < kMfTiles; ++t) xr[rx][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + (s + kXRing) * kMfK);
+      for (int t = 0; t < kMfTiles; ++t) xr[rx][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + (s + kXRing) * kXStep);
     }
+    // Keep each step's refill where it is: left free, the scheduler sinks the
+    // loads next to their products and every step then waits for memory.
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  // The waves' partial sums, added by wave 0 in wave order.
-  constexpr int R = NS * kMfTiles * 4;
-  if (wave > 0) {
+  if constexpr (KSPLIT) {
+    // The waves' partial sums, added by wave 0 in wave order.
+    constexpr int R = NS * kMfTiles * 4;
+    if (wave > 0) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j)
+      for (int j = 0; j < NS; ++j)
 #pragma unroll
-      for (int t = 0; t < kMfTiles; ++t)
+        for (int t = 0; t < kMfTiles; ++t)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) mf_red[((wave - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane] = acc[j][t][v];
+          for (int v = 0; v < 4; ++v) mf_red[((wave - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane] = acc[j][t][v];
+    }
+    lds_barrier();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w)
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+#pragma unroll
+        for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[j][t][v] += mf_red[((w - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane];
   }
-  lds_barrier();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 1; w < WAVES; ++w)
-#pragma unroll
-    for (int j = 0; j < NS; ++j)
-#pragma unroll
-      for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[j][t][v] += mf_red[((w - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane];
 
   const int mrow = 4 * (lane >> 4);  // + 16 t + v
   if constexpr (KIND == kMfQkv) {
@@ -226,7 +252,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
         const float gt = Elt<bf16_t>::r(acc[0][t][v]);
         const float up = Elt<bf16_t>::r(acc[1][t][v]);
         const float sg = Elt<bf16_t>::r(gt / (1.0f + expf(-gt)));
-        a.out[(size_t)m * a.hidden_dim + n] = Elt<bf16_t>::t(Elt<bf16_t>::r(sg * up));
+        a.out[xpack_index(m, n, a.hidden_dim)] = Elt<bf16_t>::t(Elt<bf16_t>::r(sg * up));
       }
   } else if constexpr (KIND == kMfResid) {
     const int n = strip_row<KIND>(a, g, 0, c);
@@ -280,13 +306,15 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
   }
 }
 
-template <int NS, int WAVES>
+template <int NS, int WAVES, int KIND>
 constexpr size_t mgemv_lds() {
-  return (size_t)(WAVES - 1) * NS * kMfTiles * 4 * 64 * sizeof(float);
+  return k_split<KIND>() ? (size_t)(WAVES - 1) * NS * kMfTiles * 4 * 64 * sizeof(float) : 0;
 }
 
-// RMSNorm of each row into a normalized copy: T(T(h * rs) * w) with rs =
-// rsqrt(mean(h^2) + eps) in fp32 (batched_decoder_step.py:224-229).
+// RMSNorm of each row into a normalized copy, packed like the activations the
+// projections read: T(T(h * rs) * w) with rs = rsqrt(mean(h^2) + eps) in fp32
+// (batched_decoder_step.py:224-229).  Eight consecutive elements stay
+// contiguous in the packed layout.
 __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, const bf16_t* h, const bf16_t* w, bf16_t* y,
                                                int H, float eps) {
   __shared__ float red[4];
@@ -315,7 +343,7 @@ __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, const bf16
     float out[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[e] = round_bf16(round_bf16(hv[i].get(e) * rs) * wv.get(e));
-    *reinterpret_cast<Vec8<bf16_t>*>(y + (size_t)m * H + ch * 8) = Vec8<bf16_t>::from_floats(out);
+    *reinterpret_cast<Vec8<bf16_t>*>(y + xpack_index(m, ch * 8, H)) = Vec8<bf16_t>::from_floats(out);
   }
 }
 
@@ -391,25 +419,26 @@ __global__ void k_mf_pack(const bf16_t* src, bf16_t* dst, int rows, int K, int q
 // workgroup, kind, k steps per wave).
 constexpr int kQkvWaves = 8, kOWaves = 8, kGuWaves = 4, kDownWaves = 8, kLmWaves = 4;
 constexpr int kHidSteps(int waves) { return kMfHidden / kMfK / waves; }
+constexpr int kHidAll = kMfHidden / kMfK;  // the whole K of the N-split projections
 constexpr int kInterSteps = kMfInter / kMfK / kDownWaves;
 
-template <int NS, int WAVES, int KIND, int STEPS>
+template <int NS, int WAVES, int KIND, int STEPS, bool XP>
 hipError_t mgemv_prepare() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_mgemv<NS, WAVES, KIND, STEPS>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mgemv_lds<NS, WAVES>()));
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_mgemv<NS, WAVES, KIND, STEPS, XP>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mgemv_lds<NS, WAVES, KIND>()));
 }
 
-template <int NS, int WAVES, int KIND, int STEPS>
+template <int NS, int WAVES, int KIND, int STEPS, bool XP>
 void mgemv_launch(const MfArgs& a, int grid, hipStream_t stream) {
-  k_mgemv<NS, WAVES, KIND, STEPS><<<grid, WAVES * 64, mgemv_lds<NS, WAVES>(), stream>>>(a);
+  k_mgemv<NS, WAVES, KIND, STEPS, XP><<<grid, WAVES * 64, mgemv_lds<NS, WAVES, KIND>(), stream>>>(a);
 }
 
 }  // namespace
 
 bool mfma_step_supported(const Dims& d) {
   return d.dtype_bytes == 2 && d.batch == kMfRows && d.hidden == kMfHidden && d.q_dim() == kMfHidden &&
-         d.intermediate == kMfInter && d.head_dim % 16 == 0 && d.qkv_rows() % 16 == 0 && d.vocab % 32 == 0 &&
-         d.hidden % 16 == 0;
+         d.intermediate == kMfInter && d.head_dim % 16 == 0 && d.qkv_rows() % 16 == 0 &&
+         d.vocab % (32 * kLmWaves) == 0 && d.hidden % 16 == 0;
 }
 
 int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
@@ -441,11 +470,11 @@ hipError_t mfma_pack_matrix(const void* src, void* dst, int rows, int K, int qkv
 }
 
 hipError_t prepare_mfma() {
-  hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves)>();
-  if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves)>();
-  if (e == hipSuccess) e = mgemv_prepare<2, kGuWaves, kMfGateUp, kHidSteps(kGuWaves)>();
-  if (e == hipSuccess) e = mgemv_prepare<1, kDownWaves, kMfResid, kInterSteps>();
-  if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidSteps(kLmWaves)>();
+  hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves), false>();
+  if (e == hipSuccess) e = mgemv_prepare<2, kGuWaves, kMfGateUp, kHidAll, true>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kDownWaves, kMfResid, kInterSteps, true>();
+  if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidAll, true>();
   return e;
 }
 
@@ -469,7 +498,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
     a.am_idx = sc.am_idx;
     a.am_bad = sc.am_bad;
     a.vocab = d.vocab;
-    mgemv_launch<2, kLmWaves, kMfLm, kHidSteps(kLmWaves)>(a, d.vocab / 32, stream);
+    mgemv_launch<2, kLmWaves, kMfLm, kHidAll, true>(a, d.vocab / 32 / kLmWaves, stream);
     k_mf_fold<<<d.batch, 256, 0, stream>>>(st.done, sc.am_val, sc.am_idx, sc.am_bad, d.vocab / 32, d.batch);
     return hipGetLastError();
   }
@@ -494,14 +523,14 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.heads = d.heads;
       a.kv_heads = d.kv_heads;
       a.head_dim = d.head_dim;
-      mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves)>(a, d.qkv_rows() / 16, stream);
+      mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>(a, d.qkv_rows() / 16, stream);
       break;
     case MfmaOp::kO:
       a.x = static_cast<const bf16_t*>(sc.attn);
       a.p0 = pk(po.o);
       a.K = d.q_dim();
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves)>(a, d.hidden / 16, stream);
+      mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves), false>(a, d.hidden / 16, stream);
       break;
     case MfmaOp::kGateUp:
       k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.post_norm),
@@ -512,14 +541,14 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.K = d.hidden;
       a.out = static_cast<bf16_t*>(sc.mlp);
       a.hidden_dim = d.intermediate;
-      mgemv_launch<2, kGuWaves, kMfGateUp, kHidSteps(kGuWaves)>(a, d.intermediate / 16, stream);
+      mgemv_launch<2, kGuWaves, kMfGateUp, kHidAll, true>(a, d.intermediate / 16 / kGuWaves, stream);
       break;
     case MfmaOp::kDown:
       a.x = static_cast<const bf16_t*>(sc.mlp);
       a.p0 = pk(po.down);
       a.K = d.intermediate;
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      mgemv_launch<1, kDownWaves, kMfResid, kInterSteps>(a, d.hidden / 16, stream);
+      mgemv_launch<1, kDownWaves, kMfResid, kInterSteps, true>(a, d.hidden / 16, stream);
       break;
     default:
       return hipErrorInvalidValue;
