@@ -218,10 +218,15 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
   }
 }
 
-bool use_group_attention(const Dims& d) {
-  return d.dtype_bytes == 2 && d.head_dim == kGrpD && d.groups() <= kGrpMaxG && d.batch * d.kv_heads >= 64 &&
+}  // namespace
+
+bool group_attention_fits(const Dims& d) {
+  return d.dtype_bytes == 2 && d.head_dim == kGrpD && d.groups() <= kGrpMaxG &&
          group_smem_bytes(d.groups(), d.capacity, d.blocks_per_row) <= 96 * 1024;
 }
+bool group_attention_default(const Dims& d) { return group_attention_fits(d) && d.batch * d.kv_heads >= 64; }
+
+namespace {
 
 size_t smem_bytes(int window, int blocks_per_row) {
   return (size_t)window * sizeof(float) + (size_t)kAttnThreads * 8 * sizeof(float) + (size_t)blocks_per_row * sizeof(int);
@@ -255,7 +260,7 @@ size_t attention_lds_bytes(const Dims& d) { return smem_bytes(d.capacity, d.bloc
 
 hipError_t prepare_attention(const Dims& d) {
   if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256) return hipErrorInvalidValue;
-  if (use_group_attention(d)) {
+  if (group_attention_fits(d)) {
     const int bytes = static_cast<int>(group_smem_bytes(d.groups(), d.capacity, d.blocks_per_row));
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_group<true>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -276,7 +281,7 @@ hipError_t prepare_attention(const Dims& d) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream) {
-  if (use_group_attention(d)) {
+  if (a.grouped && group_attention_fits(d)) {
     const size_t smem = group_smem_bytes(d.groups(), a.window, a.blocks_per_row);
     if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size)
       k_attn_group<true><<<a.B * a.kv_heads, kGrpThreads, smem, stream>>>(a);

@@ -315,6 +315,11 @@ bool make_plan(Engine& e, const Json& cfg) {
   }
   // the matrix-core LM head folds its partials to one per row itself
   p.argmax_parts = p.mfma ? 1 : p.lm_wg;
+  // grouped decode attention: by default for many rows; "tuning":
+  // {"grouped_attention": 0 or 1} forces it where the shape allows it
+  p.grouped_attn = group_attention_default(d) ? 1 : 0;
+  if (tune != nullptr && group_attention_fits(d))
+    p.grouped_attn = static_cast<int>(tune->number_or("grouped_attention", p.grouped_attn)) != 0 ? 1 : 0;
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
     // "down_whole": 0 keeps the split-K down projection and its reduce launch

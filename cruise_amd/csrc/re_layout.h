@@ -150,6 +150,8 @@ struct LaunchPlan {
   int down_whole_grid;
   // 1: the projections run on the matrix cores (re_mfma.hip, 64 rows)
   int mfma;
+  // 1: decode attention per (row, KV head) for all query heads of the group
+  int grouped_attn;
 };
 
 // Arguments of the paged decode attention (re_attn.hip).
@@ -164,8 +166,13 @@ struct AttnArgs {
   int B, heads, kv_heads, head_dim, block_size, blocks_per_row, window;
   long long slots;
   int bs_shift;            // log2(block_size) when it is a power of two, else -1
+  int grouped;             // 1: one workgroup per (row, KV head) (re_attn.hip k_attn_group)
 };
 size_t attention_lds_bytes(const Dims& d);
+// The grouped attention's default: many rows (B x KV heads >= 64); whether the
+// shape allows it at all.
+bool group_attention_default(const Dims& d);
+bool group_attention_fits(const Dims& d);
 hipError_t prepare_attention(const Dims& d);
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream);
 

@@ -687,6 +687,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     at.window = d.capacity;
     at.slots = d.slots();
     at.bs_shift = (d.block_size & (d.block_size - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(d.block_size)) : -1;
+    at.grouped = p.grouped_attn;
     if (want()) {
       const hipError_t err = launch_attention(at, d, stream);
       if (err != hipSuccess) return err;
