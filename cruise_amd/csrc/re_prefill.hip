@@ -5,10 +5,11 @@
 //   embed      token rows + per-token RoPE table
 //   rmsnorm    one workgroup per token
 //   GEMM       C[M,N] = A[M,K] W[N,K]^T, both operands K-contiguous.
-//              bf16: MFMA v_mfma_f32_32x32x16_bf16, 128x128 workgroup tiles
-//              (four waves of 64x64), K in steps of 32 through double-buffered
-//              LDS, fp32 accumulation; epilogues "T(acc + bias)" and the
-//              residual "T(h + T(acc))".  fp32 models: an LDS-tiled FMA GEMM.
+//              bf16: MFMA v_mfma_f32_32x32x16_bf16, 256x256 workgroup tiles
+//              (eight waves of 128x64), K in steps of 64 through two LDS
+//              stages filled by direct global -> LDS loads, fp32
+//              accumulation; epilogues "T(acc + bias)" and the residual
+//              "T(h + T(acc))".  fp32 models: an LDS-tiled FMA GEMM.
 //   qkv post   RoPE of q and k in place, K/V rows to their paged slots
 //   attention  causal within each row's prompt.  bf16, head_dim 128: MFMA
 //              for Q K^T and P V per (64-query tile, head), the bf16 scores of
@@ -137,124 +138,195 @@ __global__ void __launch_bounds__(256) k_pf_qkv_post(PrefillQkv a) {
 // ---------------------------------------------------------------------------
 // GEMMs
 // ---------------------------------------------------------------------------
-// Workgroup tile 128 x 256, K-steps of 32; wave (wm, wn) of the 2 x 2 waves
-// owns a 64 x 128 block: 2 x 4 MFMA tiles of 32 x 32, so each fragment read
-// from LDS feeds 2 (B) or 4 (A) products.
-constexpr int kGbm = 128, kGbn = 256, kGbk = 32;
-constexpr int kGld = kGbk + 8;                  // LDS row stride in elements (80 bytes)
-constexpr int kGtm = 2, kGtn = 4;               // MFMA tiles per wave
-constexpr int kGva = kGbm * kGbk / 8 / 256;     // 16-byte vectors per thread, A tile
-constexpr int kGvb = kGbn * kGbk / 8 / 256;     // 16-byte vectors per thread, W tile
+// bf16: one 256 x 256 output tile per workgroup of 8 waves, K in steps of 64.
+//
+// Operands reach LDS by direct global -> LDS loads (global_load_lds_dwordx4,
+// 16 bytes per lane, no register staging) into two stages of 64 KB: W tile
+// rows 0..255, then A tile rows 256..511, 128 bytes (one K step) per row.
+// Chunk c (16 bytes) of row r sits in slot c ^ gemm_swz(r), so the fragment
+// reads below hit distinct banks for 8 and for 16 consecutive rows.  The
+// products run as C^T = W A^T on v_mfma_f32_32x32x16_bf16: wave (wn, wm) owns
+// n 128 x m 64 (4 x 2 tiles of 32 x 32), and a lane's accumulator holds four
+// consecutive output columns of one row.  While the waves multiply stage kt,
+// stage kt + 1 is in flight; each wave waits only for its own loads, then
+// the barrier publishes the stage.  The epilogue rounds the tile to bf16 in
+// LDS (rows padded to 264 elements) and writes it as row-contiguous 16-byte
+// vectors: "T(acc + bias)" (qkv), or the residual "T(h + T(acc))".
+//
+// Workgroups are dispatched round-robin over the 8 XCDs; workgroup b runs
+// tile t = (b % 8) * ceil(T / 8) + b / 8 of a grouped order (4 M tiles by
+// every N tile), so the 32 tiles an XCD runs at once share 4 A and 8 W row
+// blocks in its L2.
+//
+// Requirements (checked by launch_gemm): K % 64 == 0, N % 8 == 0, lda, ldw
+// and ldo multiples of 8 elements, 16-byte aligned operands.
+constexpr int kGm = 256, kGn = 256, kGk = 64;
+constexpr int kGrowBytes = kGk * 2;                   // one K step of one row
+constexpr int kGstage = (kGm + kGn) * kGrowBytes;     // 64 KB
+constexpr int kGwaves = 8, kGthreads = kGwaves * 64;
+constexpr int kGdmaRows = (kGm + kGn) / kGwaves;      // rows each wave loads per stage
+constexpr int kGdmaInsts = kGdmaRows / 8;             // 8 rows (1 KB) per instruction
+constexpr int kGoutLd = kGn + 8;                      // epilogue row stride (elements)
+constexpr int kGsmem = kGm * kGoutLd * 2 > 2 * kGstage ? kGm * kGoutLd * 2 : 2 * kGstage;
+constexpr int kGgroupM = 4;
 
-template <int EPI>
-__device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int n, float y) {
-  bf16_t* out = static_cast<bf16_t*>(a.out) + (size_t)m * a.ldo + n;
-  if constexpr (EPI == kGemmStore) {
-    if (a.bias != nullptr) y += bf16_to_f(static_cast<const bf16_t*>(a.bias)[n]);
-    *out = f_to_bf16(y);
-  } else {
-    *out = f_to_bf16(bf16_to_f(*out) + round_bf16(y));
-  }
+typedef const __attribute__((address_space(1))) void* gemm_gptr;
+typedef __attribute__((address_space(3))) void* gemm_lptr;
+
+__device__ __forceinline__ int gemm_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// s_waitcnt immediate: vmcnt <= vm (6 bits), lgkmcnt 0, expcnt untouched.
+constexpr int gemm_wait_vm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
+// End of a stage: this wave's loads and LDS reads are done, then the barrier.
+// The empty asm statements keep the compiler from moving memory accesses
+// across; the wait is a real instruction the wait-count pass accounts for.
+__device__ __forceinline__ void gemm_stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(gemm_wait_vm(0));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
 }
 
-// Software pipeline: while the waves multiply K-tile kt out of LDS, tile
-// kt + 1 is in flight into registers, then goes to the other LDS buffer.
-// The barrier orders LDS only (the next prefetch may already be in flight);
-// the loads are unconditional (the last tile's addresses are clamped), so
-// each wait counts exactly.
+__device__ __forceinline__ void gemm_tile_of(int b, int nM, int nN, int& mt, int& nt) {
+  const int total = nM * nN, x = b & 7, local = b >> 3, q = total >> 3, r = total & 7;
+  const int t = x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
+  const int per_group = kGgroupM * nN, g = t / per_group, first = g * kGgroupM;
+  const int gm = min(kGgroupM, nM - first), w = t - g * per_group;
+  mt = first + w % gm;
+  nt = w / gm;
+}
+
 template <int EPI>
-__global__ void __launch_bounds__(256, 2) k_gemm_bf16(GemmArgs a) {
-  __shared__ __align__(16) bf16_t As[2][kGbm * kGld];
-  __shared__ __align__(16) bf16_t Bs[2][kGbn * kGld];
+__global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, int nN) {
+  extern __shared__ __align__(16) unsigned char gsm[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kGbm, n0 = blockIdx.x * kGbn;
-  const bf16_t* A = static_cast<const bf16_t*>(a.A);
-  const bf16_t* W = static_cast<const bf16_t*>(a.W);
-  const int nk = (a.K + kGbk - 1) / kGbk;
-  const re_u32x4 zero = {0u, 0u, 0u, 0u};
-  struct Stage {
-    re_u32x4 a[kGva], b[kGvb];
+  int mt, nt;
+  gemm_tile_of(blockIdx.x, nM, nN, mt, nt);
+  const int m0 = mt * kGm, n0 = nt * kGn;
+  // Loads: waves 0-3 bring W rows 0..255, waves 4-7 A rows 0..255.  Rows past
+  // M or N read a valid row (clamped) whose results are never stored.
+  const int row0 = wave * kGdmaRows;
+  const bool loads_w = row0 < kGn;
+  const char* gbase = loads_w ? static_cast<const char*>(a.W) + (size_t)n0 * a.ldw * 2
+                              : static_cast<const char*>(a.A) + (size_t)m0 * a.lda * 2;
+  const long long ld = loads_w ? a.ldw : a.lda;
+  const int rows_left = loads_w ? a.N - n0 : a.M - m0;
+  uint32_t goff[kGdmaInsts];
+#pragma unroll
+  for (int i = 0; i < kGdmaInsts; ++i) {
+    // lane l of instruction i writes slot l % 8 of row row0 + 8 i + l / 8
+    const int row = row0 + i * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ gemm_swz(row);
+    goff[i] = static_cast<uint32_t>(min(row & 255, rows_left - 1) * ld * 2 + chunk * 16);
+  }
+  const int nk = a.K / kGk;
+  auto issue = [&](int kt) {  // the last stage is re-read past the end (clamped, never used)
+    const char* g = gbase + (size_t)min(kt, nk - 1) * kGrowBytes;
+    unsigned char* l = gsm + (kt & 1) * kGstage + row0 * kGrowBytes;
+#pragma unroll
+    for (int i = 0; i < kGdmaInsts; ++i)
+      __builtin_amdgcn_global_load_lds((gemm_gptr)(g + goff[i]), (gemm_lptr)(l + i * 1024), 16, 0, 0);
   };
-  Stage st;
-  // 16-byte vector v of a tile with 32 columns: row v / 4, columns
-  // (v % 4) * 8 ..+8.  Rows past M or N read a valid row (clamped) whose
-  // results are never stored; columns past K read as zeros.
-  auto gload = [&](Stage& s, int kt) {
-    const int k0 = min(kt, nk - 1) * kGbk;
+  const int wn = wave & 1, wm = wave >> 1;
+  f32x16_t acc[4][2];
 #pragma unroll
-    for (int i = 0; i < kGva; ++i) {
-      const int v = tid + 256 * i, row = v >> 2, k = k0 + (v & 3) * 8;
-      const bool kin = k < a.K;
-      const re_u32x4 x = *reinterpret_cast<const re_u32x4*>(A + (size_t)min(m0 + row, a.M - 1) * a.lda + (kin ? k : 0));
-      s.a[i] = kin ? x : zero;
-    }
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < kGvb; ++i) {
-      const int v = tid + 256 * i, row = v >> 2, k = k0 + (v & 3) * 8;
-      const bool kin = k < a.K;
-      const re_u32x4 y = *reinterpret_cast<const re_u32x4*>(W + (size_t)min(n0 + row, a.N - 1) * a.ldw + (kin ? k : 0));
-      s.b[i] = kin ? y : zero;
-    }
-  };
-  auto sstore = [&](const Stage& s, int buf) {
-#pragma unroll
-    for (int i = 0; i < kGva; ++i) {
-      const int v = tid + 256 * i;
-      *reinterpret_cast<re_u32x4*>(&As[buf][(v >> 2) * kGld + (v & 3) * 8]) = s.a[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kGvb; ++i) {
-      const int v = tid + 256 * i;
-      *reinterpret_cast<re_u32x4*>(&Bs[buf][(v >> 2) * kGld + (v & 3) * 8]) = s.b[i];
-    }
-  };
-  f32x16_t acc[kGtm][kGtn];
-#pragma unroll
-  for (int i = 0; i < kGtm; ++i)
-#pragma unroll
-    for (int j = 0; j < kGtn; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  auto mma_tile = [&](int buf) {
-#pragma unroll
-    for (int ks = 0; ks < kGbk / 16; ++ks) {
-      // lane l supplies row l % 32 of its operand, elements (l / 32) * 8 ..+8
-      const int kof = ks * 16 + (lane >> 5) * 8;
-      bf16x8_t af[kGtm], bf[kGtn];
-#pragma unroll
-      for (int i = 0; i < kGtm; ++i) af[i] = lds_frag(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * kGld + kof]);
-#pragma unroll
-      for (int j = 0; j < kGtn; ++j) bf[j] = lds_frag(&Bs[buf][(wn * 128 + j * 32 + (lane & 31)) * kGld + kof]);
-#pragma unroll
-      for (int i = 0; i < kGtm; ++i)
-#pragma unroll
-        for (int j = 0; j < kGtn; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
+  // lane l supplies row l % 32 of a 32-row operand tile, K elements
+  // 8 (l / 32) ..+8 of the 16-wide sub-step
+  const int fr = lane & 31, fh = lane >> 5;
+  auto frag = [&](int st, int row, int ks) -> bf16x8_t {
+    const int c = (2 * ks + fh) ^ gemm_swz(row);
+    return lds_frag(reinterpret_cast<const bf16_t*>(gsm + st * kGstage + row * kGrowBytes + c * 16));
   };
-  gload(st, 0);
-  sstore(st, 0);
-  lds_barrier();
+  issue(0);
+  gemm_stage_barrier();
   for (int kt = 0; kt < nk; ++kt) {
-    gload(st, kt + 1);
+    const int st = kt & 1;
+    issue(kt + 1);
+    // fragments of sub-step ks + 1 are read while the products of ks run
+    bf16x8_t fa[2][4], fb[2][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[0][i] = frag(st, wn * 128 + i * 32 + fr, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[0][j] = frag(st, kGn + wm * 64 + j * 32 + fr, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mma_tile(kt & 1);
-    __builtin_amdgcn_sched_barrier(0);
-    sstore(st, (kt + 1) & 1);
-    lds_barrier();
-  }
-  // accumulator v of lane l: row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
 #pragma unroll
-  for (int i = 0; i < kGtm; ++i)
+    for (int ks = 0; ks < kGk / 16; ++ks) {
+      const int c = ks & 1, n = c ^ 1;
+      if (ks + 1 < kGk / 16) {
 #pragma unroll
-    for (int j = 0; j < kGtn; ++j)
+        for (int i = 0; i < 4; ++i) fa[n][i] = frag(st, wn * 128 + i * 32 + fr, ks + 1);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int n = n0 + wn * 128 + j * 32 + (lane & 31);
-        if (m < a.M && n < a.N) gemm_store<EPI>(a, m, n, acc[i][j][v]);
+        for (int j = 0; j < 2; ++j) fb[n][j] = frag(st, kGn + wm * 64 + j * 32 + fr, ks + 1);
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][i], fb[c][j], acc[i][j], 0, 0, 0);
+      if (ks + 1 < kGk / 16) {
+#pragma unroll
+        for (int r = 0; r < 6; ++r) {  // one fragment read per product
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    gemm_stage_barrier();
+  }
+  // acc[i][j] value v of lane l: n = 32 i + 8 (v / 4) + 4 (l / 32) + v % 4,
+  // m = 32 j + l % 32 within the wave's block
+  bf16_t* T = reinterpret_cast<bf16_t*>(gsm);
+  const bf16_t* bias = static_cast<const bf16_t*>(a.bias);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int ml = wm * 64 + j * 32 + fr, nl = wn * 128 + i * 32 + 8 * q + 4 * fh;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = acc[i][j][4 * q + e];
+        if (EPI == kGemmStore && bias != nullptr) {
+          const uint2 b = *reinterpret_cast<const uint2*>(bias + min(n0 + nl, a.N - 4));
+          y[0] += __uint_as_float(b.x << 16);
+          y[1] += __uint_as_float(b.x & 0xffff0000u);
+          y[2] += __uint_as_float(b.y << 16);
+          y[3] += __uint_as_float(b.y & 0xffff0000u);
+        }
+        *reinterpret_cast<uint2*>(T + ml * kGoutLd + nl) =
+            make_uint2(f_to_bf16(y[0]) | ((uint32_t)f_to_bf16(y[1]) << 16),
+                       f_to_bf16(y[2]) | ((uint32_t)f_to_bf16(y[3]) << 16));
+      }
+  gemm_stage_barrier();
+  bf16_t* out = static_cast<bf16_t*>(a.out);
+#pragma unroll 4
+  for (int idx = tid; idx < kGm * kGn / 8; idx += kGthreads) {
+    const int r = idx / (kGn / 8), c = idx % (kGn / 8);
+    const int m = m0 + r, n = n0 + c * 8;
+    if (m >= a.M || n >= a.N) continue;
+    re_u32x4 t = *reinterpret_cast<const re_u32x4*>(T + r * kGoutLd + c * 8);
+    re_u32x4* p = reinterpret_cast<re_u32x4*>(out + (size_t)m * a.ldo + n);
+    if constexpr (EPI == kGemmResidual) {
+      const re_u32x4 h = *p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(h[e] << 16) + __uint_as_float(t[e] << 16);
+        const float hi = __uint_as_float(h[e] & 0xffff0000u) + __uint_as_float(t[e] & 0xffff0000u);
+        t[e] = f_to_bf16(lo) | ((uint32_t)f_to_bf16(hi) << 16);
+      }
+    }
+    *p = t;
+  }
 }
 
 // fp32 models: 64 x 64 tiles, 4 x 4 outputs per thread, K in steps of 16.
@@ -645,14 +717,28 @@ hipError_t launch_prefill_qkv_post(const PrefillQkv& a, int dtype_bytes, hipStre
 
 hipError_t launch_gemm(const GemmArgs& a, int epi, int dtype_bytes, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (a.K <= 0 || a.K % 8 != 0 || a.lda % 8 != 0 || a.ldw % 8 != 0) return hipErrorInvalidValue;
   if (dtype_bytes == 2) {
-    const dim3 grid((a.N + kGbn - 1) / kGbn, (a.M + kGbm - 1) / kGbm);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W) |
+                           reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
+    if (a.K <= 0 || a.K % kGk != 0 || a.N % 8 != 0 || a.lda % 8 != 0 || a.ldw % 8 != 0 || a.ldo % 8 != 0 ||
+        !aligned)
+      return hipErrorInvalidValue;
+    static const hipError_t attr = [] {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_bf16<kGemmStore>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kGsmem);
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_bf16<kGemmResidual>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kGsmem);
+      return e;
+    }();
+    if (attr != hipSuccess) return attr;
+    const int nM = (a.M + kGm - 1) / kGm, nN = (a.N + kGn - 1) / kGn;
     if (epi == kGemmStore)
-      k_gemm_bf16<kGemmStore><<<grid, 256, 0, stream>>>(a);
+      k_gemm_bf16<kGemmStore><<<nM * nN, kGthreads, kGsmem, stream>>>(a, nM, nN);
     else
-      k_gemm_bf16<kGemmResidual><<<grid, 256, 0, stream>>>(a);
+      k_gemm_bf16<kGemmResidual><<<nM * nN, kGthreads, kGsmem, stream>>>(a, nM, nN);
   } else {
+    if (a.K <= 0) return hipErrorInvalidValue;
     const dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
     if (epi == kGemmStore)
       k_gemm_f32<kGemmStore><<<grid, 256, 0, stream>>>(a);

@@ -39,6 +39,7 @@ def main(argv=None) -> None:
     p.add_argument("--iters", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--seed", type=int, default=7)
+    p.add_argument("--tuning", default="{}", help='launch-plan overrides as JSON, e.g. {"prefill_blas": 0}')
     args = p.parse_args(argv)
     if args.window % 128 or not 2 <= args.len <= args.window:
         raise SystemExit("--window must be a multiple of 128 and 2 <= --len <= --window")
@@ -53,6 +54,7 @@ def main(argv=None) -> None:
         engine=EngineSpec(batch=args.rows, physical_blocks=args.rows * bpr, block_size=128, blocks_per_row=bpr,
                           logical_capacity=args.window),
         weights=WeightSpec("synthetic", args.seed, 0.02),
+        tuning=json.loads(args.tuning),
     )
     t0 = time.perf_counter()
     rt = ResidentEpochRuntime(cfg)
