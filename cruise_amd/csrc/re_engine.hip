@@ -300,6 +300,12 @@ bool make_plan(Engine& e, const Json& cfg) {
         p.lm_grid = p.lm_grid_eq;
       }
     }
+    // "qkv_waves": 4 or 9 waves per qkv workgroup (one row pair per wave)
+    const int qw = static_cast<int>(t->number_or("qkv_waves", p.qkv_waves));
+    if ((qw == 4 || qw == 9) && qw != p.qkv_waves) {
+      p.qkv_waves = qw;
+      p.qkv_grid = (d.qkv_rows() / 2 + qw - 1) / qw;
+    }
     p.qkv_grid = std::max(1, static_cast<int>(t->number_or("qkv_grid", p.qkv_grid)));
     p.gu_grid = std::max(1, static_cast<int>(t->number_or("gu_grid", p.gu_grid)));
     p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));
@@ -1681,6 +1687,8 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"gemv_rows_per_pass", e->plan.mb},
       {"gateup_grid", e->plan.gu_grid},
       {"down_segments", e->plan.down_segments},
+      {"down_whole_grid", e->plan.down_whole_grid},
+      {"qkv_waves", e->plan.qkv_waves},
       {"lm_grid", e->plan.lm_grid},
       {"compute_units", e->cus},
       {"epoch_memcpy_nodes", e->last_epoch_copies[0]},

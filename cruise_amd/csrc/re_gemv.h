@@ -116,9 +116,11 @@ __device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per
 // ---------------------------------------------------------------------------
 // Norm prologue: RMSNorm of rows b0..b0+MB-1 of the residual stream into LDS
 // (batched_decoder_step.py:224-229): fp32 mean of squares, rsqrt(var + eps),
-// cast to T, then a T x T product with the weight.  Thread t owns hidden
-// chunks t and t + 256 (8 elements each) of every row, so it needs the norm
-// weight of two chunks only.  Requires blockDim.x == 256, H <= 4096.
+// cast to T, then a T x T product with the weight.  Thread t < 256 owns
+// hidden chunks t and t + 256 (8 elements each) of every row, so it needs the
+// norm weight of two chunks only; threads from 256 up (workgroups of more
+// than four waves) only take part in the barriers.  Requires
+// blockDim.x >= 256, H <= 4096.
 // ---------------------------------------------------------------------------
 constexpr int kNormChunks = 2;
 
@@ -178,6 +180,7 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int
                                             float* red, int tid) {
   const int lane = tid & 63, wave = wave_index(tid);
   const int per_row = H / 8;
+  const bool owner = tid < 256;  // wave-uniform
   float ss[MB];
 #pragma unroll
   for (int m = 0; m < MB; ++m) {
@@ -185,9 +188,9 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int
 #pragma unroll
     for (int j = 0; j < kNormChunks; ++j) {
       const int c = tid + 256 * j;
-      const bool ok = c < per_row && b0 + m < B;
+      const bool ok = owner && c < per_row && b0 + m < B;
       const Vec8<T> h = ok ? in.h[m][j] : Vec8<T>{};
-      if (c < per_row) *reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8) = h;
+      if (owner && c < per_row) *reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8) = h;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = h.get(e);
@@ -197,7 +200,7 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int
     ss[m] = s;
   }
   wave_reduce_transpose<MB>(ss, lane);
-  if ((lane & (64 / MB - 1)) == 0) red[wave * MB + lane / (64 / MB)] = ss[0];
+  if (wave < 4 && (lane & (64 / MB - 1)) == 0) red[wave * MB + lane / (64 / MB)] = ss[0];
   lds_barrier();
   float rs[MB];
 #pragma unroll
@@ -210,7 +213,7 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<T, MB>& in, int b0, int
 #pragma unroll
   for (int j = 0; j < kNormChunks; ++j) {
     const int c = tid + 256 * j;
-    if (c < per_row) {
+    if (owner && c < per_row) {
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
         Vec8<T>* p = reinterpret_cast<Vec8<T>*>(xs + m * H + c * 8);

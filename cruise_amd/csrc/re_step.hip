@@ -666,7 +666,11 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
         const hipError_t err = launch_mfma_op(MfmaOp::kQkv, env, st, l, stream);
         if (err != hipSuccess) return err;
       } else {
-        launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
+        if (p.qkv_waves == 9)
+          launch_proj<T, MB, 9, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), normed_lds_bytes(MB, d.hidden, sizeof(T), 9),
+                                      stream);
+        else
+          launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
       }
     }
 
@@ -818,6 +822,14 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
   const bool full = d.hidden == kSeg;
   p.qkv_grid = fit(full ? k_proj<T, MB, WAVES, kQkv, true> : k_proj<T, MB, WAVES, kQkv, false>,
                    (d.qkv_rows() / 2 + WAVES - 1) / WAVES);
+  p.qkv_waves = WAVES;
+  // Exactly nine RoPE row pairs per CU (Qwen2.5-7B: 2,304 pairs on 256 CUs):
+  // one 9-wave workgroup per CU, so every CU streams the same bytes (with
+  // 4-wave workgroups a quarter of the CUs run three, the rest two).
+  if (sizeof(T) == 2 && MB == 4 && d.qkv_rows() / 2 == 9 * cus) {
+    p.qkv_waves = 9;
+    p.qkv_grid = cus;
+  }
   p.slot_cus = 0;
   p.gu_grid = fit(full ? k_proj<T, MB, WAVES, kGateUp, true> : k_proj<T, MB, WAVES, kGateUp, false>,
                   (d.intermediate + WAVES - 1) / WAVES);

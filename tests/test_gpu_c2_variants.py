@@ -1,0 +1,65 @@
+"""Launch-plan variants on one Qwen2.5-7B-shape bf16 layer: each must give
+exactly the default plan's logits, greedy tokens and cache writes.
+
+- {"qkv_waves": 4}: 4-wave qkv workgroups (576 of them) instead of the
+  default one 9-wave workgroup per 9 RoPE row pairs (one per CU on a 256-CU
+  MI355X); the per-pair code is the same, so the results must be too.
+
+The engine allows one instance per process, so the runtimes run one after
+the other."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.weights import generate_weights, seeded_cache
+from oracle.workloads import C2, random_tables, slot_of
+from parity import make_runtime, oracle_controller
+
+pytestmark = pytest.mark.gpu
+
+W = C2
+B = W.geometry.batch
+BS = W.geometry.block_size
+
+
+@pytest.fixture(scope="module")
+def weights_dev():
+    return generate_weights(W.dims, W.seed, device="cuda")
+
+
+def step_once(weights, tuning, inputs):
+    tok, pos, length, slot, active, table, key, value = inputs
+    rt = make_runtime(W, weights, tuning=tuning)
+    try:
+        facts = {k: rt.info(k) for k in ("qkv_waves", "qkv_grid", "compute_units")}
+        gk, gv = key.clone().cuda(), value.clone().cuda()
+        logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
+        nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
+        rt.decoder_step(tok, pos, length, gk, slot, active, table, gv, logits, nxt)
+        torch.cuda.synchronize()
+        return facts, (logits.cpu(), nxt.cpu(), gk.cpu(), gv.cpu())
+    finally:
+        rt.close()
+
+
+def test_qkv_workgroup_shapes_match_bit_for_bit(weights_dev):
+    rng = np.random.default_rng(77)
+    table = random_tables(rng, B, W.geometry.blocks_per_row, W.geometry.physical_blocks)
+    pos = rng.integers(2, 6, size=B).astype(np.int64)
+    length = (pos + 1).astype(np.int32).reshape(B, 1)
+    active = np.array([1, 1, 0, 1], dtype=np.int32)
+    tok = rng.integers(0, W.dims.vocab, size=(B, 1)).astype(np.int64)
+    slot = np.array([slot_of(table, r, int(pos[r]), BS) for r in range(B)], dtype=np.int32)
+    dec, _ = oracle_controller(W, {k: v.cpu() for k, v in weights_dev.items()})
+    key, value = seeded_cache(dec.cache_shape(), 5150, torch.bfloat16)
+    inputs = (tok, pos, length, slot, active, table, key, value)
+    base_facts, base = step_once(weights_dev, {}, inputs)
+    facts, got = step_once(weights_dev, {"qkv_waves": 4}, inputs)
+    pairs = (W.dims.num_heads + 2 * W.dims.num_kv_heads) * W.dims.head_dim // 2
+    if pairs == 9 * base_facts["compute_units"]:
+        assert base_facts["qkv_waves"] == 9 and base_facts["qkv_grid"] == base_facts["compute_units"]
+    assert facts["qkv_waves"] == 4 and facts["qkv_grid"] == (pairs + 3) // 4
+    for name, a, b in zip(("logits", "next", "key", "value"), base, got):
+        assert torch.equal(a, b), name
