@@ -335,6 +335,16 @@ bool make_plan(Engine& e, const Json& cfg) {
   p.down_grid = p.o_grid;
   p.o_segments = (d.q_dim() + k_segment_elems() - 1) / k_segment_elems();
   p.down_segments = (d.intermediate + k_segment_elems() - 1) / k_segment_elems();
+  // o-proj with exactly seven row pairs per CU (Qwen2.5-7B: 1,792 on 256
+  // CUs): one 7-wave workgroup per CU; "tuning": {"o_waves": 4} keeps
+  // 4-wave workgroups
+  p.o_waves = p.waves;
+  if (d.dtype_bytes == 2 && p.mb == 4 && p.o_segments == 1 && d.hidden / 2 == 7 * e.cus) p.o_waves = 7;
+  if (tune != nullptr) {
+    const int ow = static_cast<int>(tune->number_or("o_waves", p.o_waves));
+    if ((ow == 4 || (ow == 7 && d.dtype_bytes == 2 && p.mb == 4)) && ow != p.o_waves) p.o_waves = ow;
+  }
+  p.o_grid = (d.hidden / 2 + p.o_waves - 1) / p.o_waves;
   return true;
 }
 
@@ -1689,6 +1699,8 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"down_segments", e->plan.down_segments},
       {"down_whole_grid", e->plan.down_whole_grid},
       {"qkv_waves", e->plan.qkv_waves},
+      {"o_waves", e->plan.o_waves},
+      {"o_grid", e->plan.o_grid},
       {"lm_grid", e->plan.lm_grid},
       {"compute_units", e->cus},
       {"epoch_memcpy_nodes", e->last_epoch_copies[0]},

@@ -96,7 +96,8 @@ __device__ __forceinline__ void load_rows_block(Vec8<T> (&v)[seg_vecs_per_thread
 }
 
 // Store the block loaded by load_rows_block into LDS xs [MB, ldx] (rows >= B
-// as zero), then a workgroup barrier.
+// as zero), then a workgroup barrier.  Threads from 256 up (workgroups of
+// more than four waves) store nothing; they only join the barrier.
 template <typename T, int MB>
 __device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per_thread<MB>()], int b0, int B, int len,
                                                  T* xs, int ldx, int tid) {
@@ -105,7 +106,7 @@ __device__ __forceinline__ void store_rows_block(const Vec8<T> (&v)[seg_vecs_per
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = tid + 256 * i;
-    if (idx < MB * per_row) {
+    if (tid < 256 && idx < MB * per_row) {
       const int m = idx / per_row, k = (idx - m * per_row) * 8;
       *reinterpret_cast<Vec8<T>*>(xs + m * ldx + k) = b0 + m < B ? v[i] : Vec8<T>{};
     }

@@ -140,6 +140,7 @@ struct LaunchPlan {
   int waves;       // waves per GEMV workgroup
   int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
   int qkv_waves;          // waves per qkv workgroup (one RoPE row pair each): 4, or 9
+  int o_waves;            // waves per o-proj workgroup (one row pair each): 4, or 7
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)
   int argmax_parts;  // partial rows k_ctrl_step reduces: lm_wg, or 1 once folded

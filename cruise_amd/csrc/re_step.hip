@@ -712,7 +712,16 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
         const hipError_t err = launch_mfma_op(MfmaOp::kO, env, st, l, stream);
         if (err != hipSuccess) return err;
       } else {
-        k_resid<T, MB, WAVES><<<dim3(p.o_grid, p.o_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(o);
+        bool launched = false;
+        if constexpr (sizeof(T) == 2 && MB == 4) {
+          if (p.o_waves == 7) {
+            k_resid<T, MB, 7><<<dim3(p.o_grid, p.o_segments, p.row_tiles), 7 * 64, resid_lds_bytes(MB, sizeof(T), 7),
+                                stream>>>(o);
+            launched = true;
+          }
+        }
+        if (!launched)
+          k_resid<T, MB, WAVES><<<dim3(p.o_grid, p.o_segments, p.row_tiles), WAVES * 64, resid_smem, stream>>>(o);
       }
     }
     if (want() && p.o_segments > 1 && !p.mfma)

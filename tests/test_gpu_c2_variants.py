@@ -4,6 +4,8 @@ exactly the default plan's logits, greedy tokens and cache writes.
 - {"qkv_waves": 4}: 4-wave qkv workgroups (576 of them) instead of the
   default one 9-wave workgroup per 9 RoPE row pairs (one per CU on a 256-CU
   MI355X); the per-pair code is the same, so the results must be too.
+- {"o_waves": 4}: the same for the o-projection (448 4-wave workgroups
+  against one 7-wave workgroup per 7 row pairs).
 
 The engine allows one instance per process, so the runtimes run one after
 the other."""
@@ -33,7 +35,7 @@ def step_once(weights, tuning, inputs):
     tok, pos, length, slot, active, table, key, value = inputs
     rt = make_runtime(W, weights, tuning=tuning)
     try:
-        facts = {k: rt.info(k) for k in ("qkv_waves", "qkv_grid", "compute_units")}
+        facts = {k: rt.info(k) for k in ("qkv_waves", "qkv_grid", "o_waves", "o_grid", "compute_units")}
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -44,7 +46,9 @@ def step_once(weights, tuning, inputs):
         rt.close()
 
 
-def test_qkv_workgroup_shapes_match_bit_for_bit(weights_dev):
+@pytest.mark.parametrize("tuning", [{"qkv_waves": 4}, {"o_waves": 4}, {"qkv_waves": 4, "o_waves": 4}],
+                         ids=["qkv4", "o4", "both4"])
+def test_projection_workgroup_shapes_match_bit_for_bit(weights_dev, tuning):
     rng = np.random.default_rng(77)
     table = random_tables(rng, B, W.geometry.blocks_per_row, W.geometry.physical_blocks)
     pos = rng.integers(2, 6, size=B).astype(np.int64)
@@ -56,10 +60,17 @@ def test_qkv_workgroup_shapes_match_bit_for_bit(weights_dev):
     key, value = seeded_cache(dec.cache_shape(), 5150, torch.bfloat16)
     inputs = (tok, pos, length, slot, active, table, key, value)
     base_facts, base = step_once(weights_dev, {}, inputs)
-    facts, got = step_once(weights_dev, {"qkv_waves": 4}, inputs)
-    pairs = (W.dims.num_heads + 2 * W.dims.num_kv_heads) * W.dims.head_dim // 2
-    if pairs == 9 * base_facts["compute_units"]:
-        assert base_facts["qkv_waves"] == 9 and base_facts["qkv_grid"] == base_facts["compute_units"]
-    assert facts["qkv_waves"] == 4 and facts["qkv_grid"] == (pairs + 3) // 4
+    facts, got = step_once(weights_dev, tuning, inputs)
+    cus = base_facts["compute_units"]
+    qkv_pairs = (W.dims.num_heads + 2 * W.dims.num_kv_heads) * W.dims.head_dim // 2
+    o_pairs = W.dims.hidden // 2
+    if qkv_pairs == 9 * cus:
+        assert base_facts["qkv_waves"] == 9 and base_facts["qkv_grid"] == cus
+    if o_pairs == 7 * cus:
+        assert base_facts["o_waves"] == 7 and base_facts["o_grid"] == cus
+    if "qkv_waves" in tuning:
+        assert facts["qkv_waves"] == 4 and facts["qkv_grid"] == (qkv_pairs + 3) // 4
+    if "o_waves" in tuning:
+        assert facts["o_waves"] == 4 and facts["o_grid"] == (o_pairs + 3) // 4
     for name, a, b in zip(("logits", "next", "key", "value"), base, got):
         assert torch.equal(a, b), name
