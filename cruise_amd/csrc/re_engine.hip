@@ -315,12 +315,16 @@ bool make_plan(Engine& e, const Json& cfg) {
   // ("tuning": {"mfma": 0} keeps the row-tiled kernels)
   const Json* tune = cfg.get("tuning");
   p.mfma = 0;
+  p.lm_cu = 0;
   if (mfma_step_supported(d) && (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
     p.mfma = 1;
     p.lm_wg = mfma_lm_partials(d);
+    // "tuning": {"lm_cu": 0} keeps the 4-wave LM head and its fold launch
+    p.lm_cu = mfma_lm_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("lm_cu", 1) != 0) ? 1 : 0;
   }
-  // the matrix-core LM head folds its partials to one per row itself
-  p.argmax_parts = p.mfma ? 1 : p.lm_wg;
+  // the 4-wave matrix-core LM head folds its partials to one per row itself;
+  // the per-CU one leaves one per CU
+  p.argmax_parts = p.mfma ? (p.lm_cu ? e.cus : 1) : p.lm_wg;
   // grouped decode attention: by default for many rows; "tuning":
   // {"grouped_attention": 0 or 1} forces it where the shape allows it
   p.grouped_attn = group_attention_default(d) ? 1 : 0;
@@ -1700,6 +1704,8 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"down_whole_grid", e->plan.down_whole_grid},
       {"qkv_waves", e->plan.qkv_waves},
       {"o_waves", e->plan.o_waves},
+      {"lm_cu", e->plan.lm_cu},
+      {"argmax_parts", e->plan.argmax_parts},
       {"o_grid", e->plan.o_grid},
       {"lm_grid", e->plan.lm_grid},
       {"compute_units", e->cus},

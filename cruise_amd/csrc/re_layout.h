@@ -152,6 +152,9 @@ struct LaunchPlan {
   int down_whole_grid;
   // 1: the projections run on the matrix cores (re_mfma.hip, 64 rows)
   int mfma;
+  // 1 (with mfma): the LM head runs one workgroup per CU (k_mf_lm_cu) and its
+  // per-CU argmax partials go straight to k_ctrl_step
+  int lm_cu;
   // 1: decode attention per (row, KV head) for all query heads of the group
   int grouped_attn;
 };
@@ -213,6 +216,7 @@ void plan_grids(LaunchPlan& p, const Dims& d, int cus);
 enum class MfmaOp { kQkv, kO, kGateUp, kDown, kLmHead };
 bool mfma_step_supported(const Dims& d);
 int mfma_lm_partials(const Dims& d);
+bool mfma_lm_cu_fits(const Dims& d, int cus);
 hipError_t prepare_mfma();
 // Layout of the packed copy; returns its bytes.
 size_t mfma_packed_layout(const Dims& d, PackedOffsets* layers, size_t* lm_off);

@@ -306,6 +306,169 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
   }
 }
 
+// LM head with one workgroup per CU (the default for 64 rows).  k_mgemv's
+// 4-wave workgroups (4.6 per CU) each fetch the whole 64 x K activation block,
+// 0.7 GB per step on top of the 1.09 GB of weights; here the 8 waves of a CU's
+// one workgroup share one copy, staged through LDS in blocks of 16 k steps
+// (64 KB, two buffers, filled by global -> LDS loads).  Workgroup g owns
+// strips [g T / G, (g + 1) T / G) of the T = V / 16 column strips; wave w
+// owns strips w, w + 8, ... of that range (NS = 4 or 5 of them) over the whole
+// K, with kLcRing k steps of weights in flight.  Per step a wave reads the
+// four batch tiles' fragments from LDS and runs NS x 4 products.  The logits
+// are those of k_mgemv; the argmax partial of (workgroup, row) is the first
+// index of the maximum over the workgroup's columns (CTRL:99-119), combined
+// over the waves in wave order.
+constexpr int kLcWaves = 8;
+constexpr int kLcBlock = 16;   // k steps per LDS activation block
+constexpr int kLcRing = 4;     // weight steps in flight per wave
+constexpr int kLcMaxNs = 5;    // strips per wave at most
+constexpr int kLcBlockBytes = kMfTiles * kLcBlock * 1024;
+constexpr size_t kLcLds = 2 * (size_t)kLcBlockBytes + (size_t)kLcWaves * kMfRows * 12;
+
+typedef const __attribute__((address_space(1))) void* lc_gptr;
+typedef __attribute__((address_space(3))) void* lc_lptr;
+
+// s_waitcnt immediate: vmcnt <= vm, lgkmcnt 0, expcnt untouched.
+constexpr int lc_wait(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
+template <int NS>
+__device__ __forceinline__ void lm_cu_body(const MfArgs& a, unsigned char* lds, int s_begin, int lane, int wave,
+                                           float* cval, int* cidx, int* cbad) {
+  const int ksteps = a.K / kMfK, nblocks = ksteps / kLcBlock;
+  const bf16_t* wp[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) wp[j] = a.p0 + (size_t)(s_begin + wave + kLcWaves * j) * ksteps * 512 + lane * 8;
+  // activation block b, tile t, steps 8 (w & 1) ..+8 go to LDS by wave w's 8 loads
+  auto issue_x = [&](int b) {
+    const int t = wave >> 1, s0 = (wave & 1) * 8;
+    const bf16_t* src = a.x + ((size_t)t * ksteps + b * kLcBlock + s0) * 512 + lane * 8;
+    unsigned char* dst = lds + (b & 1) * kLcBlockBytes + (t * kLcBlock + s0) * 1024;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) __builtin_amdgcn_global_load_lds((lc_gptr)(src + i * 512), (lc_lptr)(dst + i * 1024), 16, 0, 0);
+  };
+  mf_f32x4 acc[NS][kMfTiles];
+#pragma unroll
+  for (int j = 0; j < NS; ++j)
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t) acc[j][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  re_u32x4 wr[kLcRing][NS];
+  issue_x(0);
+#pragma unroll
+  for (int s = 0; s < kLcRing; ++s)
+#pragma unroll
+    for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * 512));
+  issue_x(1);
+  // block 0 in LDS (the ring and block 1 may still be in flight)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(lc_wait(kLcRing * NS + 8));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  for (int b = 0; b < nblocks; ++b) {
+    const unsigned char* xb = lds + (b & 1) * kLcBlockBytes + lane * 16;
+#pragma unroll
+    for (int s = 0; s < kLcBlock; ++s) {
+      const int S = b * kLcBlock + s, rw = s % kLcRing;
+      mf_bf16x8 xf[kMfTiles];
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t) xf[t] = *reinterpret_cast<const mf_bf16x8*>(xb + (t * kLcBlock + s) * 1024);
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+#pragma unroll
+        for (int t = 0; t < kMfTiles; ++t)
+          acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[t], __builtin_bit_cast(mf_bf16x8, wr[rw][j]), acc[j][t], 0, 0, 0);
+      // the refill past the last step re-reads the last one (unconditional, so
+      // every wait counts exactly these loads)
+      const int nxt = min(S + kLcRing, ksteps - 1);
+#pragma unroll
+      for (int j = 0; j < NS; ++j) wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + nxt * 512));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Every wave is done with buffer b & 1, and block b + 1 (requested before
+    // this block's refills) has landed: only the ring may still be in flight.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(lc_wait(kLcRing * NS));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (b + 2 < nblocks) issue_x(b + 2);
+  }
+  __builtin_amdgcn_s_waitcnt(lc_wait(0));
+  // Logits T(y) as fp32 (batched_decoder_step.py:405-408) and this wave's
+  // first maximum per row over its strips.
+  const int c = lane & 15, mrow = 4 * (lane >> 4);
+#pragma unroll
+  for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = t * 16 + mrow + v;
+      float bv = 0.f;
+      int bi = -1, bad = 0;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const int n = (s_begin + wave + kLcWaves * j) * 16 + c;
+        const float l = Elt<bf16_t>::r(acc[j][t][v]);
+        if (m < a.B) a.logits[(size_t)m * a.vocab + n] = l;
+        bad |= isfinite(l) ? 0 : 1;
+        if (bi < 0 || l > bv) {  // strips in increasing order: ties keep the earlier
+          bv = l;
+          bi = n;
+        }
+      }
+#pragma unroll
+      for (int x = 1; x < 16; x <<= 1) {
+        const float ov = __shfl_xor(bv, x, 64);
+        const int oi = __shfl_xor(bi, x, 64);
+        bad |= __shfl_xor(bad, x, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (c == 0) {
+        cval[wave * kMfRows + m] = bv;
+        cidx[wave * kMfRows + m] = bi;
+        cbad[wave * kMfRows + m] = bad;
+      }
+    }
+}
+
+__global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_lm_cu(MfArgs a) {
+  extern __shared__ __align__(16) unsigned char lc_smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  if (stop != 0) return;  // uniform
+  const int G = gridDim.x, g = blockIdx.x, T = a.vocab / 16;
+  const int s_begin = (int)((long long)g * T / G), s_end = (int)((long long)(g + 1) * T / G);
+  const int ns = (s_end - s_begin - wave + kLcWaves - 1) / kLcWaves;  // strips of this wave
+  float* cval = reinterpret_cast<float*>(lc_smem + 2 * (size_t)kLcBlockBytes);
+  int* cidx = reinterpret_cast<int*>(cval + kLcWaves * kMfRows);
+  int* cbad = cidx + kLcWaves * kMfRows;
+  // every wave runs the same barriers whatever its strip count
+  switch (ns) {
+    case 5: lm_cu_body<5>(a, lc_smem, s_begin, lane, wave, cval, cidx, cbad); break;
+    case 4: lm_cu_body<4>(a, lc_smem, s_begin, lane, wave, cval, cidx, cbad); break;
+    case 3: lm_cu_body<3>(a, lc_smem, s_begin, lane, wave, cval, cidx, cbad); break;
+    case 2: lm_cu_body<2>(a, lc_smem, s_begin, lane, wave, cval, cidx, cbad); break;
+    default: lm_cu_body<1>(a, lc_smem, s_begin, lane, wave, cval, cidx, cbad); break;  // ns >= 1 (launch check)
+  }
+  __syncthreads();
+  if (tid < a.B) {
+    float bv = 0.f;
+    int bi = -1, bb = 0;
+    for (int w = 0; w < kLcWaves; ++w) {
+      const float v = cval[w * kMfRows + tid];
+      const int i = cidx[w * kMfRows + tid];
+      bb |= cbad[w * kMfRows + tid];
+      if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
+        bv = v;
+        bi = i;
+      }
+    }
+    a.am_val[(size_t)g * a.B + tid] = bv;
+    a.am_idx[(size_t)g * a.B + tid] = bi;
+    a.am_bad[(size_t)g * a.B + tid] = bb;
+  }
+}
+
 template <int NS, int WAVES, int KIND>
 constexpr size_t mgemv_lds() {
   return k_split<KIND>() ? (size_t)(WAVES - 1) * NS * kMfTiles * 4 * 64 * sizeof(float) : 0;
@@ -443,6 +606,13 @@ bool mfma_step_supported(const Dims& d) {
 
 int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
 
+// The per-CU LM head needs 8 to 40 strips per workgroup and whole LDS blocks.
+bool mfma_lm_cu_fits(const Dims& d, int cus) {
+  const int strips = d.vocab / 16;
+  return mfma_step_supported(d) && cus > 0 && strips >= kLcWaves * cus && strips <= kLcWaves * kLcMaxNs * cus &&
+         d.hidden % (kMfK * kLcBlock) == 0 && d.hidden / (kMfK * kLcBlock) >= 2 && cus <= mfma_lm_partials(d);
+}
+
 size_t mfma_packed_layout(const Dims& d, PackedOffsets* layers, size_t* lm_off) {
   size_t off = 0;
   auto add = [&](long long rows, long long k) {
@@ -475,6 +645,9 @@ hipError_t prepare_mfma() {
   if (e == hipSuccess) e = mgemv_prepare<2, kGuWaves, kMfGateUp, kHidAll, true>();
   if (e == hipSuccess) e = mgemv_prepare<1, kDownWaves, kMfResid, kInterSteps, true>();
   if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidAll, true>();
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_lm_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kLcLds));
   return e;
 }
 
@@ -498,6 +671,11 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
     a.am_idx = sc.am_idx;
     a.am_bad = sc.am_bad;
     a.vocab = d.vocab;
+    if (env.plan.lm_cu) {
+      // one workgroup per CU; its argmax partials go straight to k_ctrl_step
+      k_mf_lm_cu<<<env.plan.argmax_parts, kLcWaves * 64, kLcLds, stream>>>(a);
+      return hipGetLastError();
+    }
     mgemv_launch<2, kLmWaves, kMfLm, kHidAll, true>(a, d.vocab / 32 / kLmWaves, stream);
     k_mf_fold<<<d.batch, 256, 0, stream>>>(st.done, sc.am_val, sc.am_idx, sc.am_bad, d.vocab / 32, d.batch);
     return hipGetLastError();

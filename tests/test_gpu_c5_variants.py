@@ -1,0 +1,67 @@
+"""Launch-plan variants of the 64-row matrix-core step (one Qwen2.5-7B-shape
+layer in bf16): each must reproduce the default plan's logits, greedy tokens
+and cache writes exactly.
+
+- {"lm_cu": 0}: the LM head as 4-wave workgroups of two strips each with a
+  separate argmax fold launch, instead of the default one workgroup per CU
+  that stages the activations once in LDS and hands its per-CU argmax
+  partials to the controller.  Every logit is the same chain of MFMA steps
+  over k in the same order, so the two must agree bit for bit.
+
+The engine allows one instance per process, so the runtimes run one after
+the other."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.weights import generate_weights, seeded_cache
+from oracle.workloads import C5, random_tables, slot_of
+from parity import make_runtime, oracle_controller
+
+pytestmark = pytest.mark.gpu
+
+W = C5
+B = W.geometry.batch
+BS = W.geometry.block_size
+BPR = W.geometry.blocks_per_row
+
+
+@pytest.fixture(scope="module")
+def weights_dev():
+    return generate_weights(W.dims, W.seed, device="cuda")
+
+
+def step_once(weights, tuning, inputs):
+    tok, pos, length, slot, active, table, key, value = inputs
+    rt = make_runtime(W, weights, tuning=tuning)
+    try:
+        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units")}
+        gk, gv = key.clone().cuda(), value.clone().cuda()
+        logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
+        nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
+        rt.decoder_step(tok, pos, length, gk, slot, active, table, gv, logits, nxt)
+        torch.cuda.synchronize()
+        return facts, (logits.cpu(), nxt.cpu(), gk.cpu(), gv.cpu())
+    finally:
+        rt.close()
+
+
+def test_lm_head_per_cu_matches_four_wave_bit_for_bit(weights_dev):
+    rng = np.random.default_rng(6402)
+    table = random_tables(rng, B, BPR, W.geometry.physical_blocks)
+    pos = rng.integers(256, 1000, size=B).astype(np.int64)
+    length = (pos + 1).astype(np.int32).reshape(B, 1)
+    active = (rng.random(B) > 0.1).astype(np.int32)
+    tok = rng.integers(0, W.dims.vocab, size=(B, 1)).astype(np.int64)
+    slot = np.array([slot_of(table, r, int(pos[r]), BS) for r in range(B)], dtype=np.int32)
+    dec, _ = oracle_controller(W, {k: v.cpu() for k, v in weights_dev.items()})
+    key, value = seeded_cache(dec.cache_shape(), 670103, torch.bfloat16)
+    inputs = (tok, pos, length, slot, active, table, key, value)
+    base_facts, base = step_once(weights_dev, {}, inputs)
+    facts, got = step_once(weights_dev, {"lm_cu": 0}, inputs)
+    assert base_facts["lm_cu"] == 1 and base_facts["argmax_parts"] == base_facts["compute_units"]
+    assert facts["lm_cu"] == 0 and facts["argmax_parts"] == 1
+    for name, a, b in zip(("logits", "next", "key", "value"), base, got):
+        assert torch.equal(a, b), name
