@@ -16,7 +16,8 @@ namespace {
 struct CtrlArgs {
   StatePtrs st;
   int B, bpr, physical_blocks, block_size, capacity, vocab;
-  int lm_wg;          // argmax partial rows
+  int lm_wg;          // argmax partials per batch row
+  int am_row_major;   // partial p of row b at [b * lm_wg + p] (else [p * B + b])
   int layers, kv_dim, elem_bytes;  // cache geometry (import checksum length)
   const float* am_val;
   const int32_t* am_idx;
@@ -309,7 +310,8 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
       int ix[kUnroll], fl[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const size_t o = (size_t)min(w0 + lane + 64 * u, a.lm_wg - 1) * B + b;
+        const int p = min(w0 + lane + 64 * u, a.lm_wg - 1);
+        const size_t o = a.am_row_major ? (size_t)b * a.lm_wg + p : (size_t)p * B + b;
         v[u] = a.am_val[o];
         ix[u] = a.am_idx[o];
         fl[u] = a.am_bad[o];
@@ -576,6 +578,7 @@ static CtrlArgs ctrl_args(const KernelEnv& env, const StatePtrs& st) {
   a.capacity = env.dims.capacity;
   a.vocab = env.dims.vocab;
   a.lm_wg = env.plan.argmax_parts;
+  a.am_row_major = env.plan.argmax_row_major;
   a.layers = env.dims.layers;
   a.kv_dim = env.dims.kv_dim();
   a.elem_bytes = env.dims.dtype_bytes;

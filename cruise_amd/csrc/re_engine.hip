@@ -316,15 +316,19 @@ bool make_plan(Engine& e, const Json& cfg) {
   const Json* tune = cfg.get("tuning");
   p.mfma = 0;
   p.lm_cu = 0;
+  p.mf_split = 0;
   if (mfma_step_supported(d) && (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
     p.mfma = 1;
     p.lm_wg = mfma_lm_partials(d);
     // "tuning": {"lm_cu": 0} keeps the 4-wave LM head and its fold launch
     p.lm_cu = mfma_lm_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("lm_cu", 1) != 0) ? 1 : 0;
+    // "tuning": {"mf_split": 0} keeps o and down as one workgroup per strip
+    p.mf_split = mfma_split_fits(d) && (tune == nullptr || tune->number_or("mf_split", 1) != 0) ? 1 : 0;
   }
   // the 4-wave matrix-core LM head folds its partials to one per row itself;
   // the per-CU one leaves one per CU
   p.argmax_parts = p.mfma ? (p.lm_cu ? e.cus : 1) : p.lm_wg;
+  p.argmax_row_major = p.mfma && p.lm_cu ? 1 : 0;
   // grouped decode attention: by default for many rows; "tuning":
   // {"grouped_attention": 0 or 1} forces it where the shape allows it
   p.grouped_attn = group_attention_default(d) ? 1 : 0;
@@ -505,6 +509,7 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.inv_freq), (size_t)d.head_dim / 2 * sizeof(float)},
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {&e.scratch.xn, p.mfma ? (size_t)B * d.hidden * T : 0},
+      {reinterpret_cast<void**>(&e.scratch.mf_part), p.mf_split ? mfma_split_partial_bytes(d) : 0},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},
   };
@@ -1705,6 +1710,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"qkv_waves", e->plan.qkv_waves},
       {"o_waves", e->plan.o_waves},
       {"lm_cu", e->plan.lm_cu},
+      {"mf_split", e->plan.mf_split},
       {"argmax_parts", e->plan.argmax_parts},
       {"o_grid", e->plan.o_grid},
       {"lm_grid", e->plan.lm_grid},

@@ -132,6 +132,7 @@ struct Scratch {
   float* inv_freq;    // fp32 [d/2]
   float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
   void* xn;           // T [B, H] normalized rows (matrix-core projections)
+  float* mf_part;     // matrix-core o / down partial sums [8][B][H] (split plan)
 };
 
 struct LaunchPlan {
@@ -143,7 +144,8 @@ struct LaunchPlan {
   int o_waves;            // waves per o-proj workgroup (one row pair each): 4, or 7
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)
-  int argmax_parts;  // partial rows k_ctrl_step reduces: lm_wg, or 1 once folded
+  int argmax_parts;  // partials per row k_ctrl_step reduces: lm_wg, 1 once folded, or one per CU
+  int argmax_row_major;  // 1: the partials of a row are contiguous (per-CU LM head)
   int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
   int slot_w[4];   // their per-slot weights
   int gu_grid_eq, lm_grid_eq;  // the grids for equal ranges
@@ -155,6 +157,9 @@ struct LaunchPlan {
   // 1 (with mfma): the LM head runs one workgroup per CU (k_mf_lm_cu) and its
   // per-CU argmax partials go straight to k_ctrl_step
   int lm_cu;
+  // 1 (with mfma): o and down run split over (7-strip group, K range), their
+  // partials added by the next RMSNorm launch (re_mfma.hip kMfPart)
+  int mf_split;
   // 1: decode attention per (row, KV head) for all query heads of the group
   int grouped_attn;
 };
@@ -217,6 +222,8 @@ enum class MfmaOp { kQkv, kO, kGateUp, kDown, kLmHead };
 bool mfma_step_supported(const Dims& d);
 int mfma_lm_partials(const Dims& d);
 bool mfma_lm_cu_fits(const Dims& d, int cus);
+bool mfma_split_fits(const Dims& d);
+size_t mfma_split_partial_bytes(const Dims& d);
 hipError_t prepare_mfma();
 // Layout of the packed copy; returns its bytes.
 size_t mfma_packed_layout(const Dims& d, PackedOffsets* layers, size_t* lm_off);

@@ -45,7 +45,7 @@ constexpr int x_ring() { return WAVES >= 16 ? 2 : 4; }
 constexpr int kMfHidden = 3584;
 constexpr int kMfInter = 18944;
 
-enum MfKind { kMfQkv = 0, kMfGateUp = 1, kMfLm = 2, kMfResid = 3 };
+enum MfKind { kMfQkv = 0, kMfGateUp = 1, kMfLm = 2, kMfResid = 3, kMfPart = 4 };
 
 struct MfArgs {
   const int32_t* done;
@@ -67,6 +67,8 @@ struct MfArgs {
   bf16_t* out;
   bf16_t* hidden;
   int hidden_dim;
+  // partial sums (kMfPart): [gridDim.y][B][N] fp32, N = hidden_dim
+  float* part;
   // LM head
   float* logits;
   float* am_val;
@@ -111,6 +113,14 @@ __device__ __forceinline__ size_t xpack_index(int m, int k, int K) {
 template <int KIND>
 constexpr bool k_split() { return KIND == kMfQkv || KIND == kMfResid; }
 
+// kMfPart: the o and down projections split over (strip group, K range):
+// workgroup (x, y) runs strips x * WAVES + wave over the y-th K range of
+// STEPS steps, one strip per wave, and stores its fp32 partial sums.  The
+// K ranges are the ones k_mgemv<..., kMfResid> gives its 8 waves, and the
+// next RMSNorm launch adds the 8 partials in range order (the order wave 0
+// adds the waves' sums there) and the residual: the same results, while a
+// CU fetches one K range of the activations instead of all of them.
+
 template <int NS, int WAVES, int KIND, int STEPS, bool XP>
 __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
   constexpr int kXRing = x_ring<WAVES>();
@@ -120,7 +130,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
   const int c = lane & 15, kq = (lane >> 4) * 8;
   // column group of this wave: the workgroup's (KSPLIT) or the wave's own
   const int g = KSPLIT ? blockIdx.x : blockIdx.x * WAVES + wave;
-  const int kstep0 = KSPLIT ? wave * STEPS : 0;  // first k step of this wave
+  const int kstep0 = KSPLIT ? wave * STEPS : (KIND == kMfPart ? (int)blockIdx.y * STEPS : 0);  // first k step
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
   if (stop != 0) return;  // uniform
 
@@ -254,6 +264,16 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
         const float sg = Elt<bf16_t>::r(gt / (1.0f + expf(-gt)));
         a.out[xpack_index(m, n, a.hidden_dim)] = Elt<bf16_t>::t(Elt<bf16_t>::r(sg * up));
       }
+  } else if constexpr (KIND == kMfPart) {
+    const int n = strip_row<KIND>(a, g, 0, c);
+    float* part = a.part + (size_t)blockIdx.y * a.B * a.hidden_dim;
+#pragma unroll
+    for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = t * 16 + mrow + v;
+        if (m < a.B) part[(size_t)m * a.hidden_dim + n] = acc[0][t][v];
+      }
   } else if constexpr (KIND == kMfResid) {
     const int n = strip_row<KIND>(a, g, 0, c);
 #pragma unroll
@@ -317,7 +337,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
 // four batch tiles' fragments from LDS and runs NS x 4 products.  The logits
 // are those of k_mgemv; the argmax partial of (workgroup, row) is the first
 // index of the maximum over the workgroup's columns (CTRL:99-119), combined
-// over the waves in wave order.
+// over the waves in wave order, stored row-major ([row][G]).
 constexpr int kLcWaves = 8;
 constexpr int kLcBlock = 16;   // k steps per LDS activation block
 constexpr int kLcRing = 4;     // weight steps in flight per wave
@@ -463,9 +483,10 @@ __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_lm_cu(MfArgs a) {
         bi = i;
       }
     }
-    a.am_val[(size_t)g * a.B + tid] = bv;
-    a.am_idx[(size_t)g * a.B + tid] = bi;
-    a.am_bad[(size_t)g * a.B + tid] = bb;
+    // row-major partials: a row's G partials are contiguous for the controller
+    a.am_val[(size_t)tid * G + g] = bv;
+    a.am_idx[(size_t)tid * G + g] = bi;
+    a.am_bad[(size_t)tid * G + g] = bb;
   }
 }
 
@@ -478,12 +499,17 @@ constexpr size_t mgemv_lds() {
 // projections read: T(T(h * rs) * w) with rs = rsqrt(mean(h^2) + eps) in fp32
 // (batched_decoder_step.py:224-229).  Eight consecutive elements stay
 // contiguous in the packed layout.
-__global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, const bf16_t* h, const bf16_t* w, bf16_t* y,
-                                               int H, float eps) {
+//
+// With parts > 0 the residual add of the preceding split projection happens
+// first: h = T(h + T(p_0 + p_1 + ... )) over its fp32 partials in range order
+// (batched_decoder_step.py:380-386, 399-403), written back to the residual
+// stream, then normalized.
+__global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, bf16_t* h, const bf16_t* w, bf16_t* y,
+                                               int H, float eps, const float* part, int parts, int B) {
   __shared__ float red[4];
   if (done != nullptr && __builtin_nontemporal_load(done) != 0) return;
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  const bf16_t* hr = h + (size_t)m * H;
+  bf16_t* hr = h + (size_t)m * H;
   constexpr int kMaxChunks = 4;  // H <= 4 * 256 * 8
   Vec8<bf16_t> hv[kMaxChunks];
   float s = 0.f;
@@ -491,6 +517,22 @@ __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, const bf16
   for (int i = 0; i < kMaxChunks; ++i) {
     const int ch = tid + 256 * i;
     hv[i] = ch * 8 < H ? Vec8<bf16_t>::load_cached(hr + ch * 8) : Vec8<bf16_t>{};
+    if (parts > 0 && ch * 8 < H) {
+      float sum[8];
+      const float* p0 = part + (size_t)m * H + ch * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum[e] = p0[e];
+      for (int r = 1; r < parts; ++r) {
+        const float* pr = p0 + (size_t)r * B * H;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum[e] += pr[e];
+      }
+      float nh[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nh[e] = bf16_to_f(f_to_bf16(hv[i].get(e) + round_bf16(sum[e])));
+      hv[i] = Vec8<bf16_t>::from_floats(nh);
+      *reinterpret_cast<Vec8<bf16_t>*>(hr + ch * 8) = hv[i];
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) s = fmaf(hv[i].get(e), hv[i].get(e), s);
   }
@@ -584,6 +626,9 @@ constexpr int kQkvWaves = 8, kOWaves = 8, kGuWaves = 4, kDownWaves = 8, kLmWaves
 constexpr int kHidSteps(int waves) { return kMfHidden / kMfK / waves; }
 constexpr int kHidAll = kMfHidden / kMfK;  // the whole K of the N-split projections
 constexpr int kInterSteps = kMfInter / kMfK / kDownWaves;
+// split o / down: 7 strips (one per wave) by the 8 K ranges of the kernels above
+constexpr int kPartWaves = 7, kPartRanges = 8;
+static_assert(kOWaves == kPartRanges && kDownWaves == kPartRanges, "split ranges follow the K-split waves");
 
 template <int NS, int WAVES, int KIND, int STEPS, bool XP>
 hipError_t mgemv_prepare() {
@@ -592,7 +637,7 @@ hipError_t mgemv_prepare() {
 }
 
 template <int NS, int WAVES, int KIND, int STEPS, bool XP>
-void mgemv_launch(const MfArgs& a, int grid, hipStream_t stream) {
+void mgemv_launch(const MfArgs& a, dim3 grid, hipStream_t stream) {
   k_mgemv<NS, WAVES, KIND, STEPS, XP><<<grid, WAVES * 64, mgemv_lds<NS, WAVES, KIND>(), stream>>>(a);
 }
 
@@ -605,6 +650,9 @@ bool mfma_step_supported(const Dims& d) {
 }
 
 int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
+
+bool mfma_split_fits(const Dims& d) { return mfma_step_supported(d) && (d.hidden / 16) % kPartWaves == 0; }
+size_t mfma_split_partial_bytes(const Dims& d) { return (size_t)kPartRanges * d.batch * d.hidden * sizeof(float); }
 
 // The per-CU LM head needs 8 to 40 strips per workgroup and whole LDS blocks.
 bool mfma_lm_cu_fits(const Dims& d, int cus) {
@@ -648,6 +696,8 @@ hipError_t prepare_mfma() {
   if (e == hipSuccess)
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_lm_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLcLds));
+  if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kHidSteps(kOWaves), false>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kInterSteps, true>();
   return e;
 }
 
@@ -661,8 +711,9 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
   auto wt = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.weights + off); };
   auto pk = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.packed + off); };
   if (op == MfmaOp::kLmHead) {
-    k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(env.final_norm_off),
-                                           static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
+    k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<bf16_t*>(sc.hidden), wt(env.final_norm_off),
+                                           static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps, sc.mf_part,
+                                           env.plan.mf_split ? kPartRanges : 0, d.batch);
     a.x = static_cast<const bf16_t*>(sc.xn);
     a.p0 = pk(env.packed_lm_off);
     a.K = d.hidden;
@@ -685,8 +736,10 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
   const size_t cache_layer_elems = (size_t)d.slots() * d.kv_dim();
   switch (op) {
     case MfmaOp::kQkv:
-      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.input_norm),
-                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
+      // layer > 0: the previous layer's down projection is still in partials
+      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<bf16_t*>(sc.hidden), wt(lo.input_norm),
+                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps, sc.mf_part,
+                                             env.plan.mf_split && layer > 0 ? kPartRanges : 0, d.batch);
       a.x = static_cast<const bf16_t*>(sc.xn);
       a.p0 = pk(po.qkv);
       a.w1 = wt(lo.qkv_b);
@@ -708,11 +761,18 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.p0 = pk(po.o);
       a.K = d.q_dim();
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves), false>(a, d.hidden / 16, stream);
+      if (env.plan.mf_split) {
+        a.part = sc.mf_part;
+        mgemv_launch<1, kPartWaves, kMfPart, kHidSteps(kOWaves), false>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges),
+                                                                         stream);
+      } else {
+        mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves), false>(a, d.hidden / 16, stream);
+      }
       break;
     case MfmaOp::kGateUp:
-      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<const bf16_t*>(sc.hidden), wt(lo.post_norm),
-                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps);
+      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<bf16_t*>(sc.hidden), wt(lo.post_norm),
+                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps, sc.mf_part,
+                                             env.plan.mf_split ? kPartRanges : 0, d.batch);
       a.x = static_cast<const bf16_t*>(sc.xn);
       a.p0 = pk(po.gate);
       a.p1 = pk(po.up);
@@ -726,7 +786,12 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.p0 = pk(po.down);
       a.K = d.intermediate;
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      mgemv_launch<1, kDownWaves, kMfResid, kInterSteps, true>(a, d.hidden / 16, stream);
+      if (env.plan.mf_split) {
+        a.part = sc.mf_part;
+        mgemv_launch<1, kPartWaves, kMfPart, kInterSteps, true>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges), stream);
+      } else {
+        mgemv_launch<1, kDownWaves, kMfResid, kInterSteps, true>(a, d.hidden / 16, stream);
+      }
       break;
     default:
       return hipErrorInvalidValue;

@@ -7,6 +7,10 @@ and cache writes exactly.
   that stages the activations once in LDS and hands its per-CU argmax
   partials to the controller.  Every logit is the same chain of MFMA steps
   over k in the same order, so the two must agree bit for bit.
+- {"mf_split": 0}: o and down as one workgroup per 16-column strip whose 8
+  waves split K and add their sums in wave order, instead of the default
+  split over (strip group, K range) with the 8 range partials added, in
+  range order, by the next RMSNorm launch: the same sums in the same order.
 
 The engine allows one instance per process, so the runtimes run one after
 the other."""
@@ -37,7 +41,7 @@ def step_once(weights, tuning, inputs):
     tok, pos, length, slot, active, table, key, value = inputs
     rt = make_runtime(W, weights, tuning=tuning)
     try:
-        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units")}
+        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units", "mf_split")}
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -48,7 +52,8 @@ def step_once(weights, tuning, inputs):
         rt.close()
 
 
-def test_lm_head_per_cu_matches_four_wave_bit_for_bit(weights_dev):
+@pytest.mark.parametrize("tuning", [{"lm_cu": 0}, {"mf_split": 0}], ids=["lm_cu0", "mf_split0"])
+def test_matrix_core_plan_variants_match_bit_for_bit(weights_dev, tuning):
     rng = np.random.default_rng(6402)
     table = random_tables(rng, B, BPR, W.geometry.physical_blocks)
     pos = rng.integers(256, 1000, size=B).astype(np.int64)
@@ -60,8 +65,12 @@ def test_lm_head_per_cu_matches_four_wave_bit_for_bit(weights_dev):
     key, value = seeded_cache(dec.cache_shape(), 670103, torch.bfloat16)
     inputs = (tok, pos, length, slot, active, table, key, value)
     base_facts, base = step_once(weights_dev, {}, inputs)
-    facts, got = step_once(weights_dev, {"lm_cu": 0}, inputs)
+    facts, got = step_once(weights_dev, tuning, inputs)
     assert base_facts["lm_cu"] == 1 and base_facts["argmax_parts"] == base_facts["compute_units"]
-    assert facts["lm_cu"] == 0 and facts["argmax_parts"] == 1
+    assert base_facts["mf_split"] == 1
+    if "lm_cu" in tuning:
+        assert facts["lm_cu"] == 0 and facts["argmax_parts"] == 1
+    else:
+        assert facts["mf_split"] == 0
     for name, a, b in zip(("logits", "next", "key", "value"), base, got):
         assert torch.equal(a, b), name
