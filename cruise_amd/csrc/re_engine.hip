@@ -317,6 +317,7 @@ bool make_plan(Engine& e, const Json& cfg) {
   p.mfma = 0;
   p.lm_cu = 0;
   p.mf_split = 0;
+  p.gu_cu = 0;
   if (mfma_step_supported(d) && (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
     p.mfma = 1;
     p.lm_wg = mfma_lm_partials(d);
@@ -324,6 +325,8 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.lm_cu = mfma_lm_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("lm_cu", 1) != 0) ? 1 : 0;
     // "tuning": {"mf_split": 0} keeps o and down as one workgroup per strip
     p.mf_split = mfma_split_fits(d) && (tune == nullptr || tune->number_or("mf_split", 1) != 0) ? 1 : 0;
+    // "tuning": {"gu_cu": 0} keeps gate/up as 4-wave workgroups
+    p.gu_cu = mfma_gu_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("gu_cu", 1) != 0) ? e.cus : 0;
   }
   // the 4-wave matrix-core LM head folds its partials to one per row itself;
   // the per-CU one leaves one per CU
@@ -1711,6 +1714,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"o_waves", e->plan.o_waves},
       {"lm_cu", e->plan.lm_cu},
       {"mf_split", e->plan.mf_split},
+      {"gu_cu", e->plan.gu_cu},
       {"argmax_parts", e->plan.argmax_parts},
       {"o_grid", e->plan.o_grid},
       {"lm_grid", e->plan.lm_grid},

@@ -160,6 +160,8 @@ struct LaunchPlan {
   // 1 (with mfma): o and down run split over (7-strip group, K range), their
   // partials added by the next RMSNorm launch (re_mfma.hip kMfPart)
   int mf_split;
+  // > 0 (with mfma): gate/up runs one workgroup per CU (k_mf_gu_cu), this grid
+  int gu_cu;
   // 1: decode attention per (row, KV head) for all query heads of the group
   int grouped_attn;
 };
@@ -223,6 +225,7 @@ bool mfma_step_supported(const Dims& d);
 int mfma_lm_partials(const Dims& d);
 bool mfma_lm_cu_fits(const Dims& d, int cus);
 bool mfma_split_fits(const Dims& d);
+bool mfma_gu_cu_fits(const Dims& d, int cus);
 size_t mfma_split_partial_bytes(const Dims& d);
 hipError_t prepare_mfma();
 // Layout of the packed copy; returns its bytes.

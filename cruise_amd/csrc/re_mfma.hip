@@ -351,13 +351,19 @@ typedef __attribute__((address_space(3))) void* lc_lptr;
 // s_waitcnt immediate: vmcnt <= vm, lgkmcnt 0, expcnt untouched.
 constexpr int lc_wait(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
 
-template <int NS>
-__device__ __forceinline__ void lm_cu_body(const MfArgs& a, unsigned char* lds, int s_begin, int lane, int wave,
-                                           float* cval, int* cidx, int* cbad) {
+// The K loop of a per-CU workgroup: the activations pass through LDS in
+// blocks of kLcBlock steps (every wave issues its eighth of each block's
+// global -> LDS loads), and this wave streams NS weight strips (wp: step 0 of
+// each, packed) with RING steps in flight, accumulating acc[j][t] over the
+// whole K in step order.  NS = 0: a wave with no strip only loads and joins
+// the barriers (every wave runs the same 1 + K / (32 kLcBlock) barriers).
+template <int NS, int RING>
+__device__ __forceinline__ void cu_stream(const MfArgs& a, unsigned char* lds, const bf16_t* const* wp, int lane,
+                                          int wave, mf_f32x4 (*acc)[kMfTiles]) {
+  constexpr int NA = NS > 0 ? NS : 1;
+  static_assert(RING * NS + 8 <= 63, "vmcnt holds at most 63");
+  static_assert(kLcBlock % RING == 0, "ring slots are compile-time within a block");
   const int ksteps = a.K / kMfK, nblocks = ksteps / kLcBlock;
-  const bf16_t* wp[NS];
-#pragma unroll
-  for (int j = 0; j < NS; ++j) wp[j] = a.p0 + (size_t)(s_begin + wave + kLcWaves * j) * ksteps * 512 + lane * 8;
   // activation block b, tile t, steps 8 (w & 1) ..+8 go to LDS by wave w's 8 loads
   auto issue_x = [&](int b) {
     const int t = wave >> 1, s0 = (wave & 1) * 8;
@@ -366,52 +372,68 @@ __device__ __forceinline__ void lm_cu_body(const MfArgs& a, unsigned char* lds, 
 #pragma unroll
     for (int i = 0; i < 8; ++i) __builtin_amdgcn_global_load_lds((lc_gptr)(src + i * 512), (lc_lptr)(dst + i * 1024), 16, 0, 0);
   };
-  mf_f32x4 acc[NS][kMfTiles];
+  if constexpr (NS > 0) {
 #pragma unroll
-  for (int j = 0; j < NS; ++j)
+    for (int j = 0; j < NS; ++j)
 #pragma unroll
-    for (int t = 0; t < kMfTiles; ++t) acc[j][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-  re_u32x4 wr[kLcRing][NS];
+      for (int t = 0; t < kMfTiles; ++t) acc[j][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  re_u32x4 wr[RING][NA];
   issue_x(0);
+  if constexpr (NS > 0) {
 #pragma unroll
-  for (int s = 0; s < kLcRing; ++s)
+    for (int s = 0; s < RING; ++s)
 #pragma unroll
-    for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * 512));
+      for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * 512));
+  }
   issue_x(1);
   // block 0 in LDS (the ring and block 1 may still be in flight)
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(lc_wait(kLcRing * NS + 8));
+  __builtin_amdgcn_s_waitcnt(lc_wait(RING * NS + 8));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   for (int b = 0; b < nblocks; ++b) {
-    const unsigned char* xb = lds + (b & 1) * kLcBlockBytes + lane * 16;
+    if constexpr (NS > 0) {
+      const unsigned char* xb = lds + (b & 1) * kLcBlockBytes + lane * 16;
 #pragma unroll
-    for (int s = 0; s < kLcBlock; ++s) {
-      const int S = b * kLcBlock + s, rw = s % kLcRing;
-      mf_bf16x8 xf[kMfTiles];
+      for (int s = 0; s < kLcBlock; ++s) {
+        const int S = b * kLcBlock + s, rw = S % RING;
+        mf_bf16x8 xf[kMfTiles];
 #pragma unroll
-      for (int t = 0; t < kMfTiles; ++t) xf[t] = *reinterpret_cast<const mf_bf16x8*>(xb + (t * kLcBlock + s) * 1024);
+        for (int t = 0; t < kMfTiles; ++t) xf[t] = *reinterpret_cast<const mf_bf16x8*>(xb + (t * kLcBlock + s) * 1024);
 #pragma unroll
-      for (int j = 0; j < NS; ++j)
+        for (int j = 0; j < NS; ++j)
 #pragma unroll
-        for (int t = 0; t < kMfTiles; ++t)
-          acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[t], __builtin_bit_cast(mf_bf16x8, wr[rw][j]), acc[j][t], 0, 0, 0);
-      // the refill past the last step re-reads the last one (unconditional, so
-      // every wait counts exactly these loads)
-      const int nxt = min(S + kLcRing, ksteps - 1);
+          for (int t = 0; t < kMfTiles; ++t)
+            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[t], __builtin_bit_cast(mf_bf16x8, wr[rw][j]), acc[j][t], 0, 0, 0);
+        // the refill past the last step re-reads the last one (unconditional,
+        // so every wait counts exactly these loads)
+        const int nxt = min(S + RING, ksteps - 1);
 #pragma unroll
-      for (int j = 0; j < NS; ++j) wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + nxt * 512));
-      __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < NS; ++j) wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + nxt * 512));
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // Every wave is done with buffer b & 1, and block b + 1 (requested before
     // this block's refills) has landed: only the ring may still be in flight.
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(lc_wait(kLcRing * NS));
+    __builtin_amdgcn_s_waitcnt(lc_wait(RING * NS));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (b + 2 < nblocks) issue_x(b + 2);
   }
   __builtin_amdgcn_s_waitcnt(lc_wait(0));
+}
+
+template <int NS>
+__device__ __forceinline__ void lm_cu_body(const MfArgs& a, unsigned char* lds, int s_begin, int lane, int wave,
+                                           float* cval, int* cidx, int* cbad) {
+  const int ksteps = a.K / kMfK;
+  const bf16_t* wp[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) wp[j] = a.p0 + (size_t)(s_begin + wave + kLcWaves * j) * ksteps * 512 + lane * 8;
+  mf_f32x4 acc[NS][kMfTiles];
+  cu_stream<NS, kLcRing>(a, lds, wp, lane, wave, acc);
   // Logits T(y) as fp32 (batched_decoder_step.py:405-408) and this wave's
   // first maximum per row over its strips.
   const int c = lane & 15, mrow = 4 * (lane >> 4);
@@ -488,6 +510,44 @@ __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_lm_cu(MfArgs a) {
     a.am_idx[(size_t)tid * G + g] = bi;
     a.am_bad[(size_t)tid * G + g] = bb;
   }
+}
+
+// gate/up with one workgroup per CU (64 rows): the I / 16 column strips are
+// split over the CUs (4-5 each for Qwen2.5-7B), wave w < that count streams
+// strip s_begin + w of the gate and of the up matrix over the whole K -- the
+// step chains of k_mgemv's gate/up waves -- sharing the LDS-staged
+// activations with the other waves; the SiLU * up epilogue is k_mgemv's.
+constexpr int kGcRing = 16;  // weight steps in flight per wave (few waves stream)
+
+__global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_gu_cu(MfArgs a) {
+  extern __shared__ __align__(16) unsigned char lc_smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  if (stop != 0) return;  // uniform
+  const int G = gridDim.x, g = blockIdx.x, T = a.hidden_dim / 16;  // hidden_dim: I
+  const int s_begin = (int)((long long)g * T / G), s_end = (int)((long long)(g + 1) * T / G);
+  const int u = s_begin + wave;
+  if (u >= s_end) {
+    cu_stream<0, kGcRing>(a, lc_smem, nullptr, lane, wave, nullptr);
+    return;
+  }
+  const int ksteps = a.K / kMfK;
+  const bf16_t* wp[2] = {a.p0 + (size_t)u * ksteps * 512 + lane * 8, a.p1 + (size_t)u * ksteps * 512 + lane * 8};
+  mf_f32x4 acc[2][kMfTiles];
+  cu_stream<2, kGcRing>(a, lc_smem, wp, lane, wave, acc);
+  const int c = lane & 15, mrow = 4 * (lane >> 4), n = u * 16 + c;
+#pragma unroll
+  for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = t * 16 + mrow + v;
+      if (m >= a.B) continue;
+      // silu(gate) * up, each result rounded (batched_decoder_step.py:391-398)
+      const float gt = Elt<bf16_t>::r(acc[0][t][v]);
+      const float up = Elt<bf16_t>::r(acc[1][t][v]);
+      const float sg = Elt<bf16_t>::r(gt / (1.0f + expf(-gt)));
+      a.out[xpack_index(m, n, a.hidden_dim)] = Elt<bf16_t>::t(Elt<bf16_t>::r(sg * up));
+    }
 }
 
 template <int NS, int WAVES, int KIND>
@@ -651,6 +711,13 @@ bool mfma_step_supported(const Dims& d) {
 
 int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
 
+// gate/up per CU: 1 to 8 strips per workgroup and whole LDS blocks.
+bool mfma_gu_cu_fits(const Dims& d, int cus) {
+  const int strips = d.intermediate / 16;
+  return mfma_step_supported(d) && cus > 0 && strips >= cus && strips <= kLcWaves * cus &&
+         d.hidden % (kMfK * kLcBlock) == 0 && d.hidden / (kMfK * kLcBlock) >= 2;
+}
+
 bool mfma_split_fits(const Dims& d) { return mfma_step_supported(d) && (d.hidden / 16) % kPartWaves == 0; }
 size_t mfma_split_partial_bytes(const Dims& d) { return (size_t)kPartRanges * d.batch * d.hidden * sizeof(float); }
 
@@ -695,6 +762,9 @@ hipError_t prepare_mfma() {
   if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidAll, true>();
   if (e == hipSuccess)
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_lm_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kLcLds));
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_gu_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLcLds));
   if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kHidSteps(kOWaves), false>();
   if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kInterSteps, true>();
@@ -779,7 +849,10 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.K = d.hidden;
       a.out = static_cast<bf16_t*>(sc.mlp);
       a.hidden_dim = d.intermediate;
-      mgemv_launch<2, kGuWaves, kMfGateUp, kHidAll, true>(a, d.intermediate / 16 / kGuWaves, stream);
+      if (env.plan.gu_cu > 0)
+        k_mf_gu_cu<<<env.plan.gu_cu, kLcWaves * 64, kLcLds, stream>>>(a);
+      else
+        mgemv_launch<2, kGuWaves, kMfGateUp, kHidAll, true>(a, d.intermediate / 16 / kGuWaves, stream);
       break;
     case MfmaOp::kDown:
       a.x = static_cast<const bf16_t*>(sc.mlp);

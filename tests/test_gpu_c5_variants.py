@@ -11,6 +11,9 @@ and cache writes exactly.
   waves split K and add their sums in wave order, instead of the default
   split over (strip group, K range) with the 8 range partials added, in
   range order, by the next RMSNorm launch: the same sums in the same order.
+- {"gu_cu": 0}: gate/up as 4-wave workgroups (each wave one strip of gate
+  and up over the whole K) instead of one workgroup per CU whose waves run
+  the same strips' step chains over LDS-staged activations.
 
 The engine allows one instance per process, so the runtimes run one after
 the other."""
@@ -41,7 +44,7 @@ def step_once(weights, tuning, inputs):
     tok, pos, length, slot, active, table, key, value = inputs
     rt = make_runtime(W, weights, tuning=tuning)
     try:
-        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units", "mf_split")}
+        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units", "mf_split", "gu_cu")}
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -52,7 +55,7 @@ def step_once(weights, tuning, inputs):
         rt.close()
 
 
-@pytest.mark.parametrize("tuning", [{"lm_cu": 0}, {"mf_split": 0}], ids=["lm_cu0", "mf_split0"])
+@pytest.mark.parametrize("tuning", [{"lm_cu": 0}, {"mf_split": 0}, {"gu_cu": 0}], ids=["lm_cu0", "mf_split0", "gu_cu0"])
 def test_matrix_core_plan_variants_match_bit_for_bit(weights_dev, tuning):
     rng = np.random.default_rng(6402)
     table = random_tables(rng, B, BPR, W.geometry.physical_blocks)
@@ -67,10 +70,12 @@ def test_matrix_core_plan_variants_match_bit_for_bit(weights_dev, tuning):
     base_facts, base = step_once(weights_dev, {}, inputs)
     facts, got = step_once(weights_dev, tuning, inputs)
     assert base_facts["lm_cu"] == 1 and base_facts["argmax_parts"] == base_facts["compute_units"]
-    assert base_facts["mf_split"] == 1
+    assert base_facts["mf_split"] == 1 and base_facts["gu_cu"] == base_facts["compute_units"]
     if "lm_cu" in tuning:
         assert facts["lm_cu"] == 0 and facts["argmax_parts"] == 1
-    else:
+    elif "mf_split" in tuning:
         assert facts["mf_split"] == 0
+    else:
+        assert facts["gu_cu"] == 0
     for name, a, b in zip(("logits", "next", "key", "value"), base, got):
         assert torch.equal(a, b), name
