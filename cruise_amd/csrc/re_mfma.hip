@@ -564,8 +564,9 @@ constexpr size_t mgemv_lds() {
 // first: h = T(h + T(p_0 + p_1 + ... )) over its fp32 partials in range order
 // (batched_decoder_step.py:380-386, 399-403), written back to the residual
 // stream, then normalized.
+template <int PARTS>
 __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, bf16_t* h, const bf16_t* w, bf16_t* y,
-                                               int H, float eps, const float* part, int parts, int B) {
+                                               int H, float eps, const float* part, int B) {
   __shared__ float red[4];
   if (done != nullptr && __builtin_nontemporal_load(done) != 0) return;
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
@@ -577,16 +578,22 @@ __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, bf16_t* h,
   for (int i = 0; i < kMaxChunks; ++i) {
     const int ch = tid + 256 * i;
     hv[i] = ch * 8 < H ? Vec8<bf16_t>::load_cached(hr + ch * 8) : Vec8<bf16_t>{};
-    if (parts > 0 && ch * 8 < H) {
-      float sum[8];
+    if (PARTS > 0 && ch * 8 < H) {
+      // all PARTS partials requested at once, then added in order
+      re_f32x4 pv[PARTS > 0 ? PARTS : 1][2];
       const float* p0 = part + (size_t)m * H + ch * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sum[e] = p0[e];
-      for (int r = 1; r < parts; ++r) {
-        const float* pr = p0 + (size_t)r * B * H;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum[e] += pr[e];
+      for (int r = 0; r < PARTS; ++r) {
+        pv[r][0] = *reinterpret_cast<const re_f32x4*>(p0 + (size_t)r * B * H);
+        pv[r][1] = *reinterpret_cast<const re_f32x4*>(p0 + (size_t)r * B * H + 4);
       }
+      float sum[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum[e] = pv[0][e >> 2][e & 3];
+#pragma unroll
+      for (int r = 1; r < PARTS; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum[e] += pv[r][e >> 2][e & 3];
       float nh[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) nh[e] = bf16_to_f(f_to_bf16(hv[i].get(e) + round_bf16(sum[e])));
@@ -771,6 +778,19 @@ hipError_t prepare_mfma() {
   return e;
 }
 
+// The RMSNorm launch; with pending (o or down split) partials it adds them first.
+static void mf_norm(const KernelEnv& env, const StepPtrs& st, size_t w_off, bool pending, hipStream_t stream) {
+  const Dims& d = env.dims;
+  const Scratch& sc = env.scratch;
+  bf16_t* h = static_cast<bf16_t*>(sc.hidden);
+  const bf16_t* w = reinterpret_cast<const bf16_t*>(env.weights + w_off);
+  bf16_t* y = static_cast<bf16_t*>(sc.xn);
+  if (pending)
+    k_mf_norm<kPartRanges><<<d.batch, 256, 0, stream>>>(st.done, h, w, y, d.hidden, d.rms_eps, sc.mf_part, d.batch);
+  else
+    k_mf_norm<0><<<d.batch, 256, 0, stream>>>(st.done, h, w, y, d.hidden, d.rms_eps, nullptr, d.batch);
+}
+
 hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, int layer, hipStream_t stream) {
   const Dims& d = env.dims;
   const Scratch& sc = env.scratch;
@@ -781,9 +801,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
   auto wt = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.weights + off); };
   auto pk = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.packed + off); };
   if (op == MfmaOp::kLmHead) {
-    k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<bf16_t*>(sc.hidden), wt(env.final_norm_off),
-                                           static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps, sc.mf_part,
-                                           env.plan.mf_split ? kPartRanges : 0, d.batch);
+    mf_norm(env, st, env.final_norm_off, env.plan.mf_split != 0, stream);
     a.x = static_cast<const bf16_t*>(sc.xn);
     a.p0 = pk(env.packed_lm_off);
     a.K = d.hidden;
@@ -807,9 +825,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
   switch (op) {
     case MfmaOp::kQkv:
       // layer > 0: the previous layer's down projection is still in partials
-      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<bf16_t*>(sc.hidden), wt(lo.input_norm),
-                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps, sc.mf_part,
-                                             env.plan.mf_split && layer > 0 ? kPartRanges : 0, d.batch);
+      mf_norm(env, st, lo.input_norm, env.plan.mf_split != 0 && layer > 0, stream);
       a.x = static_cast<const bf16_t*>(sc.xn);
       a.p0 = pk(po.qkv);
       a.w1 = wt(lo.qkv_b);
@@ -840,9 +856,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       }
       break;
     case MfmaOp::kGateUp:
-      k_mf_norm<<<d.batch, 256, 0, stream>>>(st.done, static_cast<bf16_t*>(sc.hidden), wt(lo.post_norm),
-                                             static_cast<bf16_t*>(sc.xn), d.hidden, d.rms_eps, sc.mf_part,
-                                             env.plan.mf_split ? kPartRanges : 0, d.batch);
+      mf_norm(env, st, lo.post_norm, env.plan.mf_split != 0, stream);
       a.x = static_cast<const bf16_t*>(sc.xn);
       a.p0 = pk(po.gate);
       a.p1 = pk(po.up);
