@@ -218,6 +218,195 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped decode attention on the matrix cores (bf16, head_dim 128, up to 8
+// query heads per KV head): one workgroup of 8 waves per (row, KV head), as
+// k_attn_group, with both products on v_mfma_f32_16x16x32_bf16.
+//   scores  Sᵀ tile of 16 positions x 16 head slots: A = 16 key rows (lane l
+//           holds row l % 16, elements 8 (l / 16) + 32 kk ..+8, read straight
+//           from the cache), B = the queries (head l % 16, zero past G), four
+//           k steps of 32; s = bf16(bf16(q.k) / sqrt(d)) into LDS;
+//   softmax exact max and sum per head over LDS, p = bf16(exp(s - max) / sum);
+//   P.V     per 256-position tile the value rows are transposed into LDS
+//           (a lane loads one 16-byte chunk of 8 consecutive rows and writes
+//           8 16-byte runs of Vᵀ), then wave w accumulates output columns
+//           16 w ..+16 of all heads: A = p (head l % 16, 8 positions), B =
+//           Vᵀ (column l % 16, the same 8 positions), 8 k steps per tile.
+// Same rounding points as k_attn_group; only fp32 summation orders differ.
+// Positions past the context (and rows whose slot is outside the cache) get
+// p = 0 and a zero value row.
+// ---------------------------------------------------------------------------
+typedef __bf16 mg_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float mg_f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kMgThreads = 512, kMgWaves = 8, kMgTile = 256, kMgD = 128, kMgMaxG = 8;
+constexpr int kMgVtLd = kMgTile + 8;  // Vᵀ row stride (bf16): 16-byte reads of 16 rows hit distinct banks
+
+// scores [G][window] fp32, then Vᵀ (16-byte aligned), then the block table
+__host__ __device__ size_t mgroup_vt_offset(int G, int window) { return ((size_t)G * window * sizeof(float) + 15) & ~(size_t)15; }
+size_t mgroup_smem_bytes(int G, int window, int blocks_per_row) {
+  return mgroup_vt_offset(G, window) + (size_t)kMgD * kMgVtLd * sizeof(bf16_t) + (size_t)blocks_per_row * sizeof(int);
+}
+
+template <bool P2>
+__global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
+  extern __shared__ __align__(16) unsigned char mg_smem[];
+  __shared__ float red[kMgWaves][kMgMaxG];
+  const int G = a.heads / a.kv_heads, W = a.window;
+  const int b = blockIdx.x / a.kv_heads, g = blockIdx.x - b * a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int l16 = lane & 15, lq = lane >> 4;
+  float* sc = reinterpret_cast<float*>(mg_smem);  // [G][W]
+  bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + mgroup_vt_offset(G, W));  // [D][kMgVtLd]
+  int* tabs = reinterpret_cast<int*>(vt + (size_t)kMgD * kMgVtLd);
+  const bf16_t* KC = static_cast<const bf16_t*>(a.key_cache);
+  const bf16_t* VC = static_cast<const bf16_t*>(a.value_cache);
+  const int n = a.len[b];
+  const bool uniform = n <= 0;
+  const int neff = uniform ? W : min(n, W);
+  const int ntiles = (neff + kMgTile - 1) / kMgTile;
+
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
+  // queries as the B operand: head l % 16 (zero past G), 4 k steps
+  mg_bf16x8 qf[4];
+  {
+    const bf16_t* qrow = static_cast<const bf16_t*>(a.q) + ((size_t)b * a.heads + g * G + min(l16, G - 1)) * kMgD;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const re_u32x4 v = *reinterpret_cast<const re_u32x4*>(qrow + kk * 32 + lq * 8);
+      qf[kk] = __builtin_bit_cast(mg_bf16x8, l16 < G ? v : re_u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+  lds_barrier();
+  if (stop != 0) return;  // uniform
+
+  // element offset of position j's row (this KV head) in the layer's cache, or -1
+  auto row_off = [&](int j) -> long long {
+    if (j >= neff) return -1;
+    int blk, in_blk;
+    block_of<P2>(j, a, blk, in_blk);
+    const long long slot = (long long)tabs[min(blk, a.blocks_per_row - 1)] * a.block_size + in_blk;
+    return slot >= 0 && slot < a.slots ? (slot * a.kv_heads + g) * kMgD : -1;
+  };
+
+  // Scores: wave w runs position groups 2 w and 2 w + 1 of each tile.
+  const float scale_div = sqrtf(static_cast<float>(kMgD));
+  for (int t = 0; t < ntiles; ++t) {
+    re_u32x4 kf[2][4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const long long off = row_off(t * kMgTile + (2 * wave + q) * 16 + l16);
+      const bf16_t* row = KC + (off >= 0 ? off : 0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) kf[q][kk] = *reinterpret_cast<const re_u32x4*>(row + kk * 32 + lq * 8);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      mg_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, kf[q][kk]), qf[kk], acc, 0, 0, 0);
+      // value v of lane l: position 4 (l / 16) + v of the group, head l % 16
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int j = t * kMgTile + (2 * wave + q) * 16 + lq * 4 + v;
+        float s = round_bf16(acc[v]);  // ExactQk output is bf16
+        s = round_bf16(s / scale_div);
+        if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
+        // a missing row (slot outside the cache) is a zero key: score 0
+        if (l16 < G && j < neff) sc[(size_t)l16 * W + j] = row_off(j) >= 0 ? s : (uniform ? s : 0.f);
+      }
+    }
+  }
+  lds_barrier();
+
+  // Softmax per head over LDS: exact max and sum, then each probability rounded.
+  float mx[kMgMaxG], inv[kMgMaxG];
+#pragma unroll
+  for (int h = 0; h < kMgMaxG; ++h) {
+    float m = -INFINITY;
+    if (h < G)
+      for (int j = tid; j < neff; j += kMgThreads) m = fmaxf(m, sc[(size_t)h * W + j]);
+    m = wave_max(m);
+    if (lane == 0) red[wave][h] = m;
+  }
+  lds_barrier();
+#pragma unroll
+  for (int h = 0; h < kMgMaxG; ++h) {
+    mx[h] = red[0][h];
+#pragma unroll
+    for (int w = 1; w < kMgWaves; ++w) mx[h] = fmaxf(mx[h], red[w][h]);
+    float e = 0.f;
+    if (h < G)
+      for (int j = tid; j < neff; j += kMgThreads) e += expf(sc[(size_t)h * W + j] - mx[h]);
+    inv[h] = wave_sum(e);
+  }
+  lds_barrier();  // every max read before red is reused
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = inv[h];
+  }
+  lds_barrier();
+#pragma unroll
+  for (int h = 0; h < kMgMaxG; ++h) {
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMgWaves; ++w) total += red[w][h];
+    inv[h] = 1.0f / total;
+    if (h < G)
+      for (int j = tid; j < neff; j += kMgThreads)
+        sc[(size_t)h * W + j] = round_bf16(expf(sc[(size_t)h * W + j] - mx[h]) * inv[h]);
+  }
+  lds_barrier();
+
+  // P.V: wave w owns output columns 16 w ..+16 of every head.
+  mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
+  const int p0 = wave * 32 + lq * 8;  // this lane's 8 positions of a tile (value loads)
+  for (int t = 0; t < ntiles; ++t) {
+    // value rows p0 .. p0+7 of the tile, chunk l16 (elements 8 l16 ..+8)
+    Vec8<bf16_t> vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const long long off = row_off(t * kMgTile + p0 + i);
+      vr[i] = off >= 0 ? Vec8<bf16_t>::load_cached(VC + off + l16 * 8) : Vec8<bf16_t>{};
+    }
+    lds_barrier();  // the previous tile's Vᵀ reads are done
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      re_u32x4 col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (vr[2 * i].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        const uint32_t hi = (vr[2 * i + 1].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        col[i] = lo | (hi << 16);
+      }
+      *reinterpret_cast<re_u32x4*>(vt + (size_t)(l16 * 8 + e) * kMgVtLd + p0) = col;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < kMgTile / 32; ++k) {
+      // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past the context / G)
+      const int j0 = t * kMgTile + k * 32 + lq * 8;
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = (l16 < G && j0 + e < neff) ? sc[(size_t)l16 * W + j0 + e] : 0.f;
+      re_u32x4 pa;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pa[i] = f2_to_bf16x2_raw(pv[2 * i], pv[2 * i + 1]);  // exact: p is bf16
+      const re_u32x4 vb = *reinterpret_cast<const re_u32x4*>(vt + (size_t)(wave * 16 + l16) * kMgVtLd + k * 32 + lq * 8);
+      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, vb),
+                                                     oacc, 0, 0, 0);
+    }
+  }
+  // value v of lane l: head 4 (l / 16) + v, column 16 w + l % 16
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int h = lq * 4 + v;
+    if (h < G)
+      static_cast<bf16_t*>(a.out)[((size_t)b * a.heads + g * G + h) * kMgD + wave * 16 + l16] = f_to_bf16(oacc[v]);
+  }
+}
+
 }  // namespace
 
 bool group_attention_fits(const Dims& d) {
@@ -225,6 +414,10 @@ bool group_attention_fits(const Dims& d) {
          group_smem_bytes(d.groups(), d.capacity, d.blocks_per_row) <= 96 * 1024;
 }
 bool group_attention_default(const Dims& d) { return group_attention_fits(d) && d.batch * d.kv_heads >= 64; }
+bool group_attention_mfma_fits(const Dims& d) {
+  return group_attention_fits(d) && d.groups() <= kMgMaxG && d.head_dim == kMgD &&
+         mgroup_smem_bytes(d.groups(), d.capacity, d.blocks_per_row) <= 150 * 1024;
+}
 
 namespace {
 
@@ -269,6 +462,15 @@ hipError_t prepare_attention(const Dims& d) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) return e;
   }
+  if (group_attention_mfma_fits(d)) {
+    const int bytes = static_cast<int>(mgroup_smem_bytes(d.groups(), d.capacity, d.blocks_per_row));
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_mgroup<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_mgroup<false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+  }
   const size_t bytes = attention_lds_bytes(d);
   if (d.dtype_bytes == 2) {
     if (d.head_dim == 64) return allow_t<bf16_t, 64>(bytes);
@@ -281,6 +483,14 @@ hipError_t prepare_attention(const Dims& d) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream) {
+  if (a.grouped == 2 && group_attention_mfma_fits(d)) {
+    const size_t smem = mgroup_smem_bytes(d.groups(), a.window, a.blocks_per_row);
+    if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size)
+      k_attn_mgroup<true><<<a.B * a.kv_heads, kMgThreads, smem, stream>>>(a);
+    else
+      k_attn_mgroup<false><<<a.B * a.kv_heads, kMgThreads, smem, stream>>>(a);
+    return hipGetLastError();
+  }
   if (a.grouped && group_attention_fits(d)) {
     const size_t smem = group_smem_bytes(d.groups(), a.window, a.blocks_per_row);
     if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size)

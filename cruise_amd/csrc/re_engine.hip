@@ -337,6 +337,11 @@ bool make_plan(Engine& e, const Json& cfg) {
   p.grouped_attn = group_attention_default(d) ? 1 : 0;
   if (tune != nullptr && group_attention_fits(d))
     p.grouped_attn = static_cast<int>(tune->number_or("grouped_attention", p.grouped_attn)) != 0 ? 1 : 0;
+  // the grouped attention's products on the matrix cores ("tuning":
+  // {"attention_mfma": 0} keeps the vector-unit version)
+  if (p.grouped_attn && group_attention_mfma_fits(d) &&
+      (tune == nullptr || tune->number_or("attention_mfma", 1) != 0))
+    p.grouped_attn = 2;
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
     // "down_whole": 0 keeps the split-K down projection and its reduce launch
@@ -1715,6 +1720,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"lm_cu", e->plan.lm_cu},
       {"mf_split", e->plan.mf_split},
       {"gu_cu", e->plan.gu_cu},
+      {"grouped_attention", e->plan.grouped_attn},
       {"argmax_parts", e->plan.argmax_parts},
       {"o_grid", e->plan.o_grid},
       {"lm_grid", e->plan.lm_grid},

@@ -178,13 +178,15 @@ struct AttnArgs {
   int B, heads, kv_heads, head_dim, block_size, blocks_per_row, window;
   long long slots;
   int bs_shift;            // log2(block_size) when it is a power of two, else -1
-  int grouped;             // 1: one workgroup per (row, KV head) (re_attn.hip k_attn_group)
+  int grouped;             // 1: one workgroup per (row, KV head) (re_attn.hip k_attn_group); 2: the same on
+                           // the matrix cores (k_attn_mgroup)
 };
 size_t attention_lds_bytes(const Dims& d);
 // The grouped attention's default: many rows (B x KV heads >= 64); whether the
 // shape allows it at all.
 bool group_attention_default(const Dims& d);
 bool group_attention_fits(const Dims& d);
+bool group_attention_mfma_fits(const Dims& d);
 hipError_t prepare_attention(const Dims& d);
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream);
 
