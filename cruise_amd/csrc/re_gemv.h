@@ -80,13 +80,16 @@ constexpr int seg_vecs_per_thread() {
 
 // Load rows b0..b0+MB-1, columns [k0, k0+len), of X [B, ldg] into registers:
 // slot i of thread t holds Vec8 number t + 256*i of the row-major [MB, len]
-// block.  The loads are unconditional (addresses clamped into the block), so
-// no branch separates them from later loads and every wait counts exactly;
-// store_rows_block zeroes what lies outside.
+// block.  Within the first 256 threads the loads are unconditional (addresses
+// clamped into the block), so every wait counts exactly; store_rows_block
+// zeroes what lies outside.  Threads from 256 up (wider workgroups) load
+// nothing: each activation line they requested would take one of the CU's
+// outstanding-miss slots that the weight stream needs.
 template <typename T, int MB>
 __device__ __forceinline__ void load_rows_block(Vec8<T> (&v)[seg_vecs_per_thread<MB>()], const T* __restrict__ X,
                                                 int ldg, int b0, int B, int k0, int len, int tid) {
   const int per_row = max(len / 8, 1);
+  if (tid >= 256) return;  // wave-uniform
 #pragma unroll
   for (int i = 0; i < seg_vecs_per_thread<MB>(); ++i) {
     const int idx = min(tid + 256 * i, MB * per_row - 1);
@@ -160,8 +163,12 @@ __device__ __forceinline__ Vec8<bf16_t> norm_apply<bf16_t>(const Vec8<bf16_t>& h
 template <typename T, int MB>
 __device__ __forceinline__ void norm_load(NormIn<T, MB>& in, const T* __restrict__ hidden, const T* __restrict__ norm_w,
                                           int b0, int B, int H, int tid) {
-  // unconditional (clamped) loads; norm_to_lds ignores what lies outside
+  // unconditional (clamped) loads in the owning threads; norm_to_lds ignores
+  // what lies outside.  Threads from 256 up own nothing and load nothing (a
+  // wave-uniform branch): their requests would only hold miss slots the
+  // weight stream needs.
   const int per_row = H / 8;
+  if (tid >= 256) return;
 #pragma unroll
   for (int j = 0; j < kNormChunks; ++j) {
     const int c = min(tid + 256 * j, per_row - 1);
