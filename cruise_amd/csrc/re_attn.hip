@@ -222,29 +222,73 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
 // Grouped decode attention on the matrix cores (bf16, head_dim 128, up to 8
 // query heads per KV head): one workgroup of 8 waves per (row, KV head), as
 // k_attn_group, with both products on v_mfma_f32_16x16x32_bf16.
-//   scores  Sᵀ tile of 16 positions x 16 head slots: A = 16 key rows (lane l
-//           holds row l % 16, elements 8 (l / 16) + 32 kk ..+8, read straight
-//           from the cache), B = the queries (head l % 16, zero past G), four
-//           k steps of 32; s = bf16(bf16(q.k) / sqrt(d)) into LDS;
-//   softmax exact max and sum per head over LDS, p = bf16(exp(s - max) / sum);
-//   P.V     per 256-position tile the value rows are transposed into LDS
-//           (a lane loads one 16-byte chunk of 8 consecutive rows and writes
-//           8 16-byte runs of Vᵀ), then wave w accumulates output columns
-//           16 w ..+16 of all heads: A = p (head l % 16, 8 positions), B =
-//           Vᵀ (column l % 16, the same 8 positions), 8 k steps per tile.
+//   requests  the keys of a chunk of up to four 256-position tiles go out
+//             together (wave w: position groups 2w and 2w + 1 of each tile;
+//             lane l: row l % 16, elements 8 (l / 16) + 32 kk ..+8, the MFMA
+//             operand layout), and the first chunk's values follow as the
+//             last chunk's key tiles are consumed, so they stream during the
+//             softmax;
+//   scores    Sᵀ tile of 16 positions x 16 head slots: A = 16 key rows, B =
+//             the queries (head l % 16, zero past G), four k steps of 32;
+//             s = bf16(bf16(q.k) / sqrt(d)) into LDS;
+//   softmax   exact max and sum per head over LDS (the heads' wave
+//             reductions interleaved, one wait per exchange step), then
+//             p = bf16(exp(s - max) / sum) into a bf16 array, zero past the
+//             context;
+//   P.V       per tile the value rows are transposed into LDS (a lane holds
+//             one 16-byte chunk of 8 consecutive rows and writes 8 16-byte
+//             runs of Vᵀ), then wave w accumulates output columns 16 w ..+16
+//             of all heads: A = p (head l % 16, 8 positions, one 16-byte LDS
+//             read), B = Vᵀ (column l % 16, the same 8 positions), 8 k steps.
 // Same rounding points as k_attn_group; only fp32 summation orders differ.
-// Positions past the context (and rows whose slot is outside the cache) get
-// p = 0 and a zero value row.
+// Rows whose slot is outside the cache are zero keys (score 0) and zero
+// values.  Every key and value request is unconditional (a row past the
+// context or missing reads the cache's first row): a load under a per-lane
+// condition would make the next use wait for every outstanding load.
 // ---------------------------------------------------------------------------
 typedef __bf16 mg_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float mg_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMgThreads = 512, kMgWaves = 8, kMgTile = 256, kMgD = 128, kMgMaxG = 8;
+constexpr int kMgChunk = 4;           // tiles whose keys are requested together
 constexpr int kMgVtLd = kMgTile + 8;  // Vᵀ row stride (bf16): 16-byte reads of 16 rows hit distinct banks
 
-// scores [G][window] fp32, then Vᵀ (16-byte aligned), then the block table
-__host__ __device__ size_t mgroup_vt_offset(int G, int window) { return ((size_t)G * window * sizeof(float) + 15) & ~(size_t)15; }
-size_t mgroup_smem_bytes(int G, int window, int blocks_per_row) {
-  return mgroup_vt_offset(G, window) + (size_t)kMgD * kMgVtLd * sizeof(bf16_t) + (size_t)blocks_per_row * sizeof(int);
+// The window's tiles rounded up to whole chunks.
+__host__ __device__ int mgroup_tiles(int window) {
+  const int t = (window + kMgTile - 1) / kMgTile;
+  return (t + kMgChunk - 1) / kMgChunk * kMgChunk;
+}
+// LDS: scores [G][window] fp32, probabilities [8][tiles * 256] bf16, Vᵀ
+// [128][kMgVtLd] bf16, row offsets [tiles * 256] int, the block table.
+struct MgLayout {
+  size_t pb, vt, roff, tabs, total;
+};
+__host__ __device__ MgLayout mgroup_layout(int G, int window, int blocks_per_row) {
+  MgLayout l;
+  const size_t span = (size_t)mgroup_tiles(window) * kMgTile;
+  l.pb = ((size_t)G * window * sizeof(float) + 15) & ~(size_t)15;
+  l.vt = l.pb + (size_t)kMgMaxG * span * sizeof(bf16_t);
+  l.roff = l.vt + (size_t)kMgD * kMgVtLd * sizeof(bf16_t);
+  l.tabs = l.roff + span * sizeof(int);
+  l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
+  return l;
+}
+size_t mgroup_smem_bytes(int G, int window, int blocks_per_row) { return mgroup_layout(G, window, blocks_per_row).total; }
+
+// Wave-wide max / sum of N values at once: the N exchanges of a step are
+// independent, so they wait together.
+template <int N>
+__device__ __forceinline__ void wave_max_n(float (&v)[N]) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __shfl_xor(v[i], s, 64));
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], s, 64);
 }
 
 template <bool P2>
@@ -255,15 +299,21 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   const int b = blockIdx.x / a.kv_heads, g = blockIdx.x - b * a.kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
   const int l16 = lane & 15, lq = lane >> 4;
-  float* sc = reinterpret_cast<float*>(mg_smem);  // [G][W]
-  bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + mgroup_vt_offset(G, W));  // [D][kMgVtLd]
-  int* tabs = reinterpret_cast<int*>(vt + (size_t)kMgD * kMgVtLd);
+  const MgLayout L = mgroup_layout(G, W, a.blocks_per_row);
+  const int span = mgroup_tiles(W) * kMgTile;
+  float* sc = reinterpret_cast<float*>(mg_smem);            // [G][W]
+  bf16_t* pb = reinterpret_cast<bf16_t*>(mg_smem + L.pb);   // [kMgMaxG][span]
+  bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + L.vt);   // [D][kMgVtLd]
+  int* roff = reinterpret_cast<int*>(mg_smem + L.roff);     // [span]
+  int* tabs = reinterpret_cast<int*>(mg_smem + L.tabs);
   const bf16_t* KC = static_cast<const bf16_t*>(a.key_cache);
   const bf16_t* VC = static_cast<const bf16_t*>(a.value_cache);
   const int n = a.len[b];
   const bool uniform = n <= 0;
   const int neff = uniform ? W : min(n, W);
   const int ntiles = (neff + kMgTile - 1) / kMgTile;
+  const int nchunks = (ntiles + kMgChunk - 1) / kMgChunk;
+  const int padded = nchunks * kMgChunk * kMgTile;  // positions the requests cover (<= span)
 
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
   for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
@@ -280,26 +330,32 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   lds_barrier();
   if (stop != 0) return;  // uniform
 
-  // element offset of position j's row (this KV head) in the layer's cache, or -1
-  auto row_off = [&](int j) -> long long {
-    if (j >= neff) return -1;
-    int blk, in_blk;
-    block_of<P2>(j, a, blk, in_blk);
-    const long long slot = (long long)tabs[min(blk, a.blocks_per_row - 1)] * a.block_size + in_blk;
-    return slot >= 0 && slot < a.slots ? (slot * a.kv_heads + g) * kMgD : -1;
-  };
+  // Element offset of each position's row (this KV head) in the layer's
+  // cache, or -1 past the context or for a slot outside the cache; one LDS
+  // read per request afterwards (cache offsets of a layer fit 32 bits).
+  for (int j = tid; j < padded; j += kMgThreads) {
+    int o = -1;
+    if (j < neff) {
+      int blk, in_blk;
+      block_of<P2>(j, a, blk, in_blk);
+      const long long slot = (long long)tabs[min(blk, a.blocks_per_row - 1)] * a.block_size + in_blk;
+      if (slot >= 0 && slot < a.slots) o = static_cast<int>((slot * a.kv_heads + g) * kMgD);
+    }
+    roff[j] = o;
+  }
+  lds_barrier();
 
-  // Scores: wave w runs position groups 2 w and 2 w + 1 of each tile.
   const float scale_div = sqrtf(static_cast<float>(kMgD));
-  for (int t = 0; t < ntiles; ++t) {
-    re_u32x4 kf[2][4];
+  auto load_k = [&](re_u32x4(&kf)[2][4], int t) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const long long off = row_off(t * kMgTile + (2 * wave + q) * 16 + l16);
+      const int off = roff[t * kMgTile + (2 * wave + q) * 16 + l16];
       const bf16_t* row = KC + (off >= 0 ? off : 0);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) kf[q][kk] = *reinterpret_cast<const re_u32x4*>(row + kk * 32 + lq * 8);
     }
+  };
+  auto score_k = [&](const re_u32x4(&kf)[2][4], int t) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       mg_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -314,21 +370,66 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
         s = round_bf16(s / scale_div);
         if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
         // a missing row (slot outside the cache) is a zero key: score 0
-        if (l16 < G && j < neff) sc[(size_t)l16 * W + j] = row_off(j) >= 0 ? s : (uniform ? s : 0.f);
+        if (l16 < G && j < neff) sc[(size_t)l16 * W + j] = roff[j] >= 0 || uniform ? s : 0.f;
       }
+    }
+  };
+  // value rows p0 .. p0+7 of tile t, chunk l16 (elements 8 l16 ..+8); bit i
+  // of the returned mask marks row i valid (invalid rows enter as zero)
+  const int p0 = wave * 32 + lq * 8;
+  auto load_v = [&](Vec8<bf16_t>(&vr)[8], int t) {
+    int mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int off = roff[t * kMgTile + p0 + i];
+      vr[i] = Vec8<bf16_t>::load_cached(VC + (off >= 0 ? off : 0) + l16 * 8);
+      mask |= (off >= 0 ? 1 : 0) << i;
+    }
+    return mask;
+  };
+
+  // Scores, one chunk of key tiles at a time; the first chunk's values are
+  // requested as the last chunk's key tiles are consumed.
+  Vec8<bf16_t> vr[kMgChunk][8];
+  int vmask[kMgChunk];
+  for (int c = 0; c + 1 < nchunks; ++c) {
+    re_u32x4 kf[kMgChunk][2][4];
+#pragma unroll
+    for (int i = 0; i < kMgChunk; ++i) load_k(kf[i], c * kMgChunk + i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kMgChunk; ++i) score_k(kf[i], c * kMgChunk + i);
+  }
+  {
+    const int c = nchunks - 1;
+    re_u32x4 kf[kMgChunk][2][4];
+#pragma unroll
+    for (int i = 0; i < kMgChunk; ++i) load_k(kf[i], c * kMgChunk + i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kMgChunk; ++i) {
+      score_k(kf[i], c * kMgChunk + i);
+      vmask[i] = load_v(vr[i], i);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   lds_barrier();
 
-  // Softmax per head over LDS: exact max and sum, then each probability rounded.
+  // Softmax per head over LDS: exact max and sum, then each probability
+  // rounded to bf16 (zero from the context's end to the requests' end).
   float mx[kMgMaxG], inv[kMgMaxG];
+  {
+    float m[kMgMaxG];
 #pragma unroll
-  for (int h = 0; h < kMgMaxG; ++h) {
-    float m = -INFINITY;
-    if (h < G)
-      for (int j = tid; j < neff; j += kMgThreads) m = fmaxf(m, sc[(size_t)h * W + j]);
-    m = wave_max(m);
-    if (lane == 0) red[wave][h] = m;
+    for (int h = 0; h < kMgMaxG; ++h) m[h] = -INFINITY;
+    for (int j = tid; j < neff; j += kMgThreads)
+#pragma unroll
+      for (int h = 0; h < kMgMaxG; ++h)
+        if (h < G) m[h] = fmaxf(m[h], sc[(size_t)h * W + j]);
+    wave_max_n<kMgMaxG>(m);
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = m[h];
   }
   lds_barrier();
 #pragma unroll
@@ -336,15 +437,20 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     mx[h] = red[0][h];
 #pragma unroll
     for (int w = 1; w < kMgWaves; ++w) mx[h] = fmaxf(mx[h], red[w][h]);
-    float e = 0.f;
-    if (h < G)
-      for (int j = tid; j < neff; j += kMgThreads) e += expf(sc[(size_t)h * W + j] - mx[h]);
-    inv[h] = wave_sum(e);
   }
   lds_barrier();  // every max read before red is reused
-  if (lane == 0) {
+  {
+    float e[kMgMaxG];
 #pragma unroll
-    for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = inv[h];
+    for (int h = 0; h < kMgMaxG; ++h) e[h] = 0.f;
+    for (int j = tid; j < neff; j += kMgThreads)
+#pragma unroll
+      for (int h = 0; h < kMgMaxG; ++h)
+        if (h < G) e[h] += expf(sc[(size_t)h * W + j] - mx[h]);
+    wave_sum_n<kMgMaxG>(e);
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = e[h];
   }
   lds_barrier();
 #pragma unroll
@@ -353,31 +459,26 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
 #pragma unroll
     for (int w = 0; w < kMgWaves; ++w) total += red[w][h];
     inv[h] = 1.0f / total;
-    if (h < G)
-      for (int j = tid; j < neff; j += kMgThreads)
-        sc[(size_t)h * W + j] = round_bf16(expf(sc[(size_t)h * W + j] - mx[h]) * inv[h]);
   }
-  lds_barrier();
+  for (int j = tid; j < padded; j += kMgThreads)
+#pragma unroll
+    for (int h = 0; h < kMgMaxG; ++h) {
+      float p = 0.f;
+      if (h < G && j < neff) p = round_bf16(expf(sc[(size_t)h * W + j] - mx[h]) * inv[h]);
+      pb[(size_t)h * span + j] = f_to_bf16(p);  // exact: p is bf16
+    }
 
   // P.V: wave w owns output columns 16 w ..+16 of every head.
   mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
-  const int p0 = wave * 32 + lq * 8;  // this lane's 8 positions of a tile (value loads)
-  for (int t = 0; t < ntiles; ++t) {
-    // value rows p0 .. p0+7 of the tile, chunk l16 (elements 8 l16 ..+8)
-    Vec8<bf16_t> vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const long long off = row_off(t * kMgTile + p0 + i);
-      vr[i] = off >= 0 ? Vec8<bf16_t>::load_cached(VC + off + l16 * 8) : Vec8<bf16_t>{};
-    }
-    lds_barrier();  // the previous tile's Vᵀ reads are done
+  auto pv_tile = [&](const Vec8<bf16_t>(&v)[8], int mask, int t) {
+    lds_barrier();  // the probabilities are written and the previous tile's Vᵀ reads are done
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       re_u32x4 col;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = (vr[2 * i].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const uint32_t hi = (vr[2 * i + 1].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        const uint32_t lo = (mask >> (2 * i)) & 1 ? (v[2 * i].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
+        const uint32_t hi = (mask >> (2 * i + 1)) & 1 ? (v[2 * i + 1].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
         col[i] = lo | (hi << 16);
       }
       *reinterpret_cast<re_u32x4*>(vt + (size_t)(l16 * 8 + e) * kMgVtLd + p0) = col;
@@ -385,18 +486,23 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     lds_barrier();
 #pragma unroll
     for (int k = 0; k < kMgTile / 32; ++k) {
-      // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past the context / G)
-      const int j0 = t * kMgTile + k * 32 + lq * 8;
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = (l16 < G && j0 + e < neff) ? sc[(size_t)l16 * W + j0 + e] : 0.f;
-      re_u32x4 pa;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pa[i] = f2_to_bf16x2_raw(pv[2 * i], pv[2 * i + 1]);  // exact: p is bf16
-      const re_u32x4 vb = *reinterpret_cast<const re_u32x4*>(vt + (size_t)(wave * 16 + l16) * kMgVtLd + k * 32 + lq * 8);
-      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, vb),
+      // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past G)
+      re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
+                                                        k * 32 + lq * 8);
+      if (l16 >= G) pa = re_u32x4{0u, 0u, 0u, 0u};
+      const re_u32x4 vb4 = *reinterpret_cast<const re_u32x4*>(vt + (size_t)(wave * 16 + l16) * kMgVtLd + k * 32 + lq * 8);
+      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, vb4),
                                                      oacc, 0, 0, 0);
     }
+  };
+#pragma unroll
+  for (int i = 0; i < kMgChunk; ++i) pv_tile(vr[i], vmask[i], i);
+  for (int c = 1; c < nchunks; ++c) {
+#pragma unroll
+    for (int i = 0; i < kMgChunk; ++i) vmask[i] = load_v(vr[i], c * kMgChunk + i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kMgChunk; ++i) pv_tile(vr[i], vmask[i], c * kMgChunk + i);
   }
   // value v of lane l: head 4 (l / 16) + v, column 16 w + l % 16
 #pragma unroll
