@@ -230,9 +230,11 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
 //             softmax;
 //   scores    Sᵀ tile of 16 positions x 16 head slots: A = 16 key rows, B =
 //             the queries (head l % 16, zero past G), four k steps of 32;
-//             s = bf16(bf16(q.k) / sqrt(d)) into LDS;
-//   softmax   exact max and sum per head over LDS (the heads' wave
-//             reductions interleaved, one wait per exchange step), then
+//             s = bf16(bf16(q.k) / sqrt(d)) into LDS, position-major (the 8
+//             head slots of a position in 32 bytes);
+//   softmax   exact max and sum per head over LDS: a thread reads all heads
+//             of a position in two 16-byte reads, the heads' wave reductions
+//             are interleaved (one wait per exchange step); then
 //             p = bf16(exp(s - max) / sum) into a bf16 array, zero past the
 //             context;
 //   P.V       per tile the value rows are transposed into LDS (a lane holds
@@ -257,7 +259,7 @@ __host__ __device__ int mgroup_tiles(int window) {
   const int t = (window + kMgTile - 1) / kMgTile;
   return (t + kMgChunk - 1) / kMgChunk * kMgChunk;
 }
-// LDS: scores [G][window] fp32, probabilities [8][tiles * 256] bf16, Vᵀ
+// LDS: scores [window][8] fp32, probabilities [8][tiles * 256] bf16, Vᵀ
 // [128][kMgVtLd] bf16, row offsets [tiles * 256] int, the block table.
 struct MgLayout {
   size_t pb, vt, roff, tabs, total;
@@ -265,7 +267,8 @@ struct MgLayout {
 __host__ __device__ MgLayout mgroup_layout(int G, int window, int blocks_per_row) {
   MgLayout l;
   const size_t span = (size_t)mgroup_tiles(window) * kMgTile;
-  l.pb = ((size_t)G * window * sizeof(float) + 15) & ~(size_t)15;
+  (void)G;
+  l.pb = (size_t)window * kMgMaxG * sizeof(float);
   l.vt = l.pb + (size_t)kMgMaxG * span * sizeof(bf16_t);
   l.roff = l.vt + (size_t)kMgD * kMgVtLd * sizeof(bf16_t);
   l.tabs = l.roff + span * sizeof(int);
@@ -301,7 +304,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   const int l16 = lane & 15, lq = lane >> 4;
   const MgLayout L = mgroup_layout(G, W, a.blocks_per_row);
   const int span = mgroup_tiles(W) * kMgTile;
-  float* sc = reinterpret_cast<float*>(mg_smem);            // [G][W]
+  float* sc = reinterpret_cast<float*>(mg_smem);            // [W][kMgMaxG]
   bf16_t* pb = reinterpret_cast<bf16_t*>(mg_smem + L.pb);   // [kMgMaxG][span]
   bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + L.vt);   // [D][kMgVtLd]
   int* roff = reinterpret_cast<int*>(mg_smem + L.roff);     // [span]
@@ -370,7 +373,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
         s = round_bf16(s / scale_div);
         if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
         // a missing row (slot outside the cache) is a zero key: score 0
-        if (l16 < G && j < neff) sc[(size_t)l16 * W + j] = roff[j] >= 0 || uniform ? s : 0.f;
+        if (l16 < G && j < neff) sc[(size_t)j * kMgMaxG + l16] = roff[j] >= 0 || uniform ? s : 0.f;
       }
     }
   };
@@ -417,15 +420,27 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
 
   // Softmax per head over LDS: exact max and sum, then each probability
   // rounded to bf16 (zero from the context's end to the requests' end).
+  // Head slots from G up hold no score: they are masked, not branched on.
+  auto head_scores = [&](int j, float (&v)[kMgMaxG]) {
+    const re_f32x4 lo = *reinterpret_cast<const re_f32x4*>(sc + (size_t)j * kMgMaxG);
+    const re_f32x4 hi = *reinterpret_cast<const re_f32x4*>(sc + (size_t)j * kMgMaxG + 4);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      v[h] = lo[h];
+      v[h + 4] = hi[h];
+    }
+  };
   float mx[kMgMaxG], inv[kMgMaxG];
   {
     float m[kMgMaxG];
 #pragma unroll
     for (int h = 0; h < kMgMaxG; ++h) m[h] = -INFINITY;
-    for (int j = tid; j < neff; j += kMgThreads)
+    for (int j = tid; j < neff; j += kMgThreads) {
+      float v[kMgMaxG];
+      head_scores(j, v);
 #pragma unroll
-      for (int h = 0; h < kMgMaxG; ++h)
-        if (h < G) m[h] = fmaxf(m[h], sc[(size_t)h * W + j]);
+      for (int h = 0; h < kMgMaxG; ++h) m[h] = fmaxf(m[h], h < G ? v[h] : -INFINITY);
+    }
     wave_max_n<kMgMaxG>(m);
     if (lane == 0)
 #pragma unroll
@@ -443,10 +458,12 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     float e[kMgMaxG];
 #pragma unroll
     for (int h = 0; h < kMgMaxG; ++h) e[h] = 0.f;
-    for (int j = tid; j < neff; j += kMgThreads)
+    for (int j = tid; j < neff; j += kMgThreads) {
+      float v[kMgMaxG];
+      head_scores(j, v);
 #pragma unroll
-      for (int h = 0; h < kMgMaxG; ++h)
-        if (h < G) e[h] += expf(sc[(size_t)h * W + j] - mx[h]);
+      for (int h = 0; h < kMgMaxG; ++h) e[h] += h < G ? expf(v[h] - mx[h]) : 0.f;
+    }
     wave_sum_n<kMgMaxG>(e);
     if (lane == 0)
 #pragma unroll
@@ -460,13 +477,20 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     for (int w = 0; w < kMgWaves; ++w) total += red[w][h];
     inv[h] = 1.0f / total;
   }
-  for (int j = tid; j < padded; j += kMgThreads)
+  for (int j = tid; j < padded; j += kMgThreads) {
+    float v[kMgMaxG];
+    if (j < neff) {
+      head_scores(j, v);
+    } else {
+#pragma unroll
+      for (int h = 0; h < kMgMaxG; ++h) v[h] = 0.f;
+    }
 #pragma unroll
     for (int h = 0; h < kMgMaxG; ++h) {
-      float p = 0.f;
-      if (h < G && j < neff) p = round_bf16(expf(sc[(size_t)h * W + j] - mx[h]) * inv[h]);
+      const float p = h < G && j < neff ? round_bf16(expf(v[h] - mx[h]) * inv[h]) : 0.f;
       pb[(size_t)h * span + j] = f_to_bf16(p);  // exact: p is bf16
     }
+  }
 
   // P.V: wave w owns output columns 16 w ..+16 of every head.
   mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
