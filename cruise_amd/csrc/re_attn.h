@@ -233,7 +233,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
     float o = 0.f;
     for (int ww = 0; ww < kAttnThreads / 64; ++ww)
       for (int rr = 0; rr < S::kRg; ++rr) o += part[(ww * 64 + rr * L + cc) * 8 + e];
-    static_cast<T*>(a.out)[((size_t)b * a.heads + h) * D + tid] = Elt<T>::t(o);
+    const int k = h * D + tid;
+    static_cast<T*>(a.out)[a.packed_out ? xpack_index(b, k, a.heads * D) : (size_t)b * a.heads * D + k] = Elt<T>::t(o);
   }
 }
 

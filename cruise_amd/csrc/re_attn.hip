@@ -214,7 +214,9 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) v += osum[w * G * kGrpD + o];
     const int h = o / kGrpD, d = o - h * kGrpD;
-    static_cast<bf16_t*>(a.out)[((size_t)b * a.heads + g * G + h) * kGrpD + d] = f_to_bf16(v);
+    const int k = (g * G + h) * kGrpD + d;
+    static_cast<bf16_t*>(a.out)[a.packed_out ? xpack_index(b, k, a.heads * kGrpD) : (size_t)b * a.heads * kGrpD + k] =
+        f_to_bf16(v);
   }
 }
 
@@ -532,8 +534,11 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int h = lq * 4 + v;
-    if (h < G)
-      static_cast<bf16_t*>(a.out)[((size_t)b * a.heads + g * G + h) * kMgD + wave * 16 + l16] = f_to_bf16(oacc[v]);
+    if (h < G) {
+      const int k = (g * G + h) * kMgD + wave * 16 + l16;
+      static_cast<bf16_t*>(a.out)[a.packed_out ? xpack_index(b, k, a.heads * kMgD) : (size_t)b * a.heads * kMgD + k] =
+          f_to_bf16(oacc[v]);
+    }
   }
 }
 

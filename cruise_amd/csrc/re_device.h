@@ -185,6 +185,14 @@ __device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
 // Workgroup barrier that orders LDS only.  __syncthreads() also orders global
 // memory, so it waits for every global load in flight; this one lets weight
 // loads issued before it stay in flight across the barrier.
+// Packed 64-row activations of the matrix-core path: row m, element k of a
+// [rows, K] block at ((m/16 * K/32 + k/32) * 64 + (m%16 + 16 (k%32)/8)) * 8 +
+// k%8, so a wave's MFMA fragment of one 16-row tile and one 32-wide k step is
+// 1 KB contiguous (rows a multiple of 16, K of 32).
+__host__ __device__ __forceinline__ size_t xpack_index(int m, int k, int K) {
+  return ((size_t)((m >> 4) * (K >> 5) + (k >> 5)) * 64 + (m & 15) + 16 * ((k & 31) >> 3)) * 8 + (k & 7);
+}
+
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();

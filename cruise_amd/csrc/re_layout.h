@@ -180,6 +180,7 @@ struct AttnArgs {
   int bs_shift;            // log2(block_size) when it is a power of two, else -1
   int grouped;             // 1: one workgroup per (row, KV head) (re_attn.hip k_attn_group); 2: the same on
                            // the matrix cores (k_attn_mgroup)
+  int packed_out;          // out in the matrix-core path's packed layout (xpack_index, K = NH*d)
 };
 size_t attention_lds_bytes(const Dims& d);
 // The grouped attention's default: many rows (B x KV heads >= 64); whether the

@@ -98,12 +98,7 @@ __device__ __forceinline__ int strip_row(const MfArgs& a, int g, int j, int c) {
   }
 }
 
-// Packed activations (XP): row m, element k at ((m/16 * K/32 + k/32) * 64 +
-// (m%16 + 16 (k%32)/8)) * 8 + k%8, so a wave's fragment of one 16-row tile and
-// one k step is 1 KB contiguous, like the packed weights.
-__device__ __forceinline__ size_t xpack_index(int m, int k, int K) {
-  return ((size_t)((m >> 4) * (K >> 5) + (k >> 5)) * 64 + (m & 15) + 16 * ((k & 31) >> 3)) * 8 + (k & 7);
-}
+// Packed activations (XP): xpack_index (re_device.h).
 
 // Waves of a workgroup split K (KSPLIT: qkv, o and down, whose few column
 // strips would not fill the chip otherwise) or N (gate/up and the LM head:
@@ -763,7 +758,7 @@ hipError_t mfma_pack_matrix(const void* src, void* dst, int rows, int K, int qkv
 
 hipError_t prepare_mfma() {
   hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>();
-  if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves), false>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves), true>();
   if (e == hipSuccess) e = mgemv_prepare<2, kGuWaves, kMfGateUp, kHidAll, true>();
   if (e == hipSuccess) e = mgemv_prepare<1, kDownWaves, kMfResid, kInterSteps, true>();
   if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidAll, true>();
@@ -773,7 +768,7 @@ hipError_t prepare_mfma() {
   if (e == hipSuccess)
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_gu_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLcLds));
-  if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kHidSteps(kOWaves), false>();
+  if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kHidSteps(kOWaves), true>();
   if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kInterSteps, true>();
   return e;
 }
@@ -843,16 +838,17 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>(a, d.qkv_rows() / 16, stream);
       break;
     case MfmaOp::kO:
+      // the attention writes its output packed on this path (AttnArgs::packed_out)
       a.x = static_cast<const bf16_t*>(sc.attn);
       a.p0 = pk(po.o);
       a.K = d.q_dim();
       a.hidden = static_cast<bf16_t*>(sc.hidden);
       if (env.plan.mf_split) {
         a.part = sc.mf_part;
-        mgemv_launch<1, kPartWaves, kMfPart, kHidSteps(kOWaves), false>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges),
-                                                                         stream);
+        mgemv_launch<1, kPartWaves, kMfPart, kHidSteps(kOWaves), true>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges),
+                                                                        stream);
       } else {
-        mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves), false>(a, d.hidden / 16, stream);
+        mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves), true>(a, d.hidden / 16, stream);
       }
       break;
     case MfmaOp::kGateUp:

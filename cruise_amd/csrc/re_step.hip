@@ -692,6 +692,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     at.slots = d.slots();
     at.bs_shift = (d.block_size & (d.block_size - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(d.block_size)) : -1;
     at.grouped = p.grouped_attn;
+    at.packed_out = p.mfma;  // the matrix-core o-projection reads its input packed
     if (want()) {
       const hipError_t err = launch_attention(at, d, stream);
       if (err != hipSuccess) return err;
