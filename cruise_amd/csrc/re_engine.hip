@@ -318,6 +318,8 @@ bool make_plan(Engine& e, const Json& cfg) {
   p.lm_cu = 0;
   p.mf_split = 0;
   p.gu_cu = 0;
+  p.part_cu = 0;
+  p.qkv_split = 0;
   if (mfma_step_supported(d) && (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
     p.mfma = 1;
     p.lm_wg = mfma_lm_partials(d);
@@ -327,6 +329,11 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.mf_split = mfma_split_fits(d) && (tune == nullptr || tune->number_or("mf_split", 1) != 0) ? 1 : 0;
     // "tuning": {"gu_cu": 0} keeps gate/up as 4-wave workgroups
     p.gu_cu = mfma_gu_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("gu_cu", 1) != 0) ? e.cus : 0;
+    // "tuning": {"part_cu": 0} keeps the split o and down projections' waves
+    // fetching their activation fragments each on its own
+    p.part_cu = p.mf_split && (tune == nullptr || tune->number_or("part_cu", 1) != 0) ? 1 : 0;
+    // "tuning": {"qkv_split": 0} keeps qkv as one workgroup per strip
+    p.qkv_split = p.part_cu && mfma_qkv_split_fits(d) && (tune == nullptr || tune->number_or("qkv_split", 1) != 0) ? 1 : 0;
   }
   // the 4-wave matrix-core LM head folds its partials to one per row itself;
   // the per-CU one leaves one per CU
@@ -1720,6 +1727,8 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"lm_cu", e->plan.lm_cu},
       {"mf_split", e->plan.mf_split},
       {"gu_cu", e->plan.gu_cu},
+      {"part_cu", e->plan.part_cu},
+      {"qkv_split", e->plan.qkv_split},
       {"grouped_attention", e->plan.grouped_attn},
       {"argmax_parts", e->plan.argmax_parts},
       {"o_grid", e->plan.o_grid},

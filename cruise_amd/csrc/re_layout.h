@@ -162,6 +162,8 @@ struct LaunchPlan {
   int mf_split;
   // > 0 (with mfma): gate/up runs one workgroup per CU (k_mf_gu_cu), this grid
   int gu_cu;
+  int part_cu;     // 64-row o and down splits with their activations staged in LDS (re_mfma.hip k_mf_part_cu)
+  int qkv_split;   // 64-row qkv split over (9-strip group, K range), epilogue in k_mf_qkv_finish
   // 1: decode attention per (row, KV head) for all query heads of the group
   int grouped_attn;
 };
@@ -230,6 +232,7 @@ bool mfma_lm_cu_fits(const Dims& d, int cus);
 bool mfma_split_fits(const Dims& d);
 bool mfma_gu_cu_fits(const Dims& d, int cus);
 size_t mfma_split_partial_bytes(const Dims& d);
+bool mfma_qkv_split_fits(const Dims& d);
 hipError_t prepare_mfma();
 // Layout of the packed copy; returns its bytes.
 size_t mfma_packed_layout(const Dims& d, PackedOffsets* layers, size_t* lm_off);

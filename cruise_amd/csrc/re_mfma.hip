@@ -25,6 +25,8 @@
 //
 // The RMSNorm before qkv, gate/up and the LM head runs as its own kernel
 // (one workgroup per row) into a normalized copy of the rows.
+#include <type_traits>
+
 #include "re_device.h"
 #include "re_layout.h"
 
@@ -545,6 +547,177 @@ __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_gu_cu(MfArgs a) {
     }
 }
 
+// o, down and qkv split over (strip group, K range) with the range's
+// activations staged in LDS: k_mgemv<..., kMfPart, ...> lets each of its
+// waves fetch the range's fragments (4 tiles x 1 KB per k step) on its own;
+// here the waves copy them to LDS together (global -> LDS, one 1 KB fragment
+// per instruction), in blocks of BLK steps through two buffers, and each wave
+// reads them from LDS while it streams its strip's weights with kRing steps
+// in flight.  Every count is known at compile time, so each wait is exact.
+// Each strip is k_mgemv's chain of MFMA steps in the same order, so the
+// partials are the same bits.  QKV: the partial of column c of strip g goes
+// to qkv row qkv_strip_row(g, c) (N = the qkv rows, k_mf_qkv_finish adds
+// them up); otherwise to column 16 g + c (N = hidden, the next norm adds them).
+template <int STEPS, int BLK>
+constexpr int part_block_steps(int b) {
+  return STEPS - b * BLK < BLK ? STEPS - b * BLK : BLK;
+}
+template <int STEPS, int BLK, int WAVES>
+constexpr int part_block_copies(int b) {  // per wave
+  return (kMfTiles * part_block_steps<STEPS, BLK>(b) + WAVES - 1) / WAVES;
+}
+template <int STEPS, int BLK>
+constexpr int part_block_refills(int b) {  // weight loads issued during block b
+  int n = 0;
+  for (int s = b * BLK; s < b * BLK + part_block_steps<STEPS, BLK>(b); ++s) n += s + kRing < STEPS ? 1 : 0;
+  return n;
+}
+template <int STEPS, int BLK>
+constexpr size_t part_cu_lds() {
+  return (size_t)(STEPS > BLK ? 2 : 1) * kMfTiles * BLK * 1024;
+}
+
+template <int STEPS, int WAVES, int BLK, bool QKV>
+__global__ void __launch_bounds__(WAVES * 64) k_mf_part_cu(MfArgs a) {
+  extern __shared__ __align__(16) unsigned char pc_smem[];  // [2][kMfTiles][BLK] fragments of 1 KB
+  constexpr int NB = (STEPS + BLK - 1) / BLK;
+  constexpr int R = kRing < STEPS ? kRing : STEPS;
+  constexpr int kBuf = kMfTiles * BLK * 1024;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int c = lane & 15;
+  const int g = blockIdx.x * WAVES + wave;  // this wave's strip
+  const int kstep0 = blockIdx.y * STEPS;
+  const int ksteps = a.K / kMfK;
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  if (stop != 0) return;  // uniform
+  // block b's fragment f = t * steps + s (tile t, step s of the block) by
+  // wave f % WAVES; a wave past the end copies the last one again
+  auto stage = [&](auto bc) {
+    constexpr int b = decltype(bc)::value;
+    constexpr int ns = part_block_steps<STEPS, BLK>(b);
+    constexpr int nf = kMfTiles * ns;
+    unsigned char* dst = pc_smem + (b & 1) * kBuf;
+#pragma unroll
+    for (int i = 0; i < part_block_copies<STEPS, BLK, WAVES>(b); ++i) {
+      const int f = min(wave + i * WAVES, nf - 1);
+      const int t = f / ns, sl = f - t * ns;
+      __builtin_amdgcn_global_load_lds((lc_gptr)(a.x + ((size_t)t * ksteps + kstep0 + b * BLK + sl) * 512 + lane * 8),
+                                       (lc_lptr)(dst + (t * BLK + sl) * 1024), 16, 0, 0);
+    }
+  };
+  const bf16_t* wp = a.p0 + ((size_t)g * ksteps + kstep0) * 512 + lane * 8;
+  re_u32x4 wr[R];
+  stage(std::integral_constant<int, 0>{});
+#pragma unroll
+  for (int s = 0; s < R; ++s) wr[s] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp + s * 512));
+  int pending = R;  // loads issued after the block now awaited (compile-time after unrolling)
+  if constexpr (NB > 1) {
+    stage(std::integral_constant<int, 1>{});
+    pending += part_block_copies<STEPS, BLK, WAVES>(1);
+  }
+  // block 0 is in LDS: this wave's copies first, then everyone's
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(lc_wait(R + (NB > 1 ? part_block_copies<STEPS, BLK, WAVES>(1) : 0)));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  (void)pending;
+  mf_f32x4 acc[kMfTiles];
+#pragma unroll
+  for (int t = 0; t < kMfTiles; ++t) acc[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto block = [&](auto bc) {
+    constexpr int b = decltype(bc)::value;
+    constexpr int ns = part_block_steps<STEPS, BLK>(b);
+    const unsigned char* xb = pc_smem + (b & 1) * kBuf + lane * 16;
+#pragma unroll
+    for (int sl = 0; sl < ns; ++sl) {
+      const int s = b * BLK + sl;
+      mf_bf16x8 xf[kMfTiles];
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t) xf[t] = *reinterpret_cast<const mf_bf16x8*>(xb + (t * BLK + sl) * 1024);
+#pragma unroll
+      for (int t = 0; t < kMfTiles; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[t], __builtin_bit_cast(mf_bf16x8, wr[s % R]), acc[t], 0, 0, 0);
+      if (s + R < STEPS) wr[s % R] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp + (s + R) * 512));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (b + 1 < NB) {
+      // block b + 1 landed (only this block's refills may still be in flight),
+      // and every wave is done with buffer b & 1; then block b + 2 goes there
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(lc_wait(part_block_refills<STEPS, BLK>(b)));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if constexpr (b + 2 < NB) stage(std::integral_constant<int, b + 2>{});
+    }
+  };
+  static_assert(NB <= 6, "at most six staged blocks");
+  block(std::integral_constant<int, 0>{});
+  if constexpr (NB > 1) block(std::integral_constant<int, 1>{});
+  if constexpr (NB > 2) block(std::integral_constant<int, 2>{});
+  if constexpr (NB > 3) block(std::integral_constant<int, 3>{});
+  if constexpr (NB > 4) block(std::integral_constant<int, 4>{});
+  if constexpr (NB > 5) block(std::integral_constant<int, 5>{});
+  const int mrow = 4 * (lane >> 4);
+  const int n = QKV ? qkv_strip_row(a.head_dim, g, c) : g * 16 + c;
+  float* part = a.part + (size_t)blockIdx.y * a.B * a.hidden_dim;
+#pragma unroll
+  for (int t = 0; t < kMfTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = t * 16 + mrow + v;
+      if (m < a.B) part[(size_t)m * a.hidden_dim + n] = acc[t][v];
+    }
+}
+
+// The qkv epilogue after k_mf_part_cu: the 8 K-range partials added in range
+// order (the order k_mgemv's wave 0 adds its waves' sums), then bias, RoPE
+// and the q / paged K/V writes exactly as k_mgemv<..., kMfQkv, ...> does them.
+// Thread: one (row, head, pair j < d/2), both elements of the RoPE pair.
+__global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a, int ranges) {
+  const int half = a.head_dim >> 1;
+  const int nheads = a.hidden_dim / a.head_dim;  // q, k and v heads
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.B * nheads * half) return;
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  if (stop != 0) return;
+  const int m = idx / (nheads * half), rem = idx - m * nheads * half;
+  const int head = rem / half, j = rem - head * half;
+  const int r0 = head * a.head_dim + j, r1 = r0 + half;
+  const size_t plane = (size_t)a.B * a.hidden_dim;
+  const float* p = a.part + (size_t)m * a.hidden_dim;
+  float s0 = p[r0], s1 = p[r1];
+  for (int r = 1; r < ranges; ++r) {
+    s0 += p[r * plane + r0];
+    s1 += p[r * plane + r1];
+  }
+  // F.linear with bias: fp32 sum + bias, one rounding (g4a_linear_t_bias.py:18-21)
+  const float y0 = Elt<bf16_t>::r(s0 + Elt<bf16_t>::f(a.w1[r0]));
+  const float y1 = Elt<bf16_t>::r(s1 + Elt<bf16_t>::f(a.w1[r1]));
+  float o0 = y0, o1 = y1;
+  if (head < a.heads + a.kv_heads) {
+    // q' = q*cos + rotate_half(q)*sin, each product and the sum rounded
+    // (batched_decoder_step.py:231-240, 323-324)
+    const float cs = a.rope[((size_t)m * half + j) * 2], sn = a.rope[((size_t)m * half + j) * 2 + 1];
+    o0 = Elt<bf16_t>::r(Elt<bf16_t>::r(y0 * cs) + Elt<bf16_t>::r(-y1 * sn));
+    o1 = Elt<bf16_t>::r(Elt<bf16_t>::r(y1 * cs) + Elt<bf16_t>::r(y0 * sn));
+  }
+  if (head < a.heads) {
+    bf16_t* q = a.q + ((size_t)m * a.heads + head) * a.head_dim;
+    q[j] = Elt<bf16_t>::t(o0);
+    q[j + half] = Elt<bf16_t>::t(o1);
+  } else {
+    // paged slot write, active rows only (batched_decoder_step.py:250-264)
+    const int sl = a.slot[m];
+    if (a.active[m] != 0 && sl >= 0 && sl < a.slots) {
+      const bool is_key = head < a.heads + a.kv_heads;
+      const int kvh = is_key ? head - a.heads : head - a.heads - a.kv_heads;
+      bf16_t* cache = (is_key ? a.key_cache : a.value_cache) + ((size_t)sl * a.kv_heads + kvh) * a.head_dim;
+      cache[j] = Elt<bf16_t>::t(o0);
+      cache[j + half] = Elt<bf16_t>::t(o1);
+    }
+  }
+}
+
 template <int NS, int WAVES, int KIND>
 constexpr size_t mgemv_lds() {
   return k_split<KIND>() ? (size_t)(WAVES - 1) * NS * kMfTiles * 4 * 64 * sizeof(float) : 0;
@@ -690,6 +863,10 @@ constexpr int kHidAll = kMfHidden / kMfK;  // the whole K of the N-split project
 constexpr int kInterSteps = kMfInter / kMfK / kDownWaves;
 // split o / down: 7 strips (one per wave) by the 8 K ranges of the kernels above
 constexpr int kPartWaves = 7, kPartRanges = 8;
+// the staged split kernels: o and qkv stage their 14-step K range at once,
+// down its 74 steps in blocks of 16
+constexpr int kQkvPartWaves = 9;  // qkv strips per workgroup: 288 = 32 x 9
+constexpr int kDownBlk = 16;
 static_assert(kOWaves == kPartRanges && kDownWaves == kPartRanges, "split ranges follow the K-split waves");
 
 template <int NS, int WAVES, int KIND, int STEPS, bool XP>
@@ -721,7 +898,12 @@ bool mfma_gu_cu_fits(const Dims& d, int cus) {
 }
 
 bool mfma_split_fits(const Dims& d) { return mfma_step_supported(d) && (d.hidden / 16) % kPartWaves == 0; }
-size_t mfma_split_partial_bytes(const Dims& d) { return (size_t)kPartRanges * d.batch * d.hidden * sizeof(float); }
+bool mfma_qkv_split_fits(const Dims& d) {
+  return mfma_split_fits(d) && (d.qkv_rows() / 16) % kQkvPartWaves == 0 && d.q_dim() == d.hidden;
+}
+size_t mfma_split_partial_bytes(const Dims& d) {
+  return (size_t)kPartRanges * d.batch * std::max(d.hidden, d.qkv_rows()) * sizeof(float);
+}
 
 // The per-CU LM head needs 8 to 40 strips per workgroup and whole LDS blocks.
 bool mfma_lm_cu_fits(const Dims& d, int cus) {
@@ -756,6 +938,16 @@ hipError_t mfma_pack_matrix(const void* src, void* dst, int rows, int K, int qkv
   return hipGetLastError();
 }
 
+template <int STEPS, int WAVES, int BLK, bool QKV>
+static hipError_t part_cu_prepare() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_part_cu<STEPS, WAVES, BLK, QKV>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(part_cu_lds<STEPS, BLK>()));
+}
+template <int STEPS, int WAVES, int BLK, bool QKV>
+static void part_cu_launch(const MfArgs& a, int groups, hipStream_t stream) {
+  k_mf_part_cu<STEPS, WAVES, BLK, QKV><<<dim3(groups, kPartRanges), WAVES * 64, part_cu_lds<STEPS, BLK>(), stream>>>(a);
+}
+
 hipError_t prepare_mfma() {
   hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>();
   if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves), true>();
@@ -770,6 +962,9 @@ hipError_t prepare_mfma() {
                             static_cast<int>(kLcLds));
   if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kHidSteps(kOWaves), true>();
   if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kInterSteps, true>();
+  if (e == hipSuccess) e = part_cu_prepare<kHidSteps(kOWaves), kPartWaves, kHidSteps(kOWaves), false>();
+  if (e == hipSuccess) e = part_cu_prepare<kInterSteps, kPartWaves, kDownBlk, false>();
+  if (e == hipSuccess) e = part_cu_prepare<kHidSteps(kOWaves), kQkvPartWaves, kHidSteps(kOWaves), true>();
   return e;
 }
 
@@ -835,7 +1030,17 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.heads = d.heads;
       a.kv_heads = d.kv_heads;
       a.head_dim = d.head_dim;
-      mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>(a, d.qkv_rows() / 16, stream);
+      if (env.plan.qkv_split) {
+        // 8 K-range partials per qkv row, then the epilogue in k_mf_qkv_finish
+        a.part = sc.mf_part;
+        a.hidden_dim = d.qkv_rows();
+        part_cu_launch<kHidSteps(kOWaves), kQkvPartWaves, kHidSteps(kOWaves), true>(a, d.qkv_rows() / 16 / kQkvPartWaves,
+                                                                                   stream);
+        const int threads = d.batch * (d.qkv_rows() / d.head_dim) * (d.head_dim / 2);
+        k_mf_qkv_finish<<<(threads + 255) / 256, 256, 0, stream>>>(a, kPartRanges);
+      } else {
+        mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>(a, d.qkv_rows() / 16, stream);
+      }
       break;
     case MfmaOp::kO:
       // the attention writes its output packed on this path (AttnArgs::packed_out)
@@ -843,7 +1048,10 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.p0 = pk(po.o);
       a.K = d.q_dim();
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      if (env.plan.mf_split) {
+      if (env.plan.mf_split && env.plan.part_cu) {
+        a.part = sc.mf_part;
+        part_cu_launch<kHidSteps(kOWaves), kPartWaves, kHidSteps(kOWaves), false>(a, d.hidden / 16 / kPartWaves, stream);
+      } else if (env.plan.mf_split) {
         a.part = sc.mf_part;
         mgemv_launch<1, kPartWaves, kMfPart, kHidSteps(kOWaves), true>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges),
                                                                         stream);
@@ -869,7 +1077,10 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.p0 = pk(po.down);
       a.K = d.intermediate;
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      if (env.plan.mf_split) {
+      if (env.plan.mf_split && env.plan.part_cu) {
+        a.part = sc.mf_part;
+        part_cu_launch<kInterSteps, kPartWaves, kDownBlk, false>(a, d.hidden / 16 / kPartWaves, stream);
+      } else if (env.plan.mf_split) {
         a.part = sc.mf_part;
         mgemv_launch<1, kPartWaves, kMfPart, kInterSteps, true>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges), stream);
       } else {

@@ -14,6 +14,13 @@ and cache writes exactly.
 - {"gu_cu": 0}: gate/up as 4-wave workgroups (each wave one strip of gate
   and up over the whole K) instead of one workgroup per CU whose waves run
   the same strips' step chains over LDS-staged activations.
+- {"part_cu": 0}: the split o and down projections with every wave fetching
+  its K range's activation fragments itself, instead of the workgroup staging
+  them once in LDS: the same step chains (and qkv as in {"qkv_split": 0}).
+- {"qkv_split": 0}: qkv as one workgroup per strip whose 8 waves split K and
+  add their sums in wave order, instead of the split over (9-strip group, K
+  range) whose 8 partials k_mf_qkv_finish adds in range order before the
+  bias, RoPE and paged writes: the same sums in the same order.
 
 The engine allows one instance per process, so the runtimes run one after
 the other."""
@@ -44,7 +51,7 @@ def step_once(weights, tuning, inputs):
     tok, pos, length, slot, active, table, key, value = inputs
     rt = make_runtime(W, weights, tuning=tuning)
     try:
-        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units", "mf_split", "gu_cu")}
+        facts = {k: rt.info(k) for k in ("lm_cu", "argmax_parts", "compute_units", "mf_split", "gu_cu", "part_cu", "qkv_split")}
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -55,7 +62,11 @@ def step_once(weights, tuning, inputs):
         rt.close()
 
 
-@pytest.mark.parametrize("tuning", [{"lm_cu": 0}, {"mf_split": 0}, {"gu_cu": 0}], ids=["lm_cu0", "mf_split0", "gu_cu0"])
+@pytest.mark.parametrize(
+    "tuning",
+    [{"lm_cu": 0}, {"mf_split": 0}, {"gu_cu": 0}, {"part_cu": 0}, {"qkv_split": 0}],
+    ids=["lm_cu0", "mf_split0", "gu_cu0", "part_cu0", "qkv_split0"],
+)
 def test_matrix_core_plan_variants_match_bit_for_bit(weights_dev, tuning):
     rng = np.random.default_rng(6402)
     table = random_tables(rng, B, BPR, W.geometry.physical_blocks)
@@ -71,10 +82,15 @@ def test_matrix_core_plan_variants_match_bit_for_bit(weights_dev, tuning):
     facts, got = step_once(weights_dev, tuning, inputs)
     assert base_facts["lm_cu"] == 1 and base_facts["argmax_parts"] == base_facts["compute_units"]
     assert base_facts["mf_split"] == 1 and base_facts["gu_cu"] == base_facts["compute_units"]
+    assert base_facts["part_cu"] == 1 and base_facts["qkv_split"] == 1
     if "lm_cu" in tuning:
         assert facts["lm_cu"] == 0 and facts["argmax_parts"] == 1
     elif "mf_split" in tuning:
-        assert facts["mf_split"] == 0
+        assert facts["mf_split"] == 0 and facts["part_cu"] == 0 and facts["qkv_split"] == 0
+    elif "part_cu" in tuning:
+        assert facts["part_cu"] == 0 and facts["mf_split"] == 1 and facts["qkv_split"] == 0
+    elif "qkv_split" in tuning:
+        assert facts["qkv_split"] == 0 and facts["part_cu"] == 1
     else:
         assert facts["gu_cu"] == 0
     for name, a, b in zip(("logits", "next", "key", "value"), base, got):
