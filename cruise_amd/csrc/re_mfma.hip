@@ -673,7 +673,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_mf_part_cu(MfArgs a) {
 // order (the order k_mgemv's wave 0 adds its waves' sums), then bias, RoPE
 // and the q / paged K/V writes exactly as k_mgemv<..., kMfQkv, ...> does them.
 // Thread: one (row, head, pair j < d/2), both elements of the RoPE pair.
-__global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a, int ranges) {
+template <int RANGES>
+__global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a) {
   const int half = a.head_dim >> 1;
   const int nheads = a.hidden_dim / a.head_dim;  // q, k and v heads
   const int idx = blockIdx.x * 256 + threadIdx.x;
@@ -685,10 +686,17 @@ __global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a, int ranges) {
   const int r0 = head * a.head_dim + j, r1 = r0 + half;
   const size_t plane = (size_t)a.B * a.hidden_dim;
   const float* p = a.part + (size_t)m * a.hidden_dim;
-  float s0 = p[r0], s1 = p[r1];
-  for (int r = 1; r < ranges; ++r) {
-    s0 += p[r * plane + r0];
-    s1 += p[r * plane + r1];
+  float v0[RANGES], v1[RANGES];  // every partial requested before the first add
+#pragma unroll
+  for (int r = 0; r < RANGES; ++r) {
+    v0[r] = p[r * plane + r0];
+    v1[r] = p[r * plane + r1];
+  }
+  float s0 = v0[0], s1 = v1[0];
+#pragma unroll
+  for (int r = 1; r < RANGES; ++r) {
+    s0 += v0[r];
+    s1 += v1[r];
   }
   // F.linear with bias: fp32 sum + bias, one rounding (g4a_linear_t_bias.py:18-21)
   const float y0 = Elt<bf16_t>::r(s0 + Elt<bf16_t>::f(a.w1[r0]));
@@ -1037,7 +1045,7 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
         part_cu_launch<kHidSteps(kOWaves), kQkvPartWaves, kHidSteps(kOWaves), true>(a, d.qkv_rows() / 16 / kQkvPartWaves,
                                                                                    stream);
         const int threads = d.batch * (d.qkv_rows() / d.head_dim) * (d.head_dim / 2);
-        k_mf_qkv_finish<<<(threads + 255) / 256, 256, 0, stream>>>(a, kPartRanges);
+        k_mf_qkv_finish<kPartRanges><<<(threads + 255) / 256, 256, 0, stream>>>(a);
       } else {
         mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>(a, d.qkv_rows() / 16, stream);
       }
