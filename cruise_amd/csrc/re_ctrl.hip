@@ -37,6 +37,17 @@ __device__ __forceinline__ int compute_slot(const int32_t* table, const CtrlArgs
   return physical * a.block_size + offset;
 }
 
+// compute_slot with the block-table entry already read (physical: the entry
+// of the position's logical block, clamped into the row).
+__device__ __forceinline__ int slot_of_physical(int physical, const CtrlArgs& a, int request, long long position) {
+  if (request < 0 || request >= a.B || position < 0 || position >= a.capacity) return -1;
+  const int logical = static_cast<int>(position / a.block_size);
+  const int offset = static_cast<int>(position % a.block_size);
+  if (logical >= a.bpr) return -1;
+  if (physical < 0 || physical >= a.physical_blocks) return -1;
+  return physical * a.block_size + offset;
+}
+
 struct FeedView {
   const int64_t* token;
   const int64_t* pos;
@@ -297,49 +308,120 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   __shared__ int bad_s[256];
   __shared__ int fail_at, active_count;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  // The state of row r = tid the update below reads, requested first so it
+  // arrives while the partials are merged (clamped: threads past B ignore it).
+  const int rq = min(tid, B - 1);
+  const int32_t act_r = s.cur_active[rq];
+  const int64_t pos_r = s.cur_pos[rq];
+  const int64_t eos_r = s.eos[rq];
+  const int32_t exec_r = s.executed[rq];
+  // the block-table entry of the next position (compute_slot's lookup)
+  const int64_t np_r = pos_r + 1;
+  const int lg_r = static_cast<int>(min(max(np_r, (int64_t)0), (int64_t)a.capacity) / a.block_size);
+  const int32_t phys_r = s.table[rq * a.bpr + min(lg_r, a.bpr - 1)];
   // Final argmax over the LM head's workgroup partials (CTRL:99-119): one wave
   // per batch row; each lane requests its strided share of the partials at
   // once (clamped, ignored past the count), then a shuffle reduction keeps the
-  // first index of the maximum; any non-finite logit flags the row.
-  constexpr int kUnroll = 16;
-  for (int b = wave; b < B; b += nwaves) {
-    float bv = 0.f;
-    int bi = -1, bb = 0;
-    for (int w0 = 0; w0 < a.lm_wg; w0 += 64 * kUnroll) {
-      float v[kUnroll];
-      int ix[kUnroll], fl[kUnroll];
+  // first index of the maximum; any non-finite logit flags the row.  Up to 256
+  // partials per row (one per CU): a wave takes four rows at once, four
+  // partials per lane each, so every request of the pass is in flight
+  // together.
+  auto better = [](float ov, int oi, float bv, int bi) {
+    return oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi));
+  };
+  constexpr int kRows = 4, kPer = 4;
+  if (a.lm_wg <= 64 * kPer) {
+    for (int b0 = wave; b0 < B; b0 += nwaves * kRows) {
+      float v[kRows][kPer];
+      int ix[kRows][kPer], fl[kRows][kPer];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int p = min(w0 + lane + 64 * u, a.lm_wg - 1);
-        const size_t o = a.am_row_major ? (size_t)b * a.lm_wg + p : (size_t)p * B + b;
-        v[u] = a.am_val[o];
-        ix[u] = a.am_idx[o];
-        fl[u] = a.am_bad[o];
-      }
+      for (int i = 0; i < kRows; ++i)
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (w0 + lane + 64 * u >= a.lm_wg) continue;
-        bb |= fl[u];
-        if (ix[u] < 0) continue;
-        if (bi < 0 || v[u] > bv || (v[u] == bv && ix[u] < bi)) {
-          bv = v[u];
-          bi = ix[u];
+        for (int j = 0; j < kPer; ++j) {
+          const int b = min(b0 + i * nwaves, B - 1);
+          const int p = min(lane + 64 * j, a.lm_wg - 1);
+          const size_t o = a.am_row_major ? (size_t)b * a.lm_wg + p : (size_t)p * B + b;
+          v[i][j] = a.am_val[o];
+          ix[i][j] = a.am_idx[o];
+          fl[i][j] = a.am_bad[o];
+        }
+      float bv[kRows];
+      int bi[kRows], bb[kRows];
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        bv[i] = 0.f;
+        bi[i] = -1;
+        bb[i] = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+          if (lane + 64 * j >= a.lm_wg) continue;
+          bb[i] |= fl[i][j];
+          if (better(v[i][j], ix[i][j], bv[i], bi[i])) {
+            bv[i] = v[i][j];
+            bi[i] = ix[i][j];
+          }
         }
       }
-    }
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
-      bb |= __shfl_xor(bb, m, 64);
-      if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-        bv = ov;
-        bi = oi;
-      }
+      for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) {
+          const float ov = __shfl_xor(bv[i], m, 64);
+          const int oi = __shfl_xor(bi[i], m, 64);
+          bb[i] |= __shfl_xor(bb[i], m, 64);
+          if (better(ov, oi, bv[i], bi[i])) {
+            bv[i] = ov;
+            bi[i] = oi;
+          }
+        }
+      if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < kRows; ++i)
+          if (b0 + i * nwaves < B) {
+            tok_s[b0 + i * nwaves] = bi[i];
+            bad_s[b0 + i * nwaves] = bb[i];
+          }
     }
-    if (lane == 0) {
-      tok_s[b] = bi;
-      bad_s[b] = bb;
+  } else {
+    constexpr int kUnroll = 16;
+    for (int b = wave; b < B; b += nwaves) {
+      float bv = 0.f;
+      int bi = -1, bb = 0;
+      for (int w0 = 0; w0 < a.lm_wg; w0 += 64 * kUnroll) {
+        float v[kUnroll];
+        int ix[kUnroll], fl[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int p = min(w0 + lane + 64 * u, a.lm_wg - 1);
+          const size_t o = a.am_row_major ? (size_t)b * a.lm_wg + p : (size_t)p * B + b;
+          v[u] = a.am_val[o];
+          ix[u] = a.am_idx[o];
+          fl[u] = a.am_bad[o];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          if (w0 + lane + 64 * u >= a.lm_wg) continue;
+          bb |= fl[u];
+          if (better(v[u], ix[u], bv, bi)) {
+            bv = v[u];
+            bi = ix[u];
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(bv, m, 64);
+        const int oi = __shfl_xor(bi, m, 64);
+        bb |= __shfl_xor(bb, m, 64);
+        if (better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) {
+        tok_s[b] = bi;
+        bad_s[b] = bb;
+      }
     }
   }
   if (tid == 0) {
@@ -357,15 +439,15 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   // updated in full, as the sequential loop does before it stops.
   // B <= 256 < blockDim.x: thread r owns row r.
   const int r = tid;
-  const bool live = r < B && s.cur_active[r] != 0;
+  const bool live = r < B && act_r != 0;
   int32_t code = kStatusOk;
   int slot_next = -1;
   if (live) {
-    const int64_t next_pos = s.cur_pos[r] + 1;
+    const int64_t next_pos = np_r;
     if (bad_s[r] != 0 || tok_s[r] < 0) {
       code = kStatusNonFiniteLogits;
     } else if (next_pos != a.capacity) {
-      slot_next = compute_slot(s.table, a, r, next_pos);
+      slot_next = slot_of_physical(phys_r, a, r, next_pos);  // compute_slot with the entry requested above
       if (slot_next < 0) code = kStatusCapacityExceeded;
     }
     if (code != kStatusOk) atomicMin(&fail_at, fail_key(r, code));
@@ -374,15 +456,15 @@ __global__ void __launch_bounds__(1024) k_ctrl_step(CtrlArgs a) {
   const int first = fail_row(fail_at);  // uniform
   if (live && (r < first || (r == first && code == kStatusCapacityExceeded))) {
     const int64_t tok = tok_s[r];
-    const int64_t next_pos = s.cur_pos[r] + 1;
+    const int64_t next_pos = np_r;
     history[(call - 1) * B + r] = tok;
-    s.executed[r] += 1;
+    s.executed[r] = exec_r + 1;
     s.cur_pos[r] = next_pos;
     s.cur_token[r] = tok;
     s.cur_len[r] = static_cast<int32_t>(next_pos + 1);
     if (r < first) {
       s.cur_slot[r] = slot_next;  // -1 at the capacity
-      if (tok == s.eos[r]) {
+      if (tok == eos_r) {
         s.cur_active[r] = 0;
         s.reason[r] = kFinishEos;
       } else {
