@@ -421,12 +421,14 @@ __global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
 // Down projection with the whole K in one workgroup (bf16, B <= 4):
 // h = T(h + T(x W^T)) (batched_decoder_step.py:399-403) with no fp32
 // partials in global memory and no reduce launch.  One workgroup of 16 waves
-// per CU; workgroup g owns the row pairs [g*ppw, (g+1)*ppw).  The activations
-// x [B, K] are staged into LDS once (4 x 18944 bf16 = 148 KB at Qwen2.5-7B's
-// shape: gfx950 gives a workgroup up to 160 KB).  For one row pair, wave w
-// covers elements [w*K/16, (w+1)*K/16) of both rows in up to three 512-element
-// loads per row; each lane dots its elements against the B rows and the
-// lanes of a wave are combined by the halving exchange into LDS.  After the
+// per CU; workgroup g owns the row pairs [g*ppw, (g+1)*ppw).  For one row
+// pair, wave w covers elements [w*K/16, (w+1)*K/16) of both rows in up to
+// three 512-element loads per row; each lane dots its elements against the B
+// rows and the lanes of a wave are combined by the halving exchange into LDS.
+// A lane only ever needs its own elements of the activations x [B, K], so it
+// requests them once and keeps them for every pair (the first two chunks in
+// registers, the third in its own LDS slot): no workgroup-wide staging of the
+// 148 KB of x and no barrier before the first products.  After the
 // last pair, one thread per output adds the 16 wave totals in wave order and
 // the residual -- a fixed order, so the results do not depend on timing.
 // The next pair's weights are in flight while a pair is computed (two
@@ -436,7 +438,6 @@ __global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kWholeWaves = 16;
 constexpr int kWholeLoads = 3;   // loads per row and wave: K <= 16 * 3 * 512
-constexpr int kWholeStage = 10;  // staged activation vectors per thread: B*K <= 4 * 20480
 
 struct DownWholeArgs {
   const int32_t* done;
@@ -464,8 +465,7 @@ __device__ __forceinline__ void whole_issue(Vec8<bf16_t> (&w)[kWholeLoads][2], c
 __global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int MB = 4;
-  bf16_t* xs = reinterpret_cast<bf16_t*>(smem_raw);  // [MB][K]
-  float* red = reinterpret_cast<float*>(smem_raw + (size_t)MB * a.K * sizeof(bf16_t));  // [ppw][16][8]
+  float* red = reinterpret_cast<float*>(smem_raw);  // [ppw][16][8] wave totals
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
   const int K = a.K, span = K / kWholeWaves, k_lo = wave * span;
   const int units = a.N / 2;
@@ -478,31 +478,36 @@ __global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArg
 
   // Issue order: the flag, the residual values of this workgroup's outputs
   // (thread t < 8 x pairs: pair t/8, row (t/4)&1 of the pair, batch row t&3),
-  // the activations, then the first two pairs' weights.
+  // this wave's slice of the activations, then the first two pairs' weights.
+  // A wave only ever reads its own K range of the MB rows (elements k_lo +
+  // 512 j + 8 lane), so it keeps that slice in registers for every pair: no
+  // LDS staging and no workgroup barrier before the first products.  Loads
+  // past the range or the batch are clamped to valid addresses; their
+  // products are skipped or never stored.
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
   const int nout = (u_end - u_begin) * 8;
   const int ot = min(tid, nout - 1);
   const int o_u = u_begin + ot / 8, o_r = (ot >> 2) & 1, o_m = ot & 3;
   const bf16_t h = Hd[(size_t)min(o_m, a.B - 1) * a.N + 2 * o_u + o_r];
-  const int per_row = K / 8, nvec = MB * per_row;
-  Vec8<bf16_t> xv[kWholeStage];
+  // The last chunk's values wait in this thread's own LDS slot (registers are
+  // full at 16 waves per CU); only the thread that wrote a slot reads it.
+  constexpr int kReg = kWholeLoads - 1;
+  Vec8<bf16_t>* xl = reinterpret_cast<Vec8<bf16_t>*>(smem_raw + (size_t)a.pairs_per_wg * kWholeWaves * 8 * sizeof(float)) +
+                     (size_t)tid * MB;
+  Vec8<bf16_t> xr[kWholeLoads][MB];
 #pragma unroll
-  for (int i = 0; i < kWholeStage; ++i) {
-    const int idx = min(tid + 1024 * i, nvec - 1);
-    const int m = idx / per_row;
-    xv[i] = Vec8<bf16_t>::load_cached(X + (size_t)min(m, a.B - 1) * K + (idx - m * per_row) * 8);
+  for (int j = 0; j < kWholeLoads; ++j) {
+    const int k = min(j * kChunk + lane * 8, span - 8);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) xr[j][m] = Vec8<bf16_t>::load_cached(X + (size_t)min(m, a.B - 1) * K + k_lo + k);
   }
   Vec8<bf16_t> wa[kWholeLoads][2], wb[kWholeLoads][2];
   whole_issue(wa, W, K, u_begin, u_end, k_lo, span, lane);
   whole_issue(wb, W, K, u_begin + 1, u_end, k_lo, span, lane);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < kWholeStage; ++i) {
-    const int idx = tid + 1024 * i;
-    if (idx < nvec) *reinterpret_cast<Vec8<bf16_t>*>(xs + idx * 8) = idx / per_row < a.B ? xv[i] : Vec8<bf16_t>{};
-  }
-  lds_barrier();
-  if (stop != 0) return;
+  for (int m = 0; m < MB; ++m) xl[m] = xr[kReg][m];
+  if (stop != 0) return;  // uniform over the workgroup
 
   // One pair: products over this wave's range, wave totals to LDS.
   auto pair = [&](Vec8<bf16_t>(&w)[kWholeLoads][2], int u) {
@@ -518,7 +523,7 @@ __global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArg
       if (k < span) {
 #pragma unroll
         for (int m = 0; m < MB; ++m) {
-          const Vec8<bf16_t> x = Vec8<bf16_t>::load_cached(xs + m * K + k_lo + k);
+          const Vec8<bf16_t> x = j < kReg ? xr[j][m] : xl[m];
 #pragma unroll
           for (int r = 0; r < 2; ++r) acc[r][m] = dot8(w[j][r], x, acc[r][m]);
         }
@@ -570,7 +575,8 @@ size_t normed_lds_bytes(int mb, int hidden, int dtype_bytes, int waves) {
   return (size_t)mb * hidden * dtype_bytes + (3 * (size_t)waves * kRowsPerWave + 4) * mb * sizeof(float);
 }
 size_t down_whole_lds_bytes(int K, int pairs_per_wg) {
-  return (size_t)4 * K * sizeof(bf16_t) + (size_t)pairs_per_wg * kWholeWaves * 8 * sizeof(float);
+  (void)K;  // wave totals, then each thread's slot for its last activation chunk
+  return (size_t)pairs_per_wg * kWholeWaves * 8 * sizeof(float) + (size_t)kWholeWaves * 64 * 4 * sizeof(Vec8<bf16_t>);
 }
 size_t resid_lds_bytes(int mb, int dtype_bytes, int waves) {
   return (size_t)mb * kSeg * dtype_bytes + (size_t)waves * mb * kRowsPerWave * sizeof(float);
