@@ -300,6 +300,8 @@ bool make_plan(Engine& e, const Json& cfg) {
         p.lm_grid = p.lm_grid_eq;
       }
     }
+    // "qkv_ksplit": 0 keeps qkv as one row pair per wave over the whole K
+    if (t->number_or("qkv_ksplit", 1) == 0) p.qkv_ksplit = 0;
     // "qkv_waves": 4 or 9 waves per qkv workgroup (one row pair per wave)
     const int qw = static_cast<int>(t->number_or("qkv_waves", p.qkv_waves));
     if ((qw == 4 || qw == 9) && qw != p.qkv_waves) {
@@ -1723,6 +1725,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"down_segments", e->plan.down_segments},
       {"down_whole_grid", e->plan.down_whole_grid},
       {"qkv_waves", e->plan.qkv_waves},
+      {"qkv_ksplit", e->plan.qkv_ksplit},
       {"o_waves", e->plan.o_waves},
       {"lm_cu", e->plan.lm_cu},
       {"mf_split", e->plan.mf_split},

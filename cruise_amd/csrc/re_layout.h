@@ -141,6 +141,7 @@ struct LaunchPlan {
   int waves;       // waves per GEMV workgroup
   int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
   int qkv_waves;          // waves per qkv workgroup (one RoPE row pair each): 4, or 9
+  int qkv_ksplit;         // > 0: qkv as k_qkv_ksplit, K split over 7 waves (the grid); 0: k_proj
   int o_waves;            // waves per o-proj workgroup (one row pair each): 4, or 7
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)

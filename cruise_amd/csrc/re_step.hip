@@ -342,6 +342,146 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
 }
 
 // ---------------------------------------------------------------------------
+// qkv with K split over the waves (bf16, B <= 4, hidden = 7 x 512): one
+// 7-wave workgroup per CU owns PAIRS RoPE row pairs, and wave w owns elements
+// [512 w, 512 w + 512) of every one of them.  A lane needs only its 8
+// elements of the 4 hidden rows, so it keeps them (normalized) in registers:
+//   requests  the flag, its hidden elements and norm weights, all PAIRS
+//             pairs' weights (2 x PAIRS 16-byte loads), the epilogue inputs;
+//   RMSNorm   each wave's sums of squares go through LDS once (one barrier),
+//             then every lane applies rs to its own elements
+//             (batched_decoder_step.py:224-229, as norm_apply);
+//   products  per pair a lane dots its elements; the 8 totals (2 rows x 4
+//             batch rows) of every pair are reduced over the wave in one
+//             transposing exchange and stored per (pair, wave);
+//   epilogue  one thread per (pair, batch row) adds the 7 wave totals in wave
+//             order, then bias, RoPE and the q / paged K/V writes exactly as
+//             k_proj's qkv epilogue.
+// No LDS staging of the activations and no barrier between the weights'
+// arrival and the products; the sums run in another fp32 order than k_proj's
+// (per-wave K ranges added at the end), within the model tolerance.
+// ---------------------------------------------------------------------------
+constexpr int kQkvKsWaves = 7;
+constexpr int kQkvKsPairs = 9;  // Qwen2.5-7B: 2,304 pairs = 256 x 9
+
+template <int PAIRS>
+__global__ void __launch_bounds__(kQkvKsWaves * 64, 1) k_qkv_ksplit(ProjArgs a) {
+  constexpr int MB = 4;
+  __shared__ float nred[kQkvKsWaves][MB];
+  __shared__ float pred[PAIRS * kQkvKsWaves * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int H = a.H;
+  const int k0 = wave * kChunk + lane * 8;  // this lane's elements
+  const int u0 = blockIdx.x * PAIRS;
+  const bf16_t* W0 = static_cast<const bf16_t*>(a.w0);
+  const bf16_t* Hd = static_cast<const bf16_t*>(a.hidden);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  Vec8<bf16_t> x[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) x[m] = Vec8<bf16_t>::load_cached(Hd + (size_t)min(m, a.B - 1) * H + k0);
+  const Vec8<bf16_t> nw = Vec8<bf16_t>::load_cached(static_cast<const bf16_t*>(a.norm_w) + k0);
+  Vec8<bf16_t> w[PAIRS][2];
+#pragma unroll
+  for (int p = 0; p < PAIRS; ++p) {
+    const bf16_t* wr[kRowsPerWave];
+    int row0, row1;
+    proj_rows<kQkv, bf16_t>(a, min(u0 + p, a.units - 1), W0, nullptr, wr, row0, row1);
+    w[p][0] = Vec8<bf16_t>::load(wr[0] + k0);
+    w[p][1] = Vec8<bf16_t>::load(wr[1] + k0);
+  }
+  // epilogue inputs of thread t < PAIRS * MB: pair t / MB, batch row t % MB
+  const int ep = min(tid / MB, PAIRS - 1), em = tid % MB;
+  const int eu = min(u0 + ep, a.units - 1);
+  int er0 = 0, er1 = 0;
+  {
+    const bf16_t* wr[kRowsPerWave];
+    proj_rows<kQkv, bf16_t>(a, eu, W0, nullptr, wr, er0, er1);
+  }
+  const QkvEpi epi = qkv_epilogue_inputs<bf16_t>(a, eu, er0, er1, em);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // RMSNorm: the rows' sums of squares over the workgroup, rs, then each
+  // lane normalizes its own elements.
+  float ss[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    float t = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t = fmaf(x[m].get(e), x[m].get(e), t);
+    ss[m] = t;
+  }
+  wave_reduce_transpose<MB>(ss, lane);
+  if ((lane & (64 / MB - 1)) == 0) nred[wave][lane / (64 / MB)] = ss[0];
+  lds_barrier();
+  if (stop != 0) return;  // uniform
+  Vec8<bf16_t> y[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    float total = 0.f;
+#pragma unroll
+    for (int q = 0; q < kQkvKsWaves; ++q) total += nred[q][m];
+    y[m] = norm_apply<bf16_t>(x[m], nw, rsqrtf(total / static_cast<float>(H) + a.eps));
+  }
+
+  // Products: value index 8 p + 4 r + m for pair p, row r, batch row m.
+  float v[PAIRS * 8];
+#pragma unroll
+  for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) v[p * 8 + r * 4 + m] = dot8(w[p][r], y[m], 0.f);
+  constexpr int kFull = (PAIRS * 8) / 64;  // whole groups of 64 values
+  static_assert(PAIRS * 8 - kFull * 64 == 0 || PAIRS * 8 - kFull * 64 == 8, "a tail of one pair at most");
+#pragma unroll
+  for (int gq = 0; gq < kFull; ++gq) {
+    float t[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) t[i] = v[gq * 64 + i];
+    wave_reduce_transpose<64>(t, lane);  // lane l: total of value 64 gq + l
+    const int idx = gq * 64 + lane;
+    pred[((idx >> 3) * kQkvKsWaves + wave) * 8 + (idx & 7)] = t[0];
+  }
+  if constexpr (PAIRS * 8 > kFull * 64) {
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = v[kFull * 64 + i];
+    wave_reduce_transpose<8>(t, lane);  // lane l: total of value 8 kFull + l / 8
+    if ((lane & 7) == 0) pred[((kFull * 8) * kQkvKsWaves + wave) * 8 + (lane >> 3)] = t[0];
+  }
+  lds_barrier();
+  if (tid >= PAIRS * MB || u0 + ep >= a.units || em >= a.B) return;
+  float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+  for (int q = 0; q < kQkvKsWaves; ++q) {
+    y0 += pred[(ep * kQkvKsWaves + q) * 8 + em];
+    y1 += pred[(ep * kQkvKsWaves + q) * 8 + 4 + em];
+  }
+  // F.linear with bias, then RoPE and the stores: k_proj's qkv epilogue.
+  const float qa = Elt<bf16_t>::r(y0 + epi.bias0);
+  const float qb = Elt<bf16_t>::r(y1 + epi.bias1);
+  const int half = a.head_dim >> 1;
+  const int hg = eu / half, j = eu - hg * half;
+  const int nq = a.heads, nkv = a.kv_heads;
+  float oa = qa, ob = qb;
+  if (hg < nq + nkv) {
+    oa = Elt<bf16_t>::r(Elt<bf16_t>::r(qa * epi.cos) + Elt<bf16_t>::r(-qb * epi.sin));
+    ob = Elt<bf16_t>::r(Elt<bf16_t>::r(qb * epi.cos) + Elt<bf16_t>::r(qa * epi.sin));
+  }
+  if (hg < nq) {
+    bf16_t* q = static_cast<bf16_t*>(a.out) + (size_t)em * nq * a.head_dim + (size_t)hg * a.head_dim;
+    q[j] = Elt<bf16_t>::t(oa);
+    q[j + half] = Elt<bf16_t>::t(ob);
+  } else if (epi.active != 0 && epi.slot >= 0 && epi.slot < a.slots) {
+    const bool is_key = hg < nq + nkv;
+    const int kvh = is_key ? hg - nq : hg - nq - nkv;
+    bf16_t* cache = static_cast<bf16_t*>(is_key ? a.key_cache : a.value_cache) + ((size_t)epi.slot * nkv + kvh) * a.head_dim;
+    cache[j] = Elt<bf16_t>::t(oa);
+    cache[j + half] = Elt<bf16_t>::t(ob);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Residual projections, split-K form (o-proj; down when its activations do
 // not fit one workgroup's LDS): x W^T per K-segment.  Grid: (row groups,
 // K-segments, row tiles).  One segment: the residual add happens here
@@ -671,6 +811,8 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
       if (p.mfma) {
         const hipError_t err = launch_mfma_op(MfmaOp::kQkv, env, st, l, stream);
         if (err != hipSuccess) return err;
+      } else if (sizeof(T) == 2 && MB == 4 && p.qkv_ksplit > 0) {
+        k_qkv_ksplit<kQkvKsPairs><<<p.qkv_ksplit, kQkvKsWaves * 64, 0, stream>>>(q);
       } else {
         if (p.qkv_waves == 9)
           launch_proj<T, MB, 9, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), normed_lds_bytes(MB, d.hidden, sizeof(T), 9),
@@ -846,6 +988,12 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
     p.qkv_waves = 9;
     p.qkv_grid = cus;
   }
+  // qkv with K split over 7 waves (k_qkv_ksplit): the hidden size is 7 x 512
+  // and the pairs fill whole workgroups of kQkvKsPairs; the grid, or 0
+  p.qkv_ksplit = 0;
+  if (sizeof(T) == 2 && MB == 4 && p.row_tiles == 1 && d.hidden == kQkvKsWaves * kChunk &&
+      (d.qkv_rows() / 2) % kQkvKsPairs == 0)
+    p.qkv_ksplit = d.qkv_rows() / 2 / kQkvKsPairs;
   p.slot_cus = 0;
   p.gu_grid = fit(full ? k_proj<T, MB, WAVES, kGateUp, true> : k_proj<T, MB, WAVES, kGateUp, false>,
                   (d.intermediate + WAVES - 1) / WAVES);

@@ -7,6 +7,10 @@ exactly the default plan's logits, greedy tokens and cache writes.
 - {"o_waves": 4}: the same for the o-projection (448 4-wave workgroups
   against one 7-wave workgroup per 7 row pairs).
 
+The qkv comparisons hold the K-split qkv (k_qkv_ksplit, the default at this
+shape, whose sums run in another fp32 order and are checked against the
+oracle by the layer tests) off on both sides: {"qkv_ksplit": 0}.
+
 The engine allows one instance per process, so the runtimes run one after
 the other."""
 from __future__ import annotations
@@ -35,7 +39,7 @@ def step_once(weights, tuning, inputs):
     tok, pos, length, slot, active, table, key, value = inputs
     rt = make_runtime(W, weights, tuning=tuning)
     try:
-        facts = {k: rt.info(k) for k in ("qkv_waves", "qkv_grid", "o_waves", "o_grid", "compute_units")}
+        facts = {k: rt.info(k) for k in ("qkv_waves", "qkv_grid", "o_waves", "o_grid", "compute_units", "qkv_ksplit")}
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -59,8 +63,8 @@ def test_projection_workgroup_shapes_match_bit_for_bit(weights_dev, tuning):
     dec, _ = oracle_controller(W, {k: v.cpu() for k, v in weights_dev.items()})
     key, value = seeded_cache(dec.cache_shape(), 5150, torch.bfloat16)
     inputs = (tok, pos, length, slot, active, table, key, value)
-    base_facts, base = step_once(weights_dev, {}, inputs)
-    facts, got = step_once(weights_dev, tuning, inputs)
+    base_facts, base = step_once(weights_dev, {"qkv_ksplit": 0}, inputs)
+    facts, got = step_once(weights_dev, {"qkv_ksplit": 0, **tuning}, inputs)
     cus = base_facts["compute_units"]
     qkv_pairs = (W.dims.num_heads + 2 * W.dims.num_kv_heads) * W.dims.head_dim // 2
     o_pairs = W.dims.hidden // 2
@@ -68,6 +72,7 @@ def test_projection_workgroup_shapes_match_bit_for_bit(weights_dev, tuning):
         assert base_facts["qkv_waves"] == 9 and base_facts["qkv_grid"] == cus
     if o_pairs == 7 * cus:
         assert base_facts["o_waves"] == 7 and base_facts["o_grid"] == cus
+    assert base_facts["qkv_ksplit"] == 0 and facts["qkv_ksplit"] == 0
     if "qkv_waves" in tuning:
         assert facts["qkv_waves"] == 4 and facts["qkv_grid"] == (qkv_pairs + 3) // 4
     if "o_waves" in tuning:
