@@ -111,7 +111,7 @@ __device__ __forceinline__ void load_tile(Vec8<T> (&v)[AttnShape<D>::kLoads], co
 
 __device__ __forceinline__ float attn_block_max(float v, float* red, int tid) {
   const int lane = tid & 63, wave = wave_index(tid);
-  v = wave_max(v);
+  v = wave_max_dpp(v);
   __syncthreads();
   if (lane == 0) red[wave] = v;
   __syncthreads();
@@ -123,7 +123,7 @@ __device__ __forceinline__ float attn_block_max(float v, float* red, int tid) {
 
 __device__ __forceinline__ float attn_block_sum(float v, float* red, int tid) {
   const int lane = tid & 63, wave = wave_index(tid);
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   __syncthreads();
   if (lane == 0) red[wave] = v;
   __syncthreads();
@@ -217,8 +217,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
     }
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
-      // positions >= neff have off < 0; a missing row is a zero value
-      const float p = off[i] >= 0 ? sc[tile_pos<D>(t, w, i, r)] : 0.f;
+      // positions >= neff have off < 0; a missing row is a zero value.  The
+      // read is unconditional (index clamped into the window) so the tile's
+      // reads do not wait one by one.
+      const float pr = sc[min(tile_pos<D>(t, w, i, r), W - 1)];
+      const float p = off[i] >= 0 ? pr : 0.f;
       const Vec8<T> v = off[i] >= 0 ? vr[i] : Vec8<T>{};
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, v.get(e), acc[e]);

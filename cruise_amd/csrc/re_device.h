@@ -231,3 +231,34 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
   return v;
 }
+
+// The same reductions with the steps inside 16-lane rows on DPP moves (quad
+// swaps, then the 8- and 16-lane mirrors: a few cycles each, no LDS round
+// trip) and only the two steps across rows through ds_bpermute.  Every lane
+// ends with the same value (each step adds or compares a pair symmetrically).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_move<kDppQuadXor1>(v);
+  v += dpp_move<kDppQuadXor2>(v);
+  v += dpp_move<kDppRowHalfMirror>(v);
+  v += dpp_move<kDppRowMirror>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_move<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_move<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_move<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp_move<kDppRowMirror>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
