@@ -12,6 +12,187 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention split over the window (long contexts at few rows): one
+// workgroup per (row, query head, tile of 256 positions), so a window of n
+// tiles costs the round trips of one tile instead of n in a row.  Same
+// arithmetic and rounding points as attn_body; the row's max and sum are
+// exact before any probability is rounded:
+//   k_attn_split_scores: s_j as attn_body, into sp_scores; the tile's max m_t
+//     and e_t = sum of exp(s_j - m_t) over its positions into sp_stats;
+//   k_attn_split_pv: M = max_t m_t, sum = sum_t e_t exp(m_t - M) (tiles
+//     summed in a fixed order), p_j = bf16(exp(s_j - M) / sum), and the
+//     tile's P.V (fp32) into sp_part;
+//   k_attn_split_sum: o = T(sum of the tiles' P.V in tile order).
+// Only the fp32 summation orders differ from attn_body.  Tiles past the
+// row's context (neff) do nothing and are not read.  The 7 heads sharing a
+// KV head sit 8 * k block ids apart (block = unit + units * head_in_group,
+// unit = grp + groups * tile, units a multiple of 8 for 4 KV heads and an
+// even row count) so their key and value reads share an XCD's L2.
+
+struct SplitUnit {
+  int b, g, h, t;
+};
+
+__device__ __forceinline__ SplitUnit split_unit(const AttnArgs& a, int block) {
+  const int G = a.heads / a.kv_heads;
+  const int groups = a.B * a.kv_heads;
+  const int units = groups * a.split_tiles;
+  const int hi = block / units, u = block - hi * units;
+  const int t = u / groups, grp = u - t * groups;
+  SplitUnit s;
+  s.b = grp / a.kv_heads;
+  s.g = grp - s.b * a.kv_heads;
+  s.h = s.g * G + hi;
+  s.t = t;
+  return s;
+}
+
+__device__ __forceinline__ int split_neff(const AttnArgs& a, int b) {
+  const int n = a.len[b];
+  return n <= 0 ? a.window : min(n, a.window);
+}
+
+template <typename T, int D, bool P2>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_split_scores(AttnArgs a) {
+  using S = AttnShape<D>;
+  constexpr int L = S::kLpr;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ float red[kAttnThreads / 64];
+  int* tabs = reinterpret_cast<int*>(smem_raw);  // [blocks_per_row]
+  const int tid = threadIdx.x;
+  const SplitUnit u = split_unit(a, blockIdx.x);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const bool uniform = a.len[u.b] <= 0;
+  const int neff = split_neff(a, u.b);
+  if (stop != 0 || u.t * kAttnTile >= neff) return;  // uniform over the workgroup
+  const int lane = tid & 63, w = wave_index(tid);
+  const int r = lane / L, c = lane % L;
+  const int32_t* tab = a.table + (size_t)u.b * a.blocks_per_row;
+  for (int e = tid; e < a.blocks_per_row; e += kAttnThreads) tabs[e] = tab[e];
+  const Vec8<T> qv = Vec8<T>::load_cached(static_cast<const T*>(a.q) + ((size_t)u.b * a.heads + u.h) * D + c * 8);
+  lds_barrier();
+  int off[S::kLoads];
+  tile_offsets<D, P2>(off, tabs, u.t, w, r, c, neff, a, u.g);
+  Vec8<T> kr[S::kLoads];
+  load_tile<T, D>(kr, static_cast<const T*>(a.key_cache), off, c);
+  // a missing row (slot outside the cache) is a zero key: score 0
+  float part_dot[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) part_dot[i] = off[i] >= 0 ? dot8(kr[i], qv, 0.f) : 0.f;
+  group_reduce_transpose<L>(part_dot, c);
+  // lane (r, c) holds the score of position tile_pos(t, w, c, r)
+  const int j = tile_pos<D>(u.t, w, c, r);
+  float s = part_dot[0];
+  if constexpr (sizeof(T) == 2) s = round_bf16(s);  // ExactQk output is bf16
+  s = round_bf16(s / sqrtf(static_cast<float>(D)));
+  if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
+  const bool in = j < neff;
+  const size_t row = (size_t)u.b * a.heads + u.h;
+  if (in) a.sp_scores[row * a.window + j] = s;
+  const float mt = attn_block_max(in ? s : -INFINITY, red, tid);
+  const float et = attn_block_sum(in ? expf(s - mt) : 0.f, red, tid);
+  if (tid == 0) {
+    float* st = a.sp_stats + (row * a.split_tiles + u.t) * 2;
+    st[0] = mt;
+    st[1] = et;
+  }
+}
+
+template <typename T, int D, bool P2>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_split_pv(AttnArgs a) {
+  using S = AttnShape<D>;
+  constexpr int L = S::kLpr;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ float red[kAttnThreads / 64];
+  __shared__ float pr[kAttnTile];               // the tile's probabilities
+  __shared__ float part[kAttnThreads * 8];      // [4 waves][64 lanes][8] P.V partials
+  int* tabs = reinterpret_cast<int*>(smem_raw);  // [blocks_per_row]
+  const int tid = threadIdx.x;
+  const SplitUnit u = split_unit(a, blockIdx.x);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int neff = split_neff(a, u.b);
+  if (stop != 0 || u.t * kAttnTile >= neff) return;  // uniform over the workgroup
+  const int lane = tid & 63, w = wave_index(tid);
+  const int r = lane / L, c = lane % L;
+  // Round trip 1: the block table, this thread's score and the first tile
+  // statistics it reduces (clamped reads; the masks below drop the extras).
+  // Round trip 2: the tile's values.
+  const size_t row = (size_t)u.b * a.heads + u.h;
+  const int nt = (neff + kAttnTile - 1) / kAttnTile;
+  const float* st = a.sp_stats + row * a.split_tiles * 2;
+  const int j = u.t * kAttnTile + tid;
+  const float sj = a.sp_scores[row * a.window + min(j, neff - 1)];
+  const int i0 = min(tid, nt - 1);
+  const float m0 = st[2 * i0], e0 = st[2 * i0 + 1];
+  const int32_t* tab = a.table + (size_t)u.b * a.blocks_per_row;
+  for (int e = tid; e < a.blocks_per_row; e += kAttnThreads) tabs[e] = tab[e];
+  lds_barrier();
+  int off[S::kLoads];
+  tile_offsets<D, P2>(off, tabs, u.t, w, r, c, neff, a, u.g);
+  Vec8<T> vr[S::kLoads];
+  load_tile<T, D>(vr, static_cast<const T*>(a.value_cache), off, c);
+
+  // The row's exact max and sum from the tiles' statistics.
+  float m = tid < nt ? m0 : -INFINITY;
+  for (int i = tid + kAttnThreads; i < nt; i += kAttnThreads) m = fmaxf(m, st[2 * i]);
+  const float mx = attn_block_max(m, red, tid);
+  float e = tid < nt ? e0 * expf(m0 - mx) : 0.f;
+  for (int i = tid + kAttnThreads; i < nt; i += kAttnThreads) e += st[2 * i + 1] * expf(st[2 * i] - mx);
+  const float inv = 1.0f / attn_block_sum(e, red, tid);
+  pr[tid] = j < neff ? round_bf16(expf(sj - mx) * inv) : 0.f;
+  __syncthreads();
+
+  // P.V of the tile: lane (r, c) accumulates elements c*8..c*8+7 over its rows.
+  float acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < S::kLoads; ++i) {
+    // positions >= neff have off < 0; a missing row is a zero value
+    const float p = off[i] >= 0 ? pr[w * 64 + i * S::kRg + r] : 0.f;
+    const Vec8<T> v = off[i] >= 0 ? vr[i] : Vec8<T>{};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = fmaf(p, v.get(k), acc[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) part[(w * 64 + lane) * 8 + k] = acc[k];
+  __syncthreads();
+  if (tid < D) {
+    const int cc = tid / 8, k = tid % 8;
+    float o = 0.f;
+    for (int ww = 0; ww < kAttnThreads / 64; ++ww)
+      for (int rr = 0; rr < S::kRg; ++rr) o += part[(ww * 64 + rr * L + cc) * 8 + k];
+    a.sp_part[(row * a.split_tiles + u.t) * D + tid] = o;
+  }
+}
+
+// One thread per output element (row, head, element): the tiles' P.V in
+// tile order.
+template <typename T>
+__global__ void __launch_bounds__(256) k_attn_split_sum(AttnArgs a) {
+  const int D = a.head_dim;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.B * a.heads * D) return;
+  if (a.done != nullptr && __builtin_nontemporal_load(a.done) != 0) return;
+  const int row = i / D, k = i - row * D;
+  const int b = row / a.heads;
+  const int nt = (split_neff(a, b) + kAttnTile - 1) / kAttnTile;
+  const float* p = a.sp_part + (size_t)row * a.split_tiles * D + k;
+  // 8 tiles requested at a time (clamped reads, masked adds), added in order
+  float o = 0.f;
+  for (int t = 0; t < nt; t += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p[(size_t)min(t + i, nt - 1) * D];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o = t + i < nt ? o + v[i] : o;
+  }
+  const int hk = (row - b * a.heads) * D + k;
+  static_cast<T*>(a.out)[a.packed_out ? xpack_index(b, hk, a.heads * D) : (size_t)b * a.heads * D + hk] =
+      Elt<T>::t(o);
+}
+
+// ---------------------------------------------------------------------------
 // Grouped decode attention for many rows (B x KV heads >= 64, bf16,
 // head_dim 128): one workgroup per (row, KV head) computes the G <= 8 query
 // heads that share the KV head, so every key and value row is read once for
@@ -560,9 +741,31 @@ size_t smem_bytes(int window, int blocks_per_row) {
   return (size_t)window * sizeof(float) + (size_t)kAttnThreads * 8 * sizeof(float) + (size_t)blocks_per_row * sizeof(int);
 }
 
+// The window-split attention's three launches.
+template <typename T, int D>
+hipError_t launch_split_t(const AttnArgs& a, hipStream_t stream) {
+  const int grid = a.B * a.heads * a.split_tiles;
+  const size_t smem = (size_t)a.blocks_per_row * sizeof(int);
+  if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size) {
+    k_attn_split_scores<T, D, true><<<grid, kAttnThreads, smem, stream>>>(a);
+    k_attn_split_pv<T, D, true><<<grid, kAttnThreads, smem, stream>>>(a);
+  } else {
+    k_attn_split_scores<T, D, false><<<grid, kAttnThreads, smem, stream>>>(a);
+    k_attn_split_pv<T, D, false><<<grid, kAttnThreads, smem, stream>>>(a);
+  }
+  k_attn_split_sum<T><<<(a.B * a.heads * D + 255) / 256, 256, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 // Power-of-two block sizes take the shift-and-mask position arithmetic.
 template <typename T, int D>
 hipError_t launch_t(const AttnArgs& a, hipStream_t stream) {
+  if (a.split_tiles > 0) {
+    if (a.sp_scores == nullptr || a.sp_stats == nullptr || a.sp_part == nullptr ||
+        a.split_tiles * kAttnTile < a.window)
+      return hipErrorInvalidValue;
+    return launch_split_t<T, D>(a, stream);
+  }
   const size_t smem = smem_bytes(a.window, a.blocks_per_row);
   if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size)
     k_attn<T, D, true><<<a.B * a.heads, kAttnThreads, smem, stream>>>(a);

@@ -351,6 +351,16 @@ bool make_plan(Engine& e, const Json& cfg) {
   if (p.grouped_attn && group_attention_mfma_fits(d) &&
       (tune == nullptr || tune->number_or("attention_mfma", 1) != 0))
     p.grouped_attn = 2;
+  // the per-(row, head) attention split over the window in 256-position
+  // tiles, by default past 768 positions (where three launches of one tile
+  // each beat walking the tiles in a row); "tuning": {"attention_split": 0
+  // or 1} forces it off or on
+  p.attn_split = 0;
+  if (p.grouped_attn == 0) {
+    bool split = d.capacity > 768;
+    if (tune != nullptr) split = tune->number_or("attention_split", split ? 1 : 0) != 0;
+    if (split) p.attn_split = (d.capacity + 255) / 256;
+  }
   if (const Json* t = cfg.get("tuning")) {
     e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
     // "down_whole": 0 keeps the split-K down projection and its reduce launch
@@ -527,6 +537,10 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {&e.scratch.xn, p.mfma ? (size_t)B * d.hidden * T : 0},
       {reinterpret_cast<void**>(&e.scratch.mf_part), p.mf_split ? mfma_split_partial_bytes(d) : 0},
+      {reinterpret_cast<void**>(&e.scratch.sp_scores), (size_t)p.attn_split * 256 * B * d.heads * sizeof(float)},
+      {reinterpret_cast<void**>(&e.scratch.sp_stats), (size_t)p.attn_split * 2 * B * d.heads * sizeof(float)},
+      {reinterpret_cast<void**>(&e.scratch.sp_part),
+       (size_t)p.attn_split * d.head_dim * B * d.heads * sizeof(float)},
       {reinterpret_cast<void**>(&e.logits), (size_t)B * d.vocab * sizeof(float)},
       {reinterpret_cast<void**>(&e.checksum_dev), 64},
   };
@@ -1733,6 +1747,7 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"part_cu", e->plan.part_cu},
       {"qkv_split", e->plan.qkv_split},
       {"grouped_attention", e->plan.grouped_attn},
+      {"attention_split", e->plan.attn_split},
       {"argmax_parts", e->plan.argmax_parts},
       {"o_grid", e->plan.o_grid},
       {"lm_grid", e->plan.lm_grid},

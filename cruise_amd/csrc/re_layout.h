@@ -133,6 +133,9 @@ struct Scratch {
   float* rope;        // [B, d/2, 2] the step's RoPE cos, sin (rounded to T)
   void* xn;           // T [B, H] normalized rows (matrix-core projections)
   float* mf_part;     // matrix-core o / down partial sums [8][B][H] (split plan)
+  float* sp_scores;   // window-split attention: scores, tile statistics, tile P.V (AttnArgs)
+  float* sp_stats;
+  float* sp_part;
 };
 
 struct LaunchPlan {
@@ -167,6 +170,7 @@ struct LaunchPlan {
   int qkv_split;   // 64-row qkv split over (9-strip group, K range), epilogue in k_mf_qkv_finish
   // 1: decode attention per (row, KV head) for all query heads of the group
   int grouped_attn;
+  int attn_split;  // > 0: decode attention split over the window in this many 256-position tiles
 };
 
 // Arguments of the paged decode attention (re_attn.hip).
@@ -184,6 +188,13 @@ struct AttnArgs {
   int grouped;             // 1: one workgroup per (row, KV head) (re_attn.hip k_attn_group); 2: the same on
                            // the matrix cores (k_attn_mgroup)
   int packed_out;          // out in the matrix-core path's packed layout (xpack_index, K = NH*d)
+  // > 0: the window split into split_tiles tiles of 256 positions, one
+  // workgroup per (row, head, tile) over three launches (re_attn.hip
+  // k_attn_split_*); only with grouped == 0
+  int split_tiles;
+  float* sp_scores;        // [B*NH][window] scaled scores
+  float* sp_stats;         // [B*NH][split_tiles][2] each tile's max and sum of exp(s - max)
+  float* sp_part;          // [B*NH][split_tiles][d] each tile's P.V
 };
 size_t attention_lds_bytes(const Dims& d);
 // The grouped attention's default: many rows (B x KV heads >= 64); whether the

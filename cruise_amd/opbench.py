@@ -75,6 +75,7 @@ def main() -> int:
     p.add_argument("--context", type=int, default=128, help="tokens per row already in the KV cache")
     p.add_argument("--copy-bytes", type=int, default=0)
     p.add_argument("--tuning", default="", help="JSON object of launch-plan overrides")
+    p.add_argument("--capacity", type=int, default=256, help="window positions per row (a multiple of 128)")
     args = p.parse_args()
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.iters)
@@ -84,13 +85,16 @@ def main() -> int:
 
     from cruise_amd.runtime import EngineConfig, EngineSpec, ModelSpec, ResidentEpochRuntime, WeightSpec
 
-    capacity = 256
+    capacity = args.capacity
+    if capacity < 128 or capacity % 128 != 0:
+        raise SystemExit("--capacity must be a positive multiple of 128")
     if not 1 <= args.context <= capacity:
         raise SystemExit(f"--context must be in [1, {capacity}]")
+    bpr = capacity // 128
     cfg = EngineConfig(
         model=ModelSpec(),
         engine=EngineSpec(
-            batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=capacity
+            batch=4, physical_blocks=4 * bpr, block_size=128, blocks_per_row=bpr, logical_capacity=capacity
         ),
         weights=WeightSpec("synthetic", 1, 0.02),
         tuning=json.loads(args.tuning) if args.tuning else {},
@@ -103,7 +107,7 @@ def main() -> int:
         kv_dim = kv_heads * d
         qkv_rows = heads * d + 2 * kv_dim
         ctx = args.context
-        table = np.arange(8, dtype=np.int32).reshape(4, 2)
+        table = np.arange(4 * bpr, dtype=np.int32).reshape(4, bpr)
         pos = np.full(B, ctx - 1, np.int64)
         ln = np.full((B, 1), ctx, np.int32)
         slot = np.array([table[r, (ctx - 1) // 128] * 128 + (ctx - 1) % 128 for r in range(B)], dtype=np.int32)
