@@ -18,6 +18,7 @@
 //              (token, head).
 //   SwiGLU     elementwise on the gate and up products
 #include <algorithm>
+#include <type_traits>
 
 #include "re_device.h"
 #include "re_layout.h"
@@ -487,7 +488,6 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
   const int qloc = sm * 32 + (lane & 31);  // this lane's query within the tile
   const int qlim = p0 + qloc;              // its visible keys: j <= qlim
   constexpr float kLog2e = 1.44269504088896340736f;
-  const float scale_div = sqrtf(static_cast<float>(kAd));
 
   // Q fragments (B operand): query qloc (rows past the tile read the last one)
   bf16x8_t qf[kAd / 16];
@@ -538,8 +538,10 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
     }
   };
   // Scores of key tile kt for this lane's query: s[v] is key
-  // kt * 64 + sn * 32 + 8 (v / 4) + 4 hi + v % 4.
-  auto scores = [&](int kt, float (&sc)[16]) {
+  // kt * 64 + sn * 32 + 8 (v / 4) + 4 hi + v % 4.  MASKED: the tile reaches
+  // past some query's causal limit (the tiles before nfull end at or before
+  // the first query's position, so every query sees all of their keys).
+  auto scores = [&](int kt, float (&sc)[16], auto masked) {
     f32x16_t acc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.f;
@@ -550,34 +552,44 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int j = kt * kAk + sn * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
-      const float x = round_bf16(round_bf16(acc[v]) / scale_div);
-      sc[v] = j <= qlim ? x : -INFINITY;
+      const float x = round_bf16(div_sqrt128_bf16(round_bf16(acc[v])));
+      if constexpr (decltype(masked)::value) {
+        const int j = kt * kAk + sn * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+        sc[v] = j <= qlim ? x : -INFINITY;
+      } else {
+        sc[v] = x;
+      }
     }
   };
+  const int nfull = min(nkt, (p0 + 1) / kAk);
 
-  // Pass 1: row max and sum.
+  // Pass 1: row max and sum.  A masked score adds exp2(-inf) = 0; while all
+  // of a lane's scores so far are masked (m = -inf) its sum stays 0.
   float m = -INFINITY, l = 0.f;
-  load_k(0);
-  for (int kt = 0; kt < nkt; ++kt) {
+  auto pass1 = [&](int kt, auto masked) {
+#pragma clang fp contract(off)  // the rescaled sum is a product, then a sum
     store_k();
     load_k(kt + 1);
     lds_barrier();
     float sc[16];
-    scores(kt, sc);
+    scores(kt, sc, masked);
     float tmax = sc[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, sc[v]);
     const float mn = fmaxf(m, tmax);
-    if (mn != -INFINITY) {
-      const float bn = mn * kLog2e;
-      float add = 0.f;
+    const float bn = mn == -INFINITY ? 0.f : mn * kLog2e;
+    float add = 0.f;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) add += sc[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(sc[v], kLog2e, -bn));
-      l = (m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -bn))) + add;
-      m = mn;
-    }
+    for (int v = 0; v < 16; ++v) add += __builtin_amdgcn_exp2f(fmaf(sc[v], kLog2e, -bn));
+    l = l * __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -bn)) + add;
+    m = mn;
     lds_barrier();
+  };
+  load_k(0);
+  {
+    int kt = 0;
+    for (; kt < nfull; ++kt) pass1(kt, std::false_type{});
+    for (; kt < nkt; ++kt) pass1(kt, std::true_type{});
   }
   {
     const float m2 = __shfl_xor(m, 32, 64), l2 = __shfl_xor(l, 32, 64);
@@ -612,24 +624,21 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
-  load_k(0);
-  load_v(0);
-  for (int kt = 0; kt < nkt; ++kt) {
+  // M is finite (key 0 is visible to every query), so a masked score's
+  // probability is exp2(-inf) = 0.
+  auto pass2 = [&](int kt, auto masked) {
     store_k();
     store_v();
     load_k(kt + 1);
     load_v(kt + 1);
     lds_barrier();
     float sc[16];
-    scores(kt, sc);
+    scores(kt, sc, masked);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       float pv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = sc[8 * b + e];
-        pv[e] = x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -base)) * inv;
-      }
+      for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(fmaf(sc[8 * b + e], kLog2e, -base)) * inv;
       re_u32x4 pw;
 #pragma unroll
       for (int e = 0; e < 4; ++e) pw[e] = f2_to_bf16x2(pv[2 * e], pv[2 * e + 1]);
@@ -645,6 +654,13 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
       }
     }
     lds_barrier();
+  };
+  load_k(0);
+  load_v(0);
+  {
+    int kt = 0;
+    for (; kt < nfull; ++kt) pass2(kt, std::false_type{});
+    for (; kt < nkt; ++kt) pass2(kt, std::true_type{});
   }
   // The two key halves' partial O: the sn = 1 waves hand theirs over in LDS
   // (the tiles are free now), the sn = 0 waves add (sn 0 + sn 1) and store.
