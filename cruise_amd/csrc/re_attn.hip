@@ -723,6 +723,268 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// The matrix-core grouped attention split over the window: one workgroup per
+// (row, KV head, tile of 256 positions), so a row's long window spreads over
+// many CUs instead of one, with k_attn_mgroup's arithmetic and rounding
+// points (only fp32 summation orders differ):
+//   k_attn_msplit_scores: the tile's scores of the G heads on the matrix
+//     cores (k_attn_mgroup's key loads and products), into sp_scores, with
+//     each head's tile max m_t and e_t = sum of exp(s - m_t) into sp_stats;
+//   k_attn_msplit_pv: each head's row max M = max_t m_t and sum
+//     L = sum_t e_t exp(m_t - M) (tiles in order), p = bf16(exp(s - M) / L)
+//     and the tile's P.V on the matrix cores into sp_part (fp32);
+//   k_attn_split_sum: o = bf16(sum of the tiles' P.V in tile order).
+// Block b = grp + groups * tile (grp = row * KV heads + KV head).
+constexpr int kMsRows = kMgTile;  // positions per workgroup
+struct MsLayout {
+  size_t roff, sc, pb, vt, stat, tabs, total;
+};
+// LDS of the two kernels: row offsets [256] int, then the scores kernel's
+// scores [256][8] fp32, or the P.V kernel's probabilities [8][256] bf16, Vᵀ
+// [128][kMgVtLd] bf16 and head statistics [2][8] fp32; the block table last.
+__host__ __device__ MsLayout msplit_layout(int blocks_per_row, bool pv) {
+  MsLayout l;
+  l.roff = 0;
+  l.sc = l.roff + kMsRows * sizeof(int);
+  l.pb = l.sc;
+  l.vt = l.pb + (size_t)kMgMaxG * kMsRows * sizeof(bf16_t);
+  l.stat = l.vt + (size_t)kMgD * kMgVtLd * sizeof(bf16_t);
+  l.tabs = pv ? l.stat + 2 * kMgMaxG * sizeof(float) : l.sc + (size_t)kMsRows * kMgMaxG * sizeof(float);
+  l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
+  return l;
+}
+size_t msplit_smem_bytes(int blocks_per_row, bool pv) { return msplit_layout(blocks_per_row, pv).total; }
+
+// Row offsets of the tile's positions (this KV head), -1 past the context or
+// for a slot outside the cache.
+template <bool P2>
+__device__ __forceinline__ void msplit_offsets(const AttnArgs& a, const int* tabs, int* roff, int t, int g, int neff,
+                                               int tid) {
+  for (int jl = tid; jl < kMsRows; jl += kMgThreads) {
+    const int j = t * kMsRows + jl;
+    int o = -1;
+    if (j < neff) {
+      int blk, in_blk;
+      block_of<P2>(j, a, blk, in_blk);
+      const long long slot = (long long)tabs[min(blk, a.blocks_per_row - 1)] * a.block_size + in_blk;
+      if (slot >= 0 && slot < a.slots) o = static_cast<int>((slot * a.kv_heads + g) * kMgD);
+    }
+    roff[jl] = o;
+  }
+}
+
+template <bool P2>
+__global__ void __launch_bounds__(kMgThreads) k_attn_msplit_scores(AttnArgs a) {
+  extern __shared__ __align__(16) unsigned char ms_smem[];
+  __shared__ float red[kMgWaves][kMgMaxG];
+  const int G = a.heads / a.kv_heads, W = a.window;
+  const int groups = a.B * a.kv_heads;
+  const int t = blockIdx.x / groups, grp = blockIdx.x - t * groups;
+  const int b = grp / a.kv_heads, g = grp - b * a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const MsLayout L = msplit_layout(a.blocks_per_row, false);
+  int* roff = reinterpret_cast<int*>(ms_smem + L.roff);
+  float* sc = reinterpret_cast<float*>(ms_smem + L.sc);  // [256][kMgMaxG]
+  int* tabs = reinterpret_cast<int*>(ms_smem + L.tabs);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int n = a.len[b];
+  const bool uniform = n <= 0;
+  const int neff = uniform ? W : min(n, W);
+  if (stop != 0 || t * kMsRows >= neff) return;  // uniform over the workgroup
+  for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
+  mg_bf16x8 qf[4];
+  {
+    const bf16_t* qrow = static_cast<const bf16_t*>(a.q) + ((size_t)b * a.heads + g * G + min(l16, G - 1)) * kMgD;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const re_u32x4 v = *reinterpret_cast<const re_u32x4*>(qrow + kk * 32 + lq * 8);
+      qf[kk] = __builtin_bit_cast(mg_bf16x8, l16 < G ? v : re_u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+  lds_barrier();
+  msplit_offsets<P2>(a, tabs, roff, t, g, neff, tid);
+  lds_barrier();
+  // keys: wave w, step q reads positions (2 w + q) * 16 + l % 16 of the tile
+  const bf16_t* KC = static_cast<const bf16_t*>(a.key_cache);
+  re_u32x4 kf[2][4];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int off = roff[(2 * wave + q) * 16 + l16];
+    const bf16_t* row = KC + (off >= 0 ? off : 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kf[q][kk] = *reinterpret_cast<const re_u32x4*>(row + kk * 32 + lq * 8);
+  }
+  const float scale_div = sqrtf(static_cast<float>(kMgD));
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    mg_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, kf[q][kk]), qf[kk], acc, 0, 0, 0);
+    // value v of lane l: position 4 (l / 16) + v of the group, head l % 16
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int jl = (2 * wave + q) * 16 + lq * 4 + v;
+      float s = round_bf16(acc[v]);  // ExactQk output is bf16
+      s = round_bf16(s / scale_div);
+      if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
+      // a missing row (slot outside the cache) is a zero key: score 0
+      if (l16 < kMgMaxG) sc[(size_t)jl * kMgMaxG + l16] = roff[jl] >= 0 || uniform ? s : 0.f;
+    }
+  }
+  lds_barrier();
+  // Threads 0-255 own one position each (all heads); the rest hold nothing.
+  const int jl = tid & (kMsRows - 1);
+  const bool in = tid < kMsRows && t * kMsRows + jl < neff;
+  float v[kMgMaxG];
+  {
+    const re_f32x4 lo = *reinterpret_cast<const re_f32x4*>(sc + (size_t)jl * kMgMaxG);
+    const re_f32x4 hi = *reinterpret_cast<const re_f32x4*>(sc + (size_t)jl * kMgMaxG + 4);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      v[h] = lo[h];
+      v[h + 4] = hi[h];
+    }
+  }
+  float m[kMgMaxG];
+#pragma unroll
+  for (int h = 0; h < kMgMaxG; ++h) m[h] = in ? v[h] : -INFINITY;
+  wave_max_n<kMgMaxG>(m);
+  if (lane == 0)
+#pragma unroll
+    for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = m[h];
+  lds_barrier();
+  float mx[kMgMaxG];
+#pragma unroll
+  for (int h = 0; h < kMgMaxG; ++h) {
+    mx[h] = red[0][h];
+#pragma unroll
+    for (int w = 1; w < kMgWaves; ++w) mx[h] = fmaxf(mx[h], red[w][h]);
+  }
+  lds_barrier();  // every max read before red is reused
+  float e[kMgMaxG];
+#pragma unroll
+  for (int h = 0; h < kMgMaxG; ++h) e[h] = in ? expf(v[h] - mx[h]) : 0.f;
+  wave_sum_n<kMgMaxG>(e);
+  if (lane == 0)
+#pragma unroll
+    for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = e[h];
+  lds_barrier();
+  const size_t row0 = (size_t)b * a.heads + g * G;  // (row, first head of the group)
+  if (tid == 0) {
+#pragma unroll
+    for (int h = 0; h < kMgMaxG; ++h) {
+      if (h < G) {
+        float total = 0.f;
+#pragma unroll
+        for (int w = 0; w < kMgWaves; ++w) total += red[w][h];
+        float* st = a.sp_stats + ((row0 + h) * a.split_tiles + t) * 2;
+        st[0] = mx[h];
+        st[1] = total;
+      }
+    }
+  }
+  if (in) {
+#pragma unroll
+    for (int h = 0; h < kMgMaxG; ++h)
+      if (h < G) a.sp_scores[(row0 + h) * W + t * kMsRows + jl] = v[h];
+  }
+}
+
+template <bool P2>
+__global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
+  extern __shared__ __align__(16) unsigned char ms_smem[];
+  const int G = a.heads / a.kv_heads, W = a.window;
+  const int groups = a.B * a.kv_heads;
+  const int t = blockIdx.x / groups, grp = blockIdx.x - t * groups;
+  const int b = grp / a.kv_heads, g = grp - b * a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const MsLayout L = msplit_layout(a.blocks_per_row, true);
+  int* roff = reinterpret_cast<int*>(ms_smem + L.roff);
+  bf16_t* pb = reinterpret_cast<bf16_t*>(ms_smem + L.pb);  // [kMgMaxG][256]
+  bf16_t* vt = reinterpret_cast<bf16_t*>(ms_smem + L.vt);  // [D][kMgVtLd]
+  float* stat = reinterpret_cast<float*>(ms_smem + L.stat);  // [max, 1 / sum][kMgMaxG]
+  int* tabs = reinterpret_cast<int*>(ms_smem + L.tabs);
+  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int n = a.len[b];
+  const int neff = n <= 0 ? W : min(n, W);
+  if (stop != 0 || t * kMsRows >= neff) return;  // uniform over the workgroup
+  const int nt = (neff + kMsRows - 1) / kMsRows;
+  const size_t row0 = (size_t)b * a.heads + g * G;
+  for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
+  // Each head's row max and sum from the tiles' statistics: wave h < G
+  // reduces head h (tiles lane, lane + 64, ... then the wave in a fixed order).
+  if (wave < G) {
+    const float* st = a.sp_stats + (row0 + wave) * a.split_tiles * 2;
+    float m = -INFINITY;
+    for (int i = lane; i < nt; i += 64) m = fmaxf(m, st[2 * i]);
+    m = wave_max_dpp(m);
+    float e = 0.f;
+    for (int i = lane; i < nt; i += 64) e += st[2 * i + 1] * expf(st[2 * i] - m);
+    e = wave_sum_dpp(e);
+    if (lane == 0) {
+      stat[wave] = m;
+      stat[kMgMaxG + wave] = 1.0f / e;
+    }
+  }
+  lds_barrier();
+  msplit_offsets<P2>(a, tabs, roff, t, g, neff, tid);
+  lds_barrier();
+  // value rows p0 .. p0+7 of the tile, chunk l16 (elements 8 l16 ..+8); bit i
+  // of the mask marks row i valid (invalid rows enter as zero)
+  const bf16_t* VC = static_cast<const bf16_t*>(a.value_cache);
+  const int p0 = wave * 32 + lq * 8;
+  Vec8<bf16_t> vr[8];
+  int mask = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int off = roff[p0 + i];
+    vr[i] = Vec8<bf16_t>::load_cached(VC + (off >= 0 ? off : 0) + l16 * 8);
+    mask |= (off >= 0 ? 1 : 0) << i;
+  }
+  // probabilities of the tile: thread t covers position t % 256 of heads
+  // t / 256, t / 256 + 2, ... (zero past the context and for head slots >= G)
+  for (int i = tid; i < kMgMaxG * kMsRows; i += kMgThreads) {
+    const int h = i / kMsRows, jl = i - h * kMsRows;
+    const int j = t * kMsRows + jl;
+    float p = 0.f;
+    if (h < G && j < neff) p = round_bf16(expf(a.sp_scores[(row0 + h) * W + j] - stat[h]) * stat[kMgMaxG + h]);
+    pb[(size_t)h * kMsRows + jl] = f_to_bf16(p);  // exact: p is bf16
+  }
+  // Vᵀ of the tile, then P.V: wave w owns output columns 16 w ..+16 of every head.
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    re_u32x4 col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (mask >> (2 * i)) & 1 ? (vr[2 * i].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
+      const uint32_t hi = (mask >> (2 * i + 1)) & 1 ? (vr[2 * i + 1].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
+      col[i] = lo | (hi << 16);
+    }
+    *reinterpret_cast<re_u32x4*>(vt + (size_t)(l16 * 8 + e) * kMgVtLd + p0) = col;
+  }
+  lds_barrier();
+  mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < kMsRows / 32; ++k) {
+    // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past G)
+    re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * kMsRows + k * 32 + lq * 8);
+    if (l16 >= G) pa = re_u32x4{0u, 0u, 0u, 0u};
+    const re_u32x4 vb4 = *reinterpret_cast<const re_u32x4*>(vt + (size_t)(wave * 16 + l16) * kMgVtLd + k * 32 + lq * 8);
+    oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, vb4),
+                                                   oacc, 0, 0, 0);
+  }
+  // value v of lane l: head 4 (l / 16) + v, column 16 w + l % 16
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int h = lq * 4 + v;
+    if (h < G) a.sp_part[((row0 + h) * a.split_tiles + t) * kMgD + wave * 16 + l16] = oacc[v];
+  }
+}
+
 }  // namespace
 
 bool group_attention_fits(const Dims& d) {
@@ -733,6 +995,11 @@ bool group_attention_default(const Dims& d) { return group_attention_fits(d) && 
 bool group_attention_mfma_fits(const Dims& d) {
   return group_attention_fits(d) && d.groups() <= kMgMaxG && d.head_dim == kMgD &&
          mgroup_smem_bytes(d.groups(), d.capacity, d.blocks_per_row) <= 150 * 1024;
+}
+// The split matrix-core version: its LDS does not grow with the window.
+bool group_attention_msplit_fits(const Dims& d) {
+  return d.dtype_bytes == 2 && d.head_dim == kMgD && d.groups() <= kMgMaxG &&
+         msplit_smem_bytes(d.blocks_per_row, true) <= 150 * 1024;
 }
 
 namespace {
@@ -809,6 +1076,15 @@ hipError_t prepare_attention(const Dims& d) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) return e;
   }
+  if (group_attention_msplit_fits(d)) {
+    const int pv_bytes = static_cast<int>(msplit_smem_bytes(d.blocks_per_row, true));
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_msplit_pv<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, pv_bytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_msplit_pv<false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, pv_bytes);
+    if (e != hipSuccess) return e;
+  }
   const size_t bytes = attention_lds_bytes(d);
   if (d.dtype_bytes == 2) {
     if (d.head_dim == 64) return allow_t<bf16_t, 64>(bytes);
@@ -821,6 +1097,22 @@ hipError_t prepare_attention(const Dims& d) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream) {
+  if (a.grouped == 2 && a.split_tiles > 0 && group_attention_msplit_fits(d)) {
+    if (a.sp_scores == nullptr || a.sp_stats == nullptr || a.sp_part == nullptr ||
+        a.split_tiles * kMsRows < a.window)
+      return hipErrorInvalidValue;
+    const int grid = a.B * a.kv_heads * a.split_tiles;
+    const size_t s_smem = msplit_smem_bytes(a.blocks_per_row, false), p_smem = msplit_smem_bytes(a.blocks_per_row, true);
+    if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size) {
+      k_attn_msplit_scores<true><<<grid, kMgThreads, s_smem, stream>>>(a);
+      k_attn_msplit_pv<true><<<grid, kMgThreads, p_smem, stream>>>(a);
+    } else {
+      k_attn_msplit_scores<false><<<grid, kMgThreads, s_smem, stream>>>(a);
+      k_attn_msplit_pv<false><<<grid, kMgThreads, p_smem, stream>>>(a);
+    }
+    k_attn_split_sum<bf16_t><<<(a.B * a.heads * kMgD + 255) / 256, 256, 0, stream>>>(a);
+    return hipGetLastError();
+  }
   if (a.grouped == 2 && group_attention_mfma_fits(d)) {
     const size_t smem = mgroup_smem_bytes(d.groups(), a.window, a.blocks_per_row);
     if (a.bs_shift >= 0 && (1 << a.bs_shift) == a.block_size)

@@ -188,9 +188,10 @@ struct AttnArgs {
   int grouped;             // 1: one workgroup per (row, KV head) (re_attn.hip k_attn_group); 2: the same on
                            // the matrix cores (k_attn_mgroup)
   int packed_out;          // out in the matrix-core path's packed layout (xpack_index, K = NH*d)
-  // > 0: the window split into split_tiles tiles of 256 positions, one
-  // workgroup per (row, head, tile) over three launches (re_attn.hip
-  // k_attn_split_*); only with grouped == 0
+  // > 0: the window split into split_tiles tiles of 256 positions over three
+  // launches: one workgroup per (row, head, tile) with grouped == 0
+  // (re_attn.hip k_attn_split_*), per (row, KV head, tile) with grouped == 2
+  // (k_attn_msplit_*); not with grouped == 1
   int split_tiles;
   float* sp_scores;        // [B*NH][window] scaled scores
   float* sp_stats;         // [B*NH][split_tiles][2] each tile's max and sum of exp(s - max)
@@ -202,6 +203,7 @@ size_t attention_lds_bytes(const Dims& d);
 bool group_attention_default(const Dims& d);
 bool group_attention_fits(const Dims& d);
 bool group_attention_mfma_fits(const Dims& d);
+bool group_attention_msplit_fits(const Dims& d);
 hipError_t prepare_attention(const Dims& d);
 hipError_t launch_attention(const AttnArgs& a, const Dims& d, hipStream_t stream);
 

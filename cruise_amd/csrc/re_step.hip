@@ -841,7 +841,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
     at.bs_shift = (d.block_size & (d.block_size - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(d.block_size)) : -1;
     at.grouped = p.grouped_attn;
     at.packed_out = p.mfma;  // the matrix-core o-projection reads its input packed
-    at.split_tiles = p.grouped_attn == 0 ? p.attn_split : 0;
+    at.split_tiles = p.grouped_attn != 1 ? p.attn_split : 0;
     at.sp_scores = sc.sp_scores;
     at.sp_stats = sc.sp_stats;
     at.sp_part = sc.sp_part;

@@ -76,6 +76,7 @@ def main() -> int:
     p.add_argument("--copy-bytes", type=int, default=0)
     p.add_argument("--tuning", default="", help="JSON object of launch-plan overrides")
     p.add_argument("--capacity", type=int, default=256, help="window positions per row (a multiple of 128)")
+    p.add_argument("--batch", type=int, default=4, help="rows")
     args = p.parse_args()
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.iters)
@@ -91,10 +92,13 @@ def main() -> int:
     if not 1 <= args.context <= capacity:
         raise SystemExit(f"--context must be in [1, {capacity}]")
     bpr = capacity // 128
+    nb = args.batch
+    if nb < 1:
+        raise SystemExit("--batch must be positive")
     cfg = EngineConfig(
         model=ModelSpec(),
         engine=EngineSpec(
-            batch=4, physical_blocks=4 * bpr, block_size=128, blocks_per_row=bpr, logical_capacity=capacity
+            batch=nb, physical_blocks=nb * bpr, block_size=128, blocks_per_row=bpr, logical_capacity=capacity
         ),
         weights=WeightSpec("synthetic", 1, 0.02),
         tuning=json.loads(args.tuning) if args.tuning else {},
@@ -107,7 +111,7 @@ def main() -> int:
         kv_dim = kv_heads * d
         qkv_rows = heads * d + 2 * kv_dim
         ctx = args.context
-        table = np.arange(4 * bpr, dtype=np.int32).reshape(4, bpr)
+        table = np.arange(B * bpr, dtype=np.int32).reshape(B, bpr)
         pos = np.full(B, ctx - 1, np.int64)
         ln = np.full((B, 1), ctx, np.int32)
         slot = np.array([table[r, (ctx - 1) // 128] * 128 + (ctx - 1) % 128 for r in range(B)], dtype=np.int32)

@@ -1,10 +1,12 @@
 """The grouped decode attention of the 64-row step (one Qwen2.5-7B-shape layer
-in bf16, 28 query heads over 4 KV heads, window 1024) on the matrix cores and
-on the vector units, each against the oracle decoder at context lengths on
+in bf16, 28 query heads over 4 KV heads, window 1024) on the matrix cores --
+in one workgroup per (row, KV head), the default, and split over the window
+in 256-position tiles (`{"attention_split": 1}`) -- and on the vector units,
+each against the oracle decoder at context lengths on
 every tile edge: 1, 2, 255, 256, 257, 511, 512, 768, 1023 and 1024 positions
 (a full window), plus random ones, with some rows inactive.
 
-The two versions round at the same points (the bf16 score, its bf16 scaling,
+The versions round at the same points (the bf16 score, its bf16 scaling,
 the bf16 probability, the bf16 output) and differ only in the order of fp32
 sums, so both must meet the model tolerance against the oracle and the greedy
 tokens must match it; the cache writes precede the attention and must be
@@ -43,7 +45,7 @@ def run_step(w, weights, tuning, inputs):
     B = w.geometry.batch
     rt = make_runtime(w, weights, tuning=tuning)
     try:
-        mode = rt.info("grouped_attention")
+        mode = (rt.info("grouped_attention"), rt.info("attention_split"))
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, w.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -75,14 +77,17 @@ def check_versions(w, weights_pair, edges, seed, cache_seed):
         torch.from_numpy(slot), key, value, None, torch.from_numpy(active),
     )
     inputs = (tok, pos, length, slot, active, table, key, value)
+    tiles = (g.window + 255) // 256
     mode_m, got_m = run_step(w, dev, {}, inputs)
+    mode_s, got_s = run_step(w, dev, {"attention_split": 1}, inputs)
     mode_v, got_v = run_step(w, dev, {"attention_mfma": 0}, inputs)
-    assert mode_m == 2 and mode_v == 1
-    for got, what in ((got_m, "matrix cores"), (got_v, "vector units")):
+    assert mode_s == (2, tiles) and mode_m == (2, 0) and mode_v == (1, 0), (mode_s, mode_m, mode_v)
+    for got, what in ((got_s, "matrix cores, split"), (got_m, "matrix cores"), (got_v, "vector units")):
         logits, nxt, gk, gv = got
         assert torch.equal(nxt, ref_next), what
         assert_close_rel(logits, ref_logits.reshape(B, -1), rel_tol(w.dims), f"logits ({what})")
-    assert torch.equal(got_m[2], got_v[2]) and torch.equal(got_m[3], got_v[3])
+    for got in (got_s, got_m):
+        assert torch.equal(got[2], got_v[2]) and torch.equal(got[3], got_v[3])
 
 
 def test_grouped_attention_versions_against_oracle(weights_pair):

@@ -13,8 +13,12 @@ the bf16 output) and differ only in the order of fp32 sums, so both must
 meet the model tolerance against the oracle and the greedy tokens must match
 it; the cache writes precede the attention and must be identical.  A second
 case forces the split on a 512-position window, where the default walks the
-tiles serially.  The engine allows one instance per process, so the
-runtimes run one after the other."""
+tiles serially.  A third runs 16 rows (64 (row, KV head) pairs) at the
+4,096-position window, past the LDS of the single-launch grouped kernels:
+the matrix-core grouped attention split over the window is the default
+there, checked against the oracle and against the per-head split
+(`{"grouped_attention": 0}`).  The engine allows one instance per process,
+so the runtimes run one after the other."""
 from __future__ import annotations
 
 import numpy as np
@@ -31,6 +35,9 @@ pytestmark = pytest.mark.gpu
 W4096 = Workload("qwen7b-1layer-b12-w4096", C2.dims,
                  PagedGeometry(batch=12, physical_blocks=512, block_size=128, blocks_per_row=32, window=4096),
                  eos=C2.eos, seed=C2.seed)
+W4096_B16 = Workload("qwen7b-1layer-b16-w4096", C2.dims,
+                     PagedGeometry(batch=16, physical_blocks=640, block_size=128, blocks_per_row=32, window=4096),
+                     eos=C2.eos, seed=C2.seed)
 W512 = Workload("qwen7b-1layer-b12-w512", C2.dims,
                 PagedGeometry(batch=12, physical_blocks=64, block_size=128, blocks_per_row=4, window=512),
                 eos=C2.eos, seed=C2.seed)
@@ -58,7 +65,8 @@ def run_step(w, weights, tuning, inputs):
         rt.close()
 
 
-def check_split(w, weights_pair, edges, seed, cache_seed, split_tuning, serial_tuning, tiles):
+def check_split(w, weights_pair, edges, seed, cache_seed, split_tuning, serial_tuning, tiles,
+                modes=None):
     dev, cpu = weights_pair
     g = w.geometry
     B, BS, BPR = g.batch, g.block_size, g.blocks_per_row
@@ -81,8 +89,9 @@ def check_split(w, weights_pair, edges, seed, cache_seed, split_tuning, serial_t
     inputs = (tok, pos, length, slot, active, table, key, value)
     mode_s, got_s = run_step(w, dev, split_tuning, inputs)
     mode_t, got_t = run_step(w, dev, serial_tuning, inputs)
-    assert mode_s == (0, tiles) and mode_t == (0, 0), (mode_s, mode_t)
-    for got, what in ((got_s, "split over the window"), (got_t, "serial tiles")):
+    want = modes if modes is not None else ((0, tiles), (0, 0))
+    assert (mode_s, mode_t) == want, (mode_s, mode_t)
+    for got, what in ((got_s, f"{split_tuning} {mode_s}"), (got_t, f"{serial_tuning} {mode_t}")):
         logits, nxt, gk, gv = got
         assert torch.equal(nxt, ref_next), what
         assert_close_rel(logits, ref_logits.reshape(B, -1), rel_tol(w.dims), f"logits ({what})")
@@ -97,3 +106,8 @@ def test_window_split_4096_against_oracle(weights_pair):
 def test_window_split_forced_512_against_oracle(weights_pair):
     check_split(W512, weights_pair, (1, 2, 255, 256, 257, 300, 511, 512), 7402, 770102,
                 {"attention_split": 1}, {}, 2)
+
+
+def test_grouped_split_4096_against_oracle(weights_pair):
+    check_split(W4096_B16, weights_pair, (1, 255, 256, 257, 1024, 2047, 2049, 3000, 4095, 4096), 7403, 770103,
+                {}, {"grouped_attention": 0}, 16, modes=((2, 16), (0, 16)))
