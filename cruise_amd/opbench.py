@@ -16,6 +16,11 @@ Examples::
     python -m cruise_amd.opbench                       # every op of layer 3 + LM head
     python -m cruise_amd.opbench --op gate_up --iters 5
     python -m cruise_amd.opbench --copy-bytes 1073741824
+    python -m cruise_amd.opbench --op attention --batch 64 --capacity 4096 --context 4096
+
+``--batch`` and ``--capacity`` set the rows and the window (blocks of 128);
+``--tuning`` takes the engine's launch-plan overrides, e.g.
+``'{"attention_split": 0}'``.
 """
 from __future__ import annotations
 
