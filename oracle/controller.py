@@ -217,18 +217,21 @@ class EpochController:
         record from the feed after the copy): clear the row's blocks, run the
         decoder at positions 0..L-2 with only this row active, then record
         generation, token prompt[L-1], position L-1, length L.
+
+        Pinned by tests/test_oracle_prefill.py: the written K (post-RoPE) and
+        V of every layer against HF ``Qwen2ForCausalLM`` eager's DynamicCache
+        after the same L-1 tokens, the row's later slots zero, every other
+        block untouched, and the resident record exact; planted mistakes in
+        ``_prefill_positions`` and ``_clear_row_blocks`` fail it.
         """
         g = self.geometry
         B = g.batch
         self.ensure_caches()
         table = np.zeros((B, g.blocks_per_row), dtype=np.int32)
         table[row] = np.asarray(table_row, dtype=np.int32)
-        for local in range(g.blocks_per_row):
-            block = int(table[row, local])
-            self.resident_key[:, block].zero_()
-            self.resident_value[:, block].zero_()
+        self._clear_row_blocks(table[row])
         tiling = torch.zeros(72, dtype=torch.uint8)
-        for p in range(len(prompt) - 1):
+        for p in self._prefill_positions(prompt):
             tok = np.zeros((B, 1), dtype=np.int64)
             pos = np.zeros(B, dtype=np.int64)
             length = np.zeros((B, 1), dtype=np.int32)
@@ -256,6 +259,19 @@ class EpochController:
         self.resident_position[row] = len(prompt) - 1
         self.resident_length[row] = len(prompt)
         self.resident_valid[row] = 1
+
+    @staticmethod
+    def _prefill_positions(prompt: list[int]) -> range:
+        """Positions a prompt of length L writes before the epoch: 0..L-2
+        (the last prompt token is the epoch's first input, CTRL:458-463)."""
+        return range(len(prompt) - 1)
+
+    def _clear_row_blocks(self, table_row) -> None:
+        """Zero every block the row owns in both caches (ClearCacheRow,
+        CTRL:129-147, before the import copy at CTRL:402-405)."""
+        for block in table_row:
+            self.resident_key[:, int(block)].zero_()
+            self.resident_value[:, int(block)].zero_()
 
     def _clear_row(self, cache: torch.Tensor, block_table, row: int) -> None:
         """ClearCacheRow (CTRL:129-147), following the row's table entries (N2)."""

@@ -42,9 +42,10 @@ Parity pinning (tests/test_oracle_decoder.py): the whole step is checked
 against HF ``Qwen2ForCausalLM`` eager (``oracle.hf_reference``, the
 reference's own gate DEC:477-518) at tolerance, with weights that make the
 attention scores O(1); planted mistakes (rotate_half sign, GQA head mapping,
-dropped biases, RoPE base, norm weight, softmax scale) fail that gate; on the
-seeded N(0, 0.02) weights HF eager at bf16 rounds at the same points as DEC
-and most steps agree bit for bit; invariants DEC fixes exactly (masked
+dropped biases, RoPE base, norm weight, softmax scale) fail that gate; in
+bf16 every step's logits and the K/V each layer writes equal HF eager's bit
+for bit, with those weights and with the seeded N(0, 0.02) ones (HF eager
+rounds at DEC's points); invariants DEC fixes exactly (masked
 positions, block placement, slot-write addressing and order, inactive rows,
 row independence) are checked bit for bit.  Parity unpinned: the bf16
 rounding of scores and probabilities kept by the fp32 model (N3, no

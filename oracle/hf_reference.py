@@ -8,7 +8,7 @@ rtol=atol=5e-3 (DEC:34-35).  Here the model is built from a local
 ``Qwen2Config`` (never a downloaded checkpoint) and loaded with the same
 seeded weights as the oracle, so a mistake in the restatement (a dropped
 term, a wrong sign in ``rotate_half``, a transposed operand, a wrong GQA
-head mapping) shows as a logits mismatch.
+head mapping) shows as a logits or K/V mismatch.
 """
 from __future__ import annotations
 
@@ -36,6 +36,12 @@ def build_hf_model(dims: ModelDims, weights: dict[str, torch.Tensor], max_positi
     )
     config.rope_parameters = {"rope_type": "default", "rope_theta": dims.rope_theta}
     model = Qwen2ForCausalLM(config).to(dims.torch_dtype).eval()
+    # ``.to(dtype)`` also casts the rotary ``inv_freq`` buffer; a checkpoint
+    # loaded with ``torch_dtype`` (the reference's gate, DEC:485-491) keeps
+    # it in fp32, as DEC:213-217 computes it.  Restore the fp32 values.
+    rotary = model.model.rotary_emb
+    fp32_inv_freq, _ = rotary.compute_default_rope_parameters(config)
+    rotary.register_buffer("inv_freq", fp32_inv_freq, persistent=False)
     state = {"model.embed_tokens.weight": weights["embedding"], "model.norm.weight": weights["final_norm"], "lm_head.weight": weights["lm_head"]}
     local = {
         "input_norm": "input_layernorm.weight",
@@ -61,13 +67,26 @@ def build_hf_model(dims: ModelDims, weights: dict[str, torch.Tensor], max_positi
     return model
 
 
+def cache_layer(cache, index: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Keys and values [B, KVH, S, d] of one layer of a DynamicCache (the
+    keys are cached after RoPE)."""
+    layer = cache.layers[index]
+    return layer.keys, layer.values
+
+
 @torch.no_grad()
-def hf_incremental_logits(model, token_ids: list[int]) -> list[torch.Tensor]:
-    """One token per call with a growing cache, as DEC:488-518."""
+def hf_incremental(model, token_ids: list[int]) -> tuple[list[torch.Tensor], list[torch.Tensor], list[torch.Tensor]]:
+    """One token per call with a growing cache, as DEC:488-518.
+
+    Returns per step the last logits (fp32 [V]) and, as the reference's gate
+    records them (DEC:506-511), the key and value each layer wrote at that
+    step: [layers, KVH, d] in the model dtype.
+    """
     from transformers import DynamicCache
 
     cache = DynamicCache()
-    out = []
+    logits, keys, values = [], [], []
+    layers = model.config.num_hidden_layers
     for step, token in enumerate(token_ids):
         outputs = model(
             input_ids=torch.tensor([[token]], dtype=torch.int64),
@@ -76,5 +95,8 @@ def hf_incremental_logits(model, token_ids: list[int]) -> list[torch.Tensor]:
             use_cache=True,
         )
         cache = outputs.past_key_values
-        out.append(outputs.logits[0, -1].float().clone())
-    return out
+        logits.append(outputs.logits[0, -1].float().clone())
+        ks, vs = zip(*(cache_layer(cache, i) for i in range(layers)))
+        keys.append(torch.stack([k[0, :, step] for k in ks]).clone())
+        values.append(torch.stack([v[0, :, step] for v in vs]).clone())
+    return logits, keys, values

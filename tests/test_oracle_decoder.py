@@ -11,8 +11,12 @@ Qwen2 (2 layers, GQA 4/2).  Two weight regimes:
   errors in rotate_half, a wrong GQA head mapping, dropped q/k/v biases, a
   wrong RoPE base, a dropped norm weight and a wrong softmax scale all fail it
   by several times the tolerance;
-* the seeded N(0, 0.02) weights of the workloads, where HF eager at bf16
-  rounds at the same points as DEC and most steps agree bit for bit.
+* the seeded N(0, 0.02) weights of the workloads.
+
+In bf16 HF eager rounds at the same points as DEC, so with HF's rotary
+``inv_freq`` kept in fp32 (as a checkpoint loaded in bf16 keeps it, and as
+DEC:213-217 computes it) the oracle's logits and the K/V each layer writes
+equal HF's bit for bit at every step, under both weight regimes.
 
 Invariants the reference's semantics fix exactly (masked positions, block
 placement, slot-write addressing and order, inactive rows, row independence)
@@ -34,14 +38,16 @@ import torch.nn.functional as F
 
 import oracle.decoder as dec_mod
 from oracle.decoder import QWEN25_7B, ModelDims, OracleDecoder, PagedGeometry, weight_shapes
-from oracle.hf_reference import build_hf_model, hf_incremental_logits
+from oracle.hf_reference import build_hf_model, hf_incremental
 from oracle.weights import generate_weights
 from oracle.workloads import C3_DIMS
 
-# max |ours - HF| / max |HF| over each step's logits, sharp weights.  bf16:
-# measured 8.7e-3 (a rounding flip inside a step moves a logit by ~1 ulp,
-# 3.9e-3 relative); fp32: the oracle keeps bf16 scores/probabilities,
-# measured 2.3e-3.  Planted mistakes must exceed PLANT_FACTOR x the gate.
+# max |ours - HF| / max |HF| over each step's logits (and each layer's
+# written K/V), sharp weights.  bf16: measured 0 (bit-identical; the gate
+# leaves room for a one-ulp rounding flip inside a step, ~3.9e-3 relative,
+# on another CPU's bf16 GEMM); fp32: the oracle keeps bf16 scores and
+# probabilities, measured 2.3e-3.  Planted mistakes must exceed
+# PLANT_FACTOR x the gate.
 GATE_BF16 = 1.5e-2
 GATE_FP32 = 5e-3
 PLANT_FACTOR = 3.0
@@ -80,12 +86,14 @@ def weights():
 
 
 @pytest.fixture(scope="module")
-def hf_logits(weights):
-    out = {}
-    for dt in ("fp32", "bf16"):
-        model = build_hf_model(tiny(dt), weights[dt])
-        out[dt] = hf_incremental_logits(model, PROMPT)
-    return out
+def hf_steps(weights):
+    """Per dtype: HF eager's (logits, written keys, written values) per step."""
+    return {dt: hf_incremental(build_hf_model(tiny(dt), weights[dt]), PROMPT) for dt in ("fp32", "bf16")}
+
+
+@pytest.fixture(scope="module")
+def hf_logits(hf_steps):
+    return {dt: steps[0] for dt, steps in hf_steps.items()}
 
 
 def step_inputs(p: int, token: int, row: int = ROW):
@@ -102,17 +110,23 @@ def step_inputs(p: int, token: int, row: int = ROW):
     return tok, pos, ln, slot, act
 
 
-def oracle_incremental(dims: ModelDims, w: dict) -> list[torch.Tensor]:
+def oracle_incremental(dims: ModelDims, w: dict, with_kv: bool = False):
+    """The oracle fed PROMPT one token at a time on row ROW.  Returns the
+    row's logits per step and, with ``with_kv``, the key and value each layer
+    wrote at the step's slot ([layers, KVH, d]), as HF's cache holds them."""
     dec = OracleDecoder(dims, GEO, w)
     k = torch.zeros(dec.cache_shape(), dtype=dims.torch_dtype)
     v = torch.zeros_like(k)
-    out = []
+    out, keys, values = [], [], []
     for p, t in enumerate(PROMPT):
         tok, pos, ln, slot, act = step_inputs(p, t)
         logits, k, v, nxt = dec.forward(tok, pos, ln, TABLE, slot, k, v, None, act)
         assert int(nxt[ROW]) == p + 1
         out.append(logits[ROW, 0].clone())
-    return out
+        s = int(slot[ROW])
+        keys.append(k[:, s // GEO.block_size, s % GEO.block_size].clone())
+        values.append(v[:, s // GEO.block_size, s % GEO.block_size].clone())
+    return (out, keys, values) if with_kv else out
 
 
 def max_rel_err(ours: list[torch.Tensor], ref: list[torch.Tensor]) -> float:
@@ -144,10 +158,26 @@ def test_weight_bundle_shapes():
     assert total == 7_615_616_512  # Qwen2.5-7B parameter count
 
 
+def max_rel_err_per_layer(ours: list[torch.Tensor], ref: list[torch.Tensor]) -> float:
+    """Written K or V ([layers, KVH, d] per step): max |ours - HF| over each
+    layer's step, relative to that layer's max |HF|."""
+    return max(
+        float((a[i].float() - b[i].float()).abs().max()) / float(b[i].float().abs().max())
+        for a, b in zip(ours, ref)
+        for i in range(b.shape[0])
+    )
+
+
 @pytest.mark.parametrize("dtype,gate", [("bf16", GATE_BF16), ("fp32", GATE_FP32)])
-def test_oracle_matches_hf_eager(weights, hf_logits, dtype, gate):
-    err = max_rel_err(oracle_incremental(tiny(dtype), weights[dtype]), hf_logits[dtype])
-    assert err <= gate, f"{dtype}: max rel err {err:.2e} > {gate}"
+def test_oracle_matches_hf_eager(weights, hf_steps, dtype, gate):
+    # DEC:477-518 gates logits and the K/V each step writes.
+    logits, keys, values = oracle_incremental(tiny(dtype), weights[dtype], with_kv=True)
+    ref_logits, ref_keys, ref_values = hf_steps[dtype]
+    err = max_rel_err(logits, ref_logits)
+    assert err <= gate, f"{dtype}: logits max rel err {err:.2e} > {gate}"
+    for name, ours, ref in (("key", keys, ref_keys), ("value", values, ref_values)):
+        err = max_rel_err_per_layer(ours, ref)
+        assert err <= gate, f"{dtype}: written {name} max rel err {err:.2e} > {gate}"
 
 
 def bit_identical_steps(ours, ref) -> float:
@@ -155,15 +185,30 @@ def bit_identical_steps(ours, ref) -> float:
 
 
 def test_oracle_bf16_agrees_bit_for_bit_with_hf_eager_on_seeded_weights():
-    # The workloads' N(0, 0.02) weights: 15 of the 18 steps match bit for bit
-    # on this image; the others carry a one-ulp flip of a single rounding.
+    # The workloads' N(0, 0.02) weights: every step's logits and written K/V.
     dims = tiny("bf16")
     w = generate_weights(dims, 11)
-    ref = hf_incremental_logits(build_hf_model(dims, w), PROMPT)
-    ours = oracle_incremental(dims, w)
-    assert max_rel_err(ours, ref) <= GATE_BF16
-    frac = bit_identical_steps(ours, ref)
-    assert frac >= 2 / 3, f"only {frac:.0%} of steps bit-identical"
+    ref = hf_incremental(build_hf_model(dims, w), PROMPT)
+    ours = oracle_incremental(dims, w, with_kv=True)
+    assert max_rel_err(ours[0], ref[0]) <= GATE_BF16
+    for name, a, b in zip(("logits", "key", "value"), ours, ref):
+        frac = bit_identical_steps(a, b)
+        assert frac == 1.0, f"{name}: only {frac:.0%} of steps bit-identical"
+
+
+def test_oracle_bf16_agrees_bit_for_bit_with_hf_eager_on_sharp_weights(weights, hf_steps):
+    ours = oracle_incremental(tiny("bf16"), weights["bf16"], with_kv=True)
+    for name, a, b in zip(("logits", "key", "value"), ours, hf_steps["bf16"]):
+        frac = bit_identical_steps(a, b)
+        assert frac == 1.0, f"{name}: only {frac:.0%} of steps bit-identical"
+
+
+def test_hf_rotary_frequencies_stay_fp32():
+    # A model cast with .to(bf16) would round inv_freq to bf16; the
+    # reference's gate loads the checkpoint in bf16, where it stays fp32.
+    model = build_hf_model(tiny("bf16"), generate_weights(tiny("bf16"), 1))
+    assert model.model.rotary_emb.inv_freq.dtype == torch.float32
+    assert torch.equal(model.model.rotary_emb.inv_freq, dec_mod.inv_freq(tiny("bf16")))
 
 
 def _plant_rotate_half(mp):
