@@ -49,6 +49,8 @@ def parse_args():
     p.add_argument("--cpu-epochs", type=int, default=5, help="timed K=8 epochs of the CPU baseline")
     p.add_argument("--kernel-epochs", type=int, default=10)
     p.add_argument("--kernel-passes", type=int, default=4, help="passes over the 28 layers' gate/up launches")
+    p.add_argument("--sweep-epochs", type=int, default=20,
+                   help="timed epochs at each of K=1, 2, 4 (the K sweep beside the K=8 headline; 0 skips it)")
     p.add_argument("--workload", choices=("qwen7b-b4", "scaled-b64"), default="qwen7b-b4",
                    help="qwen7b-b4: the headline line; scaled-b64: one Qwen2.5-7B layer at 64 rows, contexts "
                         "256-1016, K=8 (a separate line, not the headline)")
@@ -112,7 +114,7 @@ def main() -> int:
     walls = []
     host_ms = []
 
-    def run_epoch(timed: bool) -> None:
+    def run_epoch(timed: bool, K: int = K, sink: dict | None = None) -> None:
         nonlocal executed_total
         for r in range(B):
             if positions[r] + K > capacity:
@@ -133,11 +135,36 @@ def main() -> int:
             executed_total += int(out.executed.sum())
             walls.append(out.wall_us)
             host_ms.append((h1 - h0) * 1e3)
+        if sink is not None:
+            sink["executed"] += int(out.executed.sum())
+            sink["host_ms"].append((h1 - h0) * 1e3)
+
+    def k_sweep_line(Kx: int, epochs: int) -> dict:
+        """tok/s, ms per epoch and per decoder step, and the host-control
+        wall of ``epochs`` K=Kx epochs on the same engine and rows (rows that
+        would reach the capacity restart before the timed region)."""
+        for r in range(B):
+            if positions[r] + Kx * (epochs + 2) > capacity:
+                start_row(r)
+        for _ in range(2):
+            run_epoch(False, Kx)
+        sink = {"executed": 0, "host_ms": []}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(epochs):
+            run_epoch(False, Kx, sink)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        steps = sink["executed"] / B
+        return {"tok_s": round(sink["executed"] / dt, 1), "ms_per_epoch": round(dt * 1e3 / epochs, 4),
+                "ms_per_decoder_step": round(dt * 1e3 / steps, 4) if steps else None,
+                "host_control_wall_ms_p50": round(statistics.median(sink["host_ms"]), 4), "epochs": epochs,
+                "tokens": sink["executed"]}
+
+    import torch
 
     for _ in range(args.warmup):
         run_epoch(False)
-    import torch
-
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for _ in range(args.steps):
@@ -165,6 +192,17 @@ def main() -> int:
     torch.cuda.synchronize()
     in_epoch = rt.timed_launch_ms()
     rt.enable_kernel_timing(False)
+    # the K sweep (untimed for the headline): the same rows at K = 1, 2, 4
+    k_sweep = {}
+    if args.sweep_epochs > 0:
+        for Kx in (1, 2, 4):
+            k_sweep[str(Kx)] = k_sweep_line(Kx, args.sweep_epochs)
+            log(f"K={Kx}: {k_sweep[str(Kx)]['tok_s']} tok/s, {k_sweep[str(Kx)]['ms_per_epoch']} ms/epoch, "
+                f"host-control wall {k_sweep[str(Kx)]['host_control_wall_ms_p50']} ms")
+        k_sweep[str(K)] = {"tok_s": round(tok_s, 1), "ms_per_epoch": round(ms_per_epoch, 4),
+                           "ms_per_decoder_step": round(ms_per_decoder_step, 4),
+                           "host_control_wall_ms_p50": round(statistics.median(host_ms), 4), "epochs": args.steps,
+                           "tokens": executed_total}
     inter = rt.info("intermediate")
     hidden = rt.info("hidden")
     k_bytes = 2 * inter * hidden * 2 + hidden * 2 + B * hidden * 2 + B * inter * 2
@@ -206,6 +244,7 @@ def main() -> int:
         "host_control_wall_ms_p50": round(statistics.median(host_ms), 4),
         "native_wall_us_p50": int(statistics.median(walls)),
         "epoch_graph_nodes": nodes,
+        "k_sweep": k_sweep or None,
         "copy_dispatches_between_epochs_in_trace": epoch_trace_copies(),
         "roofline": {
             "bound": "hbm",
@@ -292,8 +331,11 @@ def bench_scaled(args) -> int:
     kv_bytes = int(B * mean_ctx * kv_dim * 2 * 2)
     step_bytes = rt.info("streamed_weight_bytes") + kv_bytes + B * rt.vocab * 4
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
-    # the LM head op (its RMSNorm, the matrix-core projection and the argmax
-    # fold), launched alone between HIP events on the engine stream
+    # the LM head op (its RMSNorm and the matrix-core projection with its
+    # argmax partials, plus a fold launch on the alternative plan), launched
+    # alone between HIP events on the engine stream
+    lm_kernel = ("k_mf_norm + k_mf_lm_cu (per-CU argmax partials)" if rt.info("lm_cu")
+                 else "k_mf_norm + k_mgemv<2,4,LmHead> + k_mf_fold")
     lm_op = rt.info("step_ops") - 1
     lm_ms = rt.time_ops(lm_op, lm_op + 1, iters=20)
     hidden = rt.info("hidden")
@@ -325,7 +367,7 @@ def bench_scaled(args) -> int:
         "step_bytes": step_bytes,
         "step_gbs": round(step_gbs, 1),
         "step_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "LM head op (RMSNorm + k_mgemv<2,4,LmHead> + argmax fold), alone",
+        "roofline": {"bound": "hbm", "kernel": f"LM head op ({lm_kernel}), alone",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(lm_ms * 1e3, 2),
                      "algorithmic_bytes_per_launch": lm_bytes},
@@ -411,50 +453,22 @@ def traffic_bytes():
         return None
 
 
-def cpu_baseline(rt, epochs: int, warmup: int = 2):
-    """The oracle's CPU decoder path (oracle/controller.py over
-    oracle/decoder.py: the reference's controller loop and PyTorch decoder,
-    bf16, full 7B shape) on the host cores, run as the bench runs: four rows
-    prefilled with 2-5 token prompts, then K=8 epochs of the controller, each
-    8 decoder steps for 4 rows; ``warmup`` epochs, then the median of
-    ``epochs`` timed epochs.  Weights are copied from the engine."""
-    import torch
-
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.controller import ControllerGeometry, EpochController, EpochFeed, control_input_elements
-    from oracle.decoder import OracleDecoder, PagedGeometry, QWEN25_7B, weight_shapes
+def _cpu_epochs(ctl, tokens, positions, gens, table, K: int, eos: int, warmup: int, epochs: int):
+    """``warmup`` then ``epochs`` timed K-step epochs of the oracle controller
+    on rows that continue from ``tokens``/``positions`` (updated in place).
+    Returns the epoch times and the tokens each produced."""
+    from oracle.controller import EpochFeed, control_input_elements
     from cruise_amd.runtime import tiling_bytes
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    t0 = time.time()
-    weights = {}
-    for name, shape in weight_shapes(QWEN25_7B).items():
-        t = torch.empty(shape, dtype=torch.bfloat16)
-        rt.read_state(name, t)
-        weights[name] = t
-    log(f"cpu baseline: weights on host in {time.time() - t0:.1f}s, {cores} threads")
-    B, K, cap = 4, 8, 256
-    geo = PagedGeometry(batch=B, physical_blocks=8, block_size=128, blocks_per_row=2, window=cap)
-    dec = OracleDecoder(QWEN25_7B, geo, weights)
-    cg = ControllerGeometry(batch=B, capacity=cap, physical_blocks=8, blocks_per_row=2, block_size=128,
-                            vocab=QWEN25_7B.vocab, num_layers=QWEN25_7B.num_layers)
-    ctl = EpochController(cg, dec.forward, dec.cache_shape(), torch.bfloat16)
-    rng = np.random.default_rng(7)
-    table = np.arange(8, dtype=np.int32).reshape(B, 2)
-    tokens = np.zeros(B, dtype=np.int64)
-    positions = np.zeros(B, dtype=np.int64)
-    for r in range(B):
-        prompt = list(map(int, rng.integers(0, QWEN25_7B.vocab, size=int(rng.integers(2, 6)))))
-        ctl.prefill_row(r, r + 1, prompt, table[r])
-        tokens[r], positions[r] = prompt[-1], len(prompt) - 1
+    B, bpr = table.shape
+    bs = ctl.geometry.block_size
     control = np.zeros(control_input_elements(B), dtype=np.int32)
     control[0] = K
-    control[1 : 1 + B] = EOS
-    control[3 + B :] = np.arange(1, B + 1)
+    control[1 : 1 + B] = eos
+    control[3 + B :] = gens
     times, produced = [], []
     for e in range(warmup + epochs):
-        slots = (table[:, 0] * 128 + positions).astype(np.int32)
+        slots = np.array([table[r, positions[r] // bs] * bs + positions[r] % bs for r in range(B)], dtype=np.int32)
         feed = EpochFeed(tokens.copy(), positions.copy(), (positions + 1).astype(np.int32), slots,
                          np.ones(B, dtype=np.int32), table.reshape(-1), tiling_bytes(), control)
         t1 = time.perf_counter()
@@ -470,8 +484,84 @@ def cpu_baseline(rt, epochs: int, warmup: int = 2):
         if e >= warmup:
             times.append(dt)
             produced.append(int(executed.sum()))
+    return times, produced
+
+
+def _cpu_line(times, produced, K: int) -> dict:
+    med = statistics.median(times)
+    tok = statistics.median(produced)
+    return {"tok_s": round(tok / med, 3), "median_epoch_s": round(med, 4), "ms_per_decoder_step": round(1e3 * med / K, 2),
+            "epochs": len(times), "tokens_per_epoch": tok}
+
+
+def _prefilled_controller(dims, weights, geo_args, B: int, seed: int, prompt_vocab: int):
+    """The oracle controller with every row prefilled from a 2-5 token prompt."""
+    import torch
+
+    from oracle.controller import ControllerGeometry, EpochController
+    from oracle.decoder import OracleDecoder, PagedGeometry
+
+    P, BS, BPR, cap = geo_args
+    geo = PagedGeometry(batch=B, physical_blocks=P, block_size=BS, blocks_per_row=BPR, window=cap)
+    dec = OracleDecoder(dims, geo, weights)
+    cg = ControllerGeometry(batch=B, capacity=cap, physical_blocks=P, blocks_per_row=BPR, block_size=BS,
+                            vocab=dims.vocab, num_layers=dims.num_layers)
+    ctl = EpochController(cg, dec.forward, dec.cache_shape(), dims.torch_dtype)
+    rng = np.random.default_rng(seed)
+    table = np.arange(B * BPR, dtype=np.int32).reshape(B, BPR)
+    tokens = np.zeros(B, dtype=np.int64)
+    positions = np.zeros(B, dtype=np.int64)
+    for r in range(B):
+        prompt = list(map(int, rng.integers(0, prompt_vocab, size=int(rng.integers(2, 6)))))
+        ctl.prefill_row(r, r + 1, prompt, table[r])
+        tokens[r], positions[r] = prompt[-1], len(prompt) - 1
+    return ctl, table, tokens, positions, np.arange(1, B + 1)
+
+
+def cpu_baseline(rt, epochs: int, warmup: int = 2):
+    """The oracle's CPU decoder path (oracle/controller.py over
+    oracle/decoder.py: the reference's controller loop and PyTorch decoder,
+    bf16, full 7B shape) on the host cores, run as the bench runs: four rows
+    prefilled with 2-5 token prompts, then K=8 epochs of the controller, each
+    8 decoder steps for 4 rows; ``warmup`` epochs, then the median of
+    ``epochs`` timed epochs.  Weights are copied from the engine.  The same
+    rows then continue at K=1, 2 and 4, and the tiny fp32 model (2 layers,
+    hidden 256) runs K=2 epochs: the legs of the K sweep."""
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle.decoder import QWEN25_7B, weight_shapes
+    from oracle.weights import generate_weights
+    from oracle.workloads import C1
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t0 = time.time()
+    weights = {}
+    for name, shape in weight_shapes(QWEN25_7B).items():
+        t = torch.empty(shape, dtype=torch.bfloat16)
+        rt.read_state(name, t)
+        weights[name] = t
+    log(f"cpu baseline: weights on host in {time.time() - t0:.1f}s, {cores} threads")
+    B, K = 4, 8
+    ctl, table, tokens, positions, gens = _prefilled_controller(QWEN25_7B, weights, (8, 128, 2, 256), B, 7,
+                                                                QWEN25_7B.vocab)
+    sweep = {}
+    times, produced = _cpu_epochs(ctl, tokens, positions, gens, table, K, EOS, warmup, epochs)
+    sweep[str(K)] = _cpu_line(times, produced, K)
     med = statistics.median(times)
     tok_per_epoch = statistics.median(produced)
+    log(f"cpu baseline: {epochs} timed K=8 epochs, median {med:.3f}s for {tok_per_epoch} tokens")
+    for Kx in (1, 2, 4):
+        sweep[str(Kx)] = _cpu_line(*_cpu_epochs(ctl, tokens, positions, gens, table, Kx, EOS, warmup, epochs), Kx)
+        log(f"cpu baseline: K={Kx}: {sweep[str(Kx)]['tok_s']} tok/s")
+    del ctl, weights
+    tiny_w = generate_weights(C1.dims, C1.seed)
+    g = C1.geometry
+    tctl, ttable, ttok, tpos, tgens = _prefilled_controller(C1.dims, tiny_w, (g.physical_blocks, g.block_size,
+                                                            g.blocks_per_row, g.window), g.batch, C1.seed, C1.dims.vocab)
+    tiny = _cpu_line(*_cpu_epochs(tctl, ttok, tpos, tgens, ttable, 2, C1.eos, warmup, epochs), 2)
+    log(f"cpu baseline: tiny fp32 K=2: {tiny['tok_s']} tok/s")
     cpu_name = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -481,7 +571,6 @@ def cpu_baseline(rt, epochs: int, warmup: int = 2):
                     break
     except OSError:
         pass
-    log(f"cpu baseline: {epochs} timed K=8 epochs, median {med:.3f}s for {tok_per_epoch} tokens")
     return {
         "value": round(tok_per_epoch / med, 3),
         "unit": "tok/s",
@@ -491,6 +580,8 @@ def cpu_baseline(rt, epochs: int, warmup: int = 2):
                    f"{cpu_name}: {warmup} warm-up then {epochs} timed K=8 epochs after 2-5 token prompts; "
                    f"median epoch {med:.3f}s for {tok_per_epoch} tokens"),
         "median_epoch_s": round(med, 4),
+        "k_sweep": sweep,
+        "tiny_fp32_k2": dict(tiny, model="2 layers, hidden 256, GQA 4/2, head_dim 64, vocab 4096, fp32, B=4"),
     }
 
 

@@ -55,7 +55,8 @@ std::mutex g_noalloc_mutex;
 uint8_t* g_noalloc_ptr[kMaxDevices] = {};
 
 // Resolves the array's address on `device`, which must be current; once per
-// device (at engine creation).  False on a HIP error.
+// device (on the no-allocation entry point's first call there).  False on a
+// HIP error.
 bool noalloc_setup(int device) {
   if (device < 0 || device >= kMaxDevices) return false;
   std::lock_guard<std::mutex> lock(g_noalloc_mutex);
@@ -1044,10 +1045,6 @@ extern "C" void* resident_epoch_create(const char* air_path, const char* graph_c
     return nullptr;
   }
   e->device = 0;
-  if (!noalloc_setup(e->device)) {  // the no-allocation scratch's address on this device
-    *status = kCreateRuntime;
-    return nullptr;
-  }
   hipDeviceProp_t prop{};
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess && prop.multiProcessorCount > 0)
     e->cus = prop.multiProcessorCount;
@@ -1629,6 +1626,9 @@ extern "C" int32_t resident_epoch_prefill_batch_noalloc(void* engine, int32_t n_
   PrefillRequest req;
   if (e == nullptr || !parse_prefill(e->dims, n_rows, rows, generations, prompts, prompt_lens, block_tables, req))
     return -1;
+  // The array's address on the engine's device, resolved on this entry
+  // point's first call there (resolving allocates nothing).
+  if (hipSetDevice(e->device) != hipSuccess || !noalloc_setup(e->device)) return -2;
   uint8_t* scratch_ptr = noalloc_scratch(e->device);
   if (scratch_ptr == nullptr) return -2;
   std::lock_guard<std::mutex> lock(e->execute_mutex);
@@ -1821,7 +1821,7 @@ extern "C" int32_t resident_epoch_time_layer_op(void* engine, int32_t which, int
   std::lock_guard<std::mutex> lock(e->execute_mutex);
   const KernelEnv env = e->env();
   const int per_layer = (step_op_count(env) - 2) / e->dims.layers;
-  if (which < 0 || which >= per_layer) return -1;
+  if (which < 0 || which >= per_layer || !layer_op_launches(env, which)) return -1;
   if (e->dec_key == nullptr) {
     if (hipMalloc(&e->dec_key, e->cache_bytes) != hipSuccess) return -2;
     if (hipMalloc(&e->dec_value, e->cache_bytes) != hipSuccess) return -2;

@@ -233,6 +233,7 @@ struct KernelEnv {
 hipError_t launch_decoder_step(const KernelEnv& env, const StepPtrs& step, hipStream_t stream);
 hipError_t launch_step_ops(const KernelEnv& env, const StepPtrs& step, hipStream_t stream, int begin, int end);
 int step_op_count(const KernelEnv& env);
+bool layer_op_launches(const KernelEnv& env, int which);
 // The op whose launch the epoch timing brackets: layer's gate/up projection.
 int timed_op_index(const KernelEnv& env, int layer);
 // Grid sizes of the grid-stride projections from the kernels' occupancy.

@@ -1045,6 +1045,21 @@ void plan_grids(LaunchPlan& p, const Dims& d, int cus) {
 }
 
 int step_op_count(const KernelEnv& env) { return 2 + kOpsPerLayer * env.dims.layers; }
+
+// Whether per-layer op `which` launches a kernel under the engine's plan: the
+// o- and down-reduce entries launch only when their projection runs split-K
+// on the row-tiled path (the whole-K down and the matrix-core path reduce
+// inside the projection).
+bool layer_op_launches(const KernelEnv& env, int which) {
+  const LaunchPlan& p = env.plan;
+  constexpr int kOReduceOp = 3, kDownReduceOp = 6;
+  if (which == kOReduceOp) return !p.mfma && p.o_segments > 1;
+  if (which == kDownReduceOp) {
+    const bool down_whole = env.dims.dtype_bytes == 2 && p.mb == 4 && p.down_whole_grid > 0;
+    return !p.mfma && !down_whole && p.down_segments > 1;
+  }
+  return which >= 0 && which < kOpsPerLayer;
+}
 int timed_op_index(const KernelEnv& env, int layer) {
   (void)env;
   return 1 + kOpsPerLayer * layer + kGateUpOp;

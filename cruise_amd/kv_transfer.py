@@ -1,50 +1,74 @@
-"""Paged-KV transfer into the resident epoch: host snapshot files and
-device-to-device transfer through HIP IPC.
+"""Handing a prefilled row's KV to the resident epoch.
 
-Mirrors src/vllm_ascend_resident_epoch/kv_transfer.py.  A prefilled row
-enters device ownership by importing one KV block per layer (its first
-block, positions 0..block_size-1) from the stock cache the prompt was
-prefilled into:
+A row that was prefilled outside the device program (stock prefill into a
+paged cache) becomes device-owned by importing its first KV block of every
+layer: positions 0..block_size-1, the only block a prompt that fits the
+epoch's window occupies.  Two transports exist:
 
-* host snapshot: the blocks are gathered into one payload
-  ``[K|V][layer][row][block_size, kv_heads, head]`` and written to a file
-  under /dev/shm with an 80-byte header (kv_transfer.py:31, 431-466); the
-  engine reads it, imports it with the epoch's one feed copy and proves the
-  import with an Adler-32 of the imported bytes (kv_transfer.py:159-174).
-* device IPC: only metadata crosses the process boundary (4,088 bytes,
-  kv_transfer.py:33-34, 67-137): for each of the 2 x layers caches an IPC
-  handle of the allocation holding it and the cache's offset inside it, plus
-  the scheduler block of every imported row.  The engine opens the handles
-  once and copies the blocks device to device.
+* **host snapshot** -- the selected blocks travel through a file under
+  /dev/shm that the engine reads into the epoch's one feed copy;
+* **device IPC** -- only a 4,088-byte record crosses the process boundary:
+  one HIP IPC handle per K and V cache of every layer, each cache's offset in
+  its allocation, and the scheduler block of every imported row.  The engine
+  maps the handles once and gathers the blocks on the device.
 
-The one difference from the reference is the key: an Ascend IPC key is an
-ASCII name, a HIP IPC handle is a 64-byte binary record
-(``hipIpcMemHandle_t``), so ``DeviceKVTransfer.keys`` holds 64-byte
-``bytes`` values, written to the same 64-byte slots of the record.
+What must match the engine and the reference's callers byte for byte, and is
+kept for that reason only (src/vllm_ascend_resident_epoch/kv_transfer.py:
+14-34, 159-174):
+
+* the 80-byte snapshot header ``<QIIQQI4i7I`` (magic "CRUISEKV", version 1)
+  followed by the payload ``[K | V][layer][row][block]``;
+* the IPC record: header ``<QIIQ4i4i56Q`` (magic "CRUISEIP", version 2) and
+  56 key slots of 64 bytes;
+* the payload checksum: Adler-32 over the selected rows' blocks, K before V,
+  layer-major, rows ascending.  The device recomputes it over the bytes it
+  imported and the host compares.
+
+A HIP IPC handle (``hipIpcMemHandle_t``) is a 64-byte binary record, so a
+key slot holds those 64 bytes where an Ascend key was an ASCII name.
+
+The rest is this module's own:
+
+* the checksum is one ``zlib.adler32`` over a fancy-indexed numpy view
+  ``payload[:, :, rows]``, whose C order is exactly the order above;
+* both transfers validate through one rule table each (``TransferError``
+  names the broken rule), sharing the row-selection rules;
+* a snapshot is gathered on the caches' device with ``index_select`` and
+  reaches the host as one copy per cache (K, V) for all layers;
+* the snapshot file is written through ``mkstemp`` in the target directory,
+  fsynced and renamed into place, so a reader never sees a partial file and
+  concurrent writers never collide;
+* IPC exports live in a small registry keyed by the caches' addresses and
+  their allocations, so a moved or reallocated cache is exported afresh.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import secrets
 import struct
+import tempfile
 import zlib
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from functools import lru_cache
 from pathlib import Path
-from typing import Any
+from typing import Any, Callable, Iterable
+
+import numpy as np
 
 TRANSFER_MAGIC = 0x4352554953454B56  # "CRUISEKV"
 TRANSFER_VERSION = 1
 TRANSFER_HEADER_BYTES = 80
 IPC_METADATA_MAGIC = 0x4352554953454950  # "CRUISEIP"
 IPC_METADATA_VERSION = 2
-IPC_KEY_BYTES = 64  # also sizeof(hipIpcMemHandle_t)
+IPC_KEY_BYTES = 64  # sizeof(hipIpcMemHandle_t)
 
 
 @dataclass(frozen=True)
 class KVGeometry:
-    """Shape of the imported blocks (Qwen2.5-7B at B=4 by default)."""
+    """Shape of the imported blocks; Qwen2.5-7B at B=4 by default."""
 
     layers: int = 28
     batch: int = 4
@@ -63,7 +87,7 @@ class KVGeometry:
 
     @property
     def cache_bytes(self) -> int:
-        """Bytes of one cache (K or V) of the payload."""
+        """Bytes of the K (or V) half of a payload."""
         return self.layers * self.batch * self.block_bytes
 
     @property
@@ -72,11 +96,13 @@ class KVGeometry:
 
     @property
     def key_count(self) -> int:
+        """Caches a device transfer names: K and V of every layer."""
         return 2 * self.layers
 
 
 QWEN7B_B4 = KVGeometry()
 
+# The reference geometry's sizes, as its callers import them.
 LAYERS = QWEN7B_B4.layers
 GRAPH_BATCH_SIZE = QWEN7B_B4.batch
 BLOCK_SIZE = QWEN7B_B4.block_size
@@ -88,45 +114,73 @@ ROW_BYTES = 2 * QWEN7B_B4.block_bytes
 PAYLOAD_BYTES = QWEN7B_B4.payload_bytes
 IPC_KEY_COUNT = QWEN7B_B4.key_count
 
-# Little-endian records: the snapshot header and the IPC metadata header
-# (kv_transfer.py:31, 33).
 HEADER = struct.Struct("<QIIQQI4i7I")
 IPC_METADATA_HEADER = struct.Struct(f"<QIIQ4i4i{IPC_KEY_COUNT}Q")
 IPC_METADATA_BYTES = IPC_METADATA_HEADER.size + IPC_KEY_COUNT * IPC_KEY_BYTES
 assert HEADER.size == TRANSFER_HEADER_BYTES and IPC_METADATA_BYTES == 4088
 
 
-def _check(condition: bool, message: str) -> None:
-    if not condition:
-        raise ValueError(message)
+class TransferError(ValueError):
+    """A transfer record broke one of its rules (``rule`` names it)."""
+
+    def __init__(self, rule: str, detail: str):
+        super().__init__(f"{detail} [{rule}]")
+        self.rule = rule
 
 
-def _check_mask_and_generations(mask: int, generations: tuple[int, ...], rows: int, what: str) -> None:
-    _check(len(generations) == rows, f"{what} generation vector must have {rows} rows")
-    _check(0 < mask < 1 << rows, f"{what} mask must select at least one row")
+Rule = tuple[str, Callable[[Any], bool], str]
+
+
+def _enforce(rules: Iterable[Rule], record: Any) -> None:
+    for name, holds, detail in rules:
+        if not holds(record):
+            raise TransferError(name, detail)
+
+
+# ---------------------------------------------------------------------------
+# Payload view and checksum
+# ---------------------------------------------------------------------------
+def selected_rows(mask: int, batch: int) -> list[int]:
+    return [row for row in range(batch) if mask >> row & 1]
+
+
+def payload_blocks(payload: bytes, geometry: KVGeometry) -> np.ndarray:
+    """The payload as uint8 [2 (K, V), layers, batch, block_bytes]."""
+    g = geometry
+    if len(payload) != g.payload_bytes:
+        raise TransferError("payload-size", f"a payload of this geometry has {g.payload_bytes} bytes, not {len(payload)}")
+    return np.frombuffer(payload, dtype=np.uint8).reshape(2, g.layers, g.batch, g.block_bytes)
 
 
 def kv_payload_checksum(payload: bytes, import_mask: int, geometry: KVGeometry = QWEN7B_B4) -> int:
-    """Adler-32 over the imported blocks: the K cache, then the V cache, each
-    layer-major and, inside a layer, in ascending row order over the rows of
-    import_mask (kv_transfer.py:159-174; the engine's device checksum sums
-    the same bytes)."""
-    g = geometry
-    _check(len(payload) == g.payload_bytes, "cannot checksum an incomplete KV transfer payload")
-    view = memoryview(payload)
-    value = 1
-    rows = [r for r in range(g.batch) if import_mask & (1 << r)]
-    for cache in range(2):
-        for layer in range(g.layers):
-            for row in rows:
-                start = cache * g.cache_bytes + (layer * g.batch + row) * g.block_bytes
-                value = zlib.adler32(view[start : start + g.block_bytes], value)
-    return value & 0xFFFFFFFF
+    """Adler-32 of the selected rows' blocks, K before V, layer-major, rows
+    ascending: the C order of ``blocks[:, :, rows]``."""
+    rows = selected_rows(import_mask, geometry.batch)
+    picked = np.ascontiguousarray(payload_blocks(payload, geometry)[:, :, rows])
+    return zlib.adler32(memoryview(picked).cast("B")) & 0xFFFFFFFF
 
 
+# ---------------------------------------------------------------------------
+# Row selection, shared by both transfers
+# ---------------------------------------------------------------------------
+def _selection_rules(batch_of: Callable[[Any], int]) -> tuple[Rule, ...]:
+    return (
+        ("transfer-id", lambda t: t.transfer_id > 0, "a transfer id is a positive integer"),
+        ("generation-count", lambda t: len(t.row_generations) == batch_of(t),
+         "the generation vector has one entry per graph row"),
+        ("mask-range", lambda t: 0 < t.import_mask < 1 << batch_of(t),
+         "the import mask selects one or more of the graph's rows and nothing else"),
+        ("generation-sign", lambda t: min(t.row_generations) >= 0, "generations are never negative"),
+    )
+
+
+# ---------------------------------------------------------------------------
+# Host snapshot
+# ---------------------------------------------------------------------------
 @dataclass(frozen=True)
 class ResidentKVSnapshot:
-    """A host copy of the imported blocks (kv_transfer.py:37-64)."""
+    """The selected rows' blocks copied to the host, with their checksum
+    (unselected rows' blocks are zero)."""
 
     transfer_id: int
     import_mask: int
@@ -135,31 +189,100 @@ class ResidentKVSnapshot:
     checksum: int
     geometry: KVGeometry = field(default=QWEN7B_B4)
 
+    RULES = _selection_rules(lambda s: s.geometry.batch) + (
+        ("generation-selects-row",
+         lambda s: all((s.import_mask >> r & 1) == (gen > 0) for r, gen in enumerate(s.row_generations)),
+         "exactly the rows with a generation are selected"),
+        ("payload-size", lambda s: len(s.payload) == s.geometry.payload_bytes,
+         "the payload holds every row's block of every layer, K then V"),
+        ("checksum", lambda s: s.checksum == kv_payload_checksum(s.payload, s.import_mask, s.geometry),
+         "the checksum is not the payload's"),
+    )
+
     def validate(self) -> None:
+        _enforce(self.RULES, self)
+
+    def header(self) -> bytes:
         g = self.geometry
-        _check(self.transfer_id > 0, "KV transfer id must be positive")
-        _check_mask_and_generations(self.import_mask, tuple(self.row_generations), g.batch, "KV transfer")
-        _check(all(gen >= 0 for gen in self.row_generations), "KV transfer generations must be non-negative")
-        for row, gen in enumerate(self.row_generations):
-            _check(bool(self.import_mask & (1 << row)) == (gen > 0), "KV transfer mask and generations disagree")
-        _check(
-            len(self.payload) == g.payload_bytes,
-            f"KV transfer payload must be {g.payload_bytes} bytes, got {len(self.payload)}",
+        return HEADER.pack(
+            TRANSFER_MAGIC, TRANSFER_VERSION, TRANSFER_HEADER_BYTES, self.transfer_id, len(self.payload),
+            self.import_mask, *self.row_generations,
+            g.layers, g.batch, g.block_size, g.kv_heads, g.head_size, g.element_bytes, self.checksum,
         )
-        _check(
-            self.checksum == kv_payload_checksum(self.payload, self.import_mask, g),
-            "KV transfer checksum does not match its payload",
-        )
+
+    @classmethod
+    def parse(cls, raw: bytes) -> "ResidentKVSnapshot":
+        if len(raw) < TRANSFER_HEADER_BYTES:
+            raise TransferError("file-size", "the file ends inside its header")
+        magic, version, header_bytes, transfer_id, payload_bytes, mask, *rest = HEADER.unpack_from(raw)
+        gens, dims, checksum = tuple(rest[:4]), rest[4:10], rest[10]
+        if (magic, version, header_bytes) != (TRANSFER_MAGIC, TRANSFER_VERSION, TRANSFER_HEADER_BYTES):
+            raise TransferError("magic", "not a version-1 KV snapshot file")
+        if len(raw) != header_bytes + payload_bytes:
+            raise TransferError("file-size", "the file size disagrees with its header")
+        snapshot = cls(transfer_id, mask, gens, bytes(raw[header_bytes:]), checksum, KVGeometry(*dims))
+        snapshot.validate()
+        return snapshot
+
+
+def _under_dev_shm(path: Path) -> bool:
+    return path.parts[:3] == ("/", "dev", "shm") and len(path.parts) > 3
+
+
+def write_kv_snapshot(path: str | Path, snapshot: ResidentKVSnapshot) -> None:
+    """Publish a snapshot at ``path`` (under /dev/shm, where the engine reads
+    transfer files): written to a fresh temporary file in the same directory,
+    fsynced, then renamed over ``path``."""
+    snapshot.validate()
+    target = Path(path).resolve()
+    if not _under_dev_shm(target):
+        raise TransferError("location", f"the engine reads transfer files under /dev/shm only, not {target}")
+    target.parent.mkdir(parents=True, exist_ok=True)
+    fd, staging = tempfile.mkstemp(dir=target.parent, prefix=f".{target.name}.", suffix=".partial")
+    try:
+        with os.fdopen(fd, "wb") as out:
+            out.write(snapshot.header())
+            out.write(snapshot.payload)
+            out.flush()
+            os.fsync(out.fileno())
+        os.replace(staging, target)
+    except BaseException:
+        with contextlib.suppress(FileNotFoundError):
+            os.unlink(staging)
+        raise
+
+
+def read_kv_snapshot(path: str | Path) -> ResidentKVSnapshot:
+    return ResidentKVSnapshot.parse(Path(path).read_bytes())
+
+
+# ---------------------------------------------------------------------------
+# Device IPC record
+# ---------------------------------------------------------------------------
+def _blocks_inside_sources(t: "DeviceKVTransfer") -> bool:
+    block = t.geometry.block_bytes
+    ends = [(t.block_ids[r] + 1) * block for r in selected_rows(t.import_mask, t.geometry.batch)]
+    return all(0 <= off and off + end <= t.source_bytes for off in t.source_offsets for end in ends)
+
+
+def _rows_consistent(t: "DeviceKVTransfer") -> bool:
+    for row, (gen, block) in enumerate(zip(t.row_generations, t.block_ids)):
+        if t.import_mask >> row & 1:
+            if gen <= 0 or block < 0:
+                return False
+        elif gen != 0 or block != 0:
+            return False
+    return True
 
 
 @dataclass(frozen=True)
 class DeviceKVTransfer:
-    """IPC metadata of a device-to-device import (kv_transfer.py:67-137).
+    """A device-to-device import, as metadata only.
 
-    keys[2*l] / keys[2*l+1]: the HIP IPC handle (64 bytes) of the allocation
-    holding layer l's K / V cache; source_offsets: each cache's byte offset
-    in its allocation; source_bytes: the common allocation size; block_ids:
-    the scheduler block of each imported row (0 for the others)."""
+    ``keys[2 l]`` / ``keys[2 l + 1]``: the IPC handle of the allocation that
+    holds layer l's K / V cache, at byte ``source_offsets[...]`` of it;
+    ``source_bytes``: the size every such allocation has; ``block_ids``: the
+    stock cache block of each selected row (0 for the others)."""
 
     transfer_id: int
     import_mask: int
@@ -170,179 +293,132 @@ class DeviceKVTransfer:
     keys: tuple[bytes, ...]
     geometry: KVGeometry = field(default=QWEN7B_B4)
 
+    RULES = _selection_rules(lambda t: t.geometry.batch) + (
+        ("record-capacity", lambda t: t.geometry.key_count <= IPC_KEY_COUNT,
+         f"the record has key slots for {IPC_KEY_COUNT // 2} layers"),
+        ("block-count", lambda t: len(t.block_ids) == t.geometry.batch, "the block vector has one entry per graph row"),
+        ("source-size", lambda t: t.source_bytes > 0, "the exported allocations have a size"),
+        ("offset-count", lambda t: len(t.source_offsets) == t.geometry.key_count,
+         "one source offset per K and V cache of every layer"),
+        ("key-count", lambda t: len(t.keys) == t.geometry.key_count, "one key per K and V cache of every layer"),
+        ("row-fields", _rows_consistent,
+         "a selected row carries a generation and a block; an unselected row carries zeros"),
+        ("block-range", _blocks_inside_sources, "a selected block lies past the end of an exported allocation"),
+        ("key-format", lambda t: all(isinstance(k, (bytes, bytearray)) and len(k) == IPC_KEY_BYTES and any(k)
+                                     for k in t.keys),
+         f"a key is a nonzero {IPC_KEY_BYTES}-byte IPC handle"),
+    )
+
     def validate(self) -> None:
-        g = self.geometry
-        _check(g.key_count <= IPC_KEY_COUNT, "device KV transfer has more caches than the wire record")
-        _check(self.transfer_id > 0, "device KV transfer id must be positive")
-        _check(len(self.block_ids) == g.batch, f"device KV transfer block vector must have {g.batch} rows")
-        _check_mask_and_generations(self.import_mask, tuple(self.row_generations), g.batch, "device KV transfer")
-        _check(self.source_bytes > 0, "device KV transfer source size must be positive")
-        _check(len(self.source_offsets) == g.key_count, f"device KV transfer must carry {g.key_count} source offsets")
-        _check(len(self.keys) == g.key_count, f"device KV transfer must carry {g.key_count} keys")
-        for row in range(g.batch):
-            gen, block = self.row_generations[row], self.block_ids[row]
-            if self.import_mask & (1 << row):
-                _check(gen > 0 and block >= 0, "selected device KV rows need generation and block")
-                end = (block + 1) * g.block_bytes
-                for offset in self.source_offsets:
-                    _check(0 <= offset and offset + end <= self.source_bytes, "device KV block is outside its exported allocation")
-            else:
-                _check(gen == 0 and block == 0, "unselected device KV rows must be zeroed")
-        for key in self.keys:
-            _check(
-                isinstance(key, (bytes, bytearray)) and len(key) == IPC_KEY_BYTES and any(key),
-                "device KV IPC key does not fit the wire contract",
-            )
+        _enforce(self.RULES, self)
 
     def wire_bytes(self) -> bytes:
-        """The 4,088-byte record the engine reads (ResidentEpochIpcMetadata);
-        slots of layers past geometry.layers stay zero."""
+        """The 4,088-byte record the engine reads (``ResidentEpochIpcMetadata``);
+        the slots of layers a smaller geometry lacks stay zero."""
         self.validate()
-        pad = IPC_KEY_COUNT - len(self.keys)
-        header = IPC_METADATA_HEADER.pack(
-            IPC_METADATA_MAGIC,
-            IPC_METADATA_VERSION,
-            self.import_mask,
-            self.source_bytes,
-            *self.row_generations,
-            *self.block_ids,
-            *self.source_offsets,
-            *([0] * pad),
+        unused = IPC_KEY_COUNT - len(self.keys)
+        record = bytearray(IPC_METADATA_BYTES)
+        IPC_METADATA_HEADER.pack_into(
+            record, 0, IPC_METADATA_MAGIC, IPC_METADATA_VERSION, self.import_mask, self.source_bytes,
+            *self.row_generations, *self.block_ids, *self.source_offsets, *([0] * unused),
         )
-        record = header + b"".join(bytes(k) for k in self.keys) + bytes(pad * IPC_KEY_BYTES)
-        assert len(record) == IPC_METADATA_BYTES
-        return record
+        for slot, key in enumerate(self.keys):
+            start = IPC_METADATA_HEADER.size + slot * IPC_KEY_BYTES
+            record[start : start + IPC_KEY_BYTES] = key
+        return bytes(record)
 
 
 # ---------------------------------------------------------------------------
-# Host snapshot files
+# Reading a worker's stock caches
 # ---------------------------------------------------------------------------
-def write_kv_snapshot(path: str | Path, snapshot: ResidentKVSnapshot) -> None:
-    """Write header + payload atomically (temporary file, fsync, rename);
-    the file must lie under /dev/shm (kv_transfer.py:431-466)."""
-    snapshot.validate()
-    g = snapshot.geometry
-    target = Path(path).resolve()
-    _check(str(target).startswith("/dev/shm/"), "KV transfer files must be under /dev/shm")
-    target.parent.mkdir(parents=True, exist_ok=True)
-    staging = target.with_name(f".{target.name}.tmp-{os.getpid()}-{snapshot.transfer_id}")
-    if staging.exists():
-        raise RuntimeError(f"stale KV transfer temporary file exists: {staging}")
-    header = HEADER.pack(
-        TRANSFER_MAGIC,
-        TRANSFER_VERSION,
-        TRANSFER_HEADER_BYTES,
-        snapshot.transfer_id,
-        len(snapshot.payload),
-        snapshot.import_mask,
-        *snapshot.row_generations,
-        g.layers,
-        g.batch,
-        g.block_size,
-        g.kv_heads,
-        g.head_size,
-        g.element_bytes,
-        snapshot.checksum,
-    )
-    try:
-        with staging.open("xb") as out:
-            out.write(header)
-            out.write(snapshot.payload)
-            out.flush()
-            os.fsync(out.fileno())
-        os.replace(staging, target)
-    finally:
-        staging.unlink(missing_ok=True)
+@dataclass(frozen=True)
+class _Import:
+    row: int
+    block: int
+    generation: int
 
 
-def read_kv_snapshot(path: str | Path) -> ResidentKVSnapshot:
-    """Parse a snapshot file back (header checks as the engine makes them)."""
-    raw = Path(path).read_bytes()
-    _check(len(raw) >= TRANSFER_HEADER_BYTES, "KV transfer file is shorter than its header")
-    fields = HEADER.unpack_from(raw)
-    magic, version, header_bytes, transfer_id, payload_bytes, mask = fields[:6]
-    gens = tuple(fields[6:10])
-    layers, batch, block_size, kv_heads, head_size, element_bytes, checksum = fields[10:]
-    _check(magic == TRANSFER_MAGIC and version == TRANSFER_VERSION, "not a KV transfer file")
-    _check(header_bytes == TRANSFER_HEADER_BYTES, "KV transfer header size mismatch")
-    _check(len(raw) == header_bytes + payload_bytes, "KV transfer file size mismatch")
-    g = KVGeometry(layers, batch, block_size, kv_heads, head_size, element_bytes)
-    snap = ResidentKVSnapshot(transfer_id, mask, gens, raw[header_bytes:], checksum, g)
-    snap.validate()
-    return snap
+def _imports_of(plan: Any, what: str) -> list[_Import]:
+    picked = []
+    for request in plan.requests:
+        if not request.kv_import_required:
+            continue
+        if len(request.scheduler_block_ids) != 1:
+            raise TransferError("one-block", f"{what}: an imported row occupies exactly one stock block")
+        picked.append(_Import(request.row, int(request.scheduler_block_ids[0]), int(request.generation)))
+    if not picked:
+        raise TransferError("no-imports", f"{what}: the plan imports no row")
+    return sorted(picked, key=lambda i: i.row)
 
 
-# ---------------------------------------------------------------------------
-# Capture from the stock KV cache of a worker
-# ---------------------------------------------------------------------------
-def _stock_caches(worker: Any) -> list:
-    runner = getattr(worker, "model_runner", None)
-    caches = getattr(runner, "kv_caches", None)
-    if not isinstance(caches, list) or not caches:
-        raise RuntimeError("stock KV cache layout is not a list of per-layer K/V pairs")
-    for layer in caches:
+def _cache_pairs(worker: Any) -> list[tuple[Any, Any]]:
+    """(K, V) per layer from ``worker.model_runner.kv_caches``."""
+    layers = getattr(getattr(worker, "model_runner", None), "kv_caches", None)
+    if not isinstance(layers, list) or not layers:
+        raise RuntimeError("the worker holds no per-layer stock KV caches")
+    pairs = []
+    for layer in layers:
         if not isinstance(layer, (tuple, list)) or len(layer) < 2:
-            raise RuntimeError("stock vLLM KV cache layer is not a K/V pair")
-    return caches
+            raise RuntimeError("a stock KV cache layer is not a (K, V) pair")
+        pairs.append((layer[0], layer[1]))
+    return pairs
 
 
-def _geometry_of(caches: list, batch: int) -> KVGeometry:
-    """Geometry of stock caches laid out [blocks, block_size, kv_heads, head]."""
-    key = caches[0][0]
+def _geometry(pairs: list[tuple[Any, Any]], batch: int) -> KVGeometry:
+    key = pairs[0][0]
     if key.dim() != 4:
-        raise RuntimeError("stock KV cache entries must be [blocks, block_size, kv_heads, head]")
-    _, bs, kvh, hd = (int(s) for s in key.shape)
-    return KVGeometry(len(caches), batch, bs, kvh, hd, int(key.element_size()))
+        raise RuntimeError("stock KV caches are laid out [blocks, block_size, kv_heads, head]")
+    _, block_size, kv_heads, head = (int(s) for s in key.shape)
+    return KVGeometry(len(pairs), batch, block_size, kv_heads, head, int(key.element_size()))
 
 
-def _import_rows(plan: Any, what: str) -> list:
-    rows = [r for r in plan.requests if r.kv_import_required]
-    if not rows:
-        raise ValueError(f"{what} requested for a plan without imports")
-    for r in rows:
-        if len(r.scheduler_block_ids) != 1:
-            raise ValueError(f"{what} requires one scheduler block per row")
-    return rows
+def _fresh_transfer_id() -> int:
+    return secrets.randbits(63) or 1
+
+
+def _import_fields(imports: list[_Import], batch: int) -> tuple[int, tuple[int, ...], tuple[int, ...]]:
+    gens, blocks = [0] * batch, [0] * batch
+    for i in imports:
+        gens[i.row], blocks[i.row] = i.generation, i.block
+    return sum(1 << i.row for i in imports), tuple(gens), tuple(blocks)
 
 
 def capture_kv_snapshot(worker: Any, plan: Any, batch: int | None = None) -> ResidentKVSnapshot:
-    """Copy each imported row's scheduler block of every layer into a
-    compact payload (kv_transfer.py:362-428)."""
+    """Copy each imported row's stock block of every layer into a snapshot.
+
+    The blocks are gathered where the caches live (one ``index_select`` per
+    layer and cache) and copied to the host once per cache (K, then V)."""
     import torch
 
-    rows = _import_rows(plan, "KV snapshot")
-    caches = _stock_caches(worker)
-    g = _geometry_of(caches, batch or plan.graph_batch_size)
+    imports = _imports_of(plan, "KV snapshot")
+    pairs = _cache_pairs(worker)
+    g = _geometry(pairs, batch or plan.graph_batch_size)
     if plan.logical_capacity > g.block_size:
-        raise ValueError("a snapshot transfers one block per row: capacity must fit one block")
-    block_of = {r.row: int(r.scheduler_block_ids[0]) for r in rows}
-    parts: list[list] = [[], []]
-    for key, value in (layer[:2] for layer in caches):
-        for cache, tensor in ((0, key), (1, value)):
-            if tensor.dtype != key.dtype:
-                raise ValueError("K and V caches differ in dtype")
-            for row in range(g.batch):
-                block = block_of.get(row)
-                if block is None:
-                    parts[cache].append(torch.zeros(tensor.shape[1:], dtype=tensor.dtype))
-                    continue
-                if not 0 <= block < tensor.shape[0]:
-                    raise ValueError("scheduler block is outside the stock KV cache")
-                parts[cache].append(tensor[block].detach().to("cpu").contiguous())
-    payload = b"".join(
-        torch.stack(p).contiguous().view(torch.uint8).numpy().tobytes() for p in parts
-    )
-    gens = [0] * g.batch
-    for r in rows:
-        gens[r.row] = int(r.generation)
-    mask = sum(1 << r.row for r in rows)
-    snap = ResidentKVSnapshot(secrets.randbits(63) or 1, mask, tuple(gens), payload,
-                              kv_payload_checksum(payload, mask, g), g)
-    snap.validate()
-    return snap
+        raise TransferError("window", "a snapshot carries one block per row: the epoch's window must fit in it")
+    dtype = pairs[0][0].dtype
+    blocks = torch.tensor([i.block for i in imports], dtype=torch.int64)
+    rows = [i.row for i in imports]
+    out = np.zeros((2, g.layers, g.batch, g.block_bytes), dtype=np.uint8)
+    for half in range(2):
+        caches = [pair[half] for pair in pairs]
+        if any(c.dtype != dtype or tuple(c.shape[1:]) != tuple(caches[0].shape[1:]) for c in caches):
+            raise TransferError("cache-format", "every stock cache shares one dtype and block shape")
+        if any(not 0 <= i.block < c.shape[0] for c in caches for i in imports):
+            raise TransferError("block-range", "an imported block lies outside its stock cache")
+        index = blocks.to(caches[0].device)
+        gathered = torch.stack([c.detach().index_select(0, index) for c in caches])  # [layers, rows, block...]
+        host = gathered.contiguous().cpu().view(torch.uint8).numpy()
+        out[half][:, rows] = host.reshape(g.layers, len(rows), g.block_bytes)
+    payload = out.tobytes()
+    mask, gens, _ = _import_fields(imports, g.batch)
+    snapshot = ResidentKVSnapshot(_fresh_transfer_id(), mask, gens, payload, kv_payload_checksum(payload, mask, g), g)
+    snapshot.validate()
+    return snapshot
 
 
-# HIP runtime entry points used by the exporting side.
+# ---------------------------------------------------------------------------
+# Device IPC exports
+# ---------------------------------------------------------------------------
 @lru_cache(maxsize=1)
 def _hip() -> ctypes.CDLL:
     lib = ctypes.CDLL("libamdhip64.so", mode=ctypes.RTLD_GLOBAL)
@@ -353,12 +429,12 @@ def _hip() -> ctypes.CDLL:
     return lib
 
 
-def _allocation_of(data_ptr: int) -> tuple[int, int]:
-    """(base, size) of the device allocation containing data_ptr."""
+def _allocation_of(address: int) -> tuple[int, int]:
+    """(base, size) of the device allocation that contains ``address``."""
     base, size = ctypes.c_void_p(), ctypes.c_size_t()
-    rc = _hip().hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), ctypes.c_void_p(data_ptr))
-    if rc != 0 or not base.value or size.value == 0:
-        raise RuntimeError(f"cannot resolve the device allocation holding the stock KV cache (hip error {rc})")
+    rc = _hip().hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), ctypes.c_void_p(address))
+    if rc != 0 or not base.value or not size.value:
+        raise RuntimeError(f"hipMemGetAddressRange found no allocation for a stock KV cache (error {rc})")
     return int(base.value), int(size.value)
 
 
@@ -366,80 +442,87 @@ def _ipc_handle(base: int) -> bytes:
     handle = ctypes.create_string_buffer(IPC_KEY_BYTES)
     rc = _hip().hipIpcGetMemHandle(handle, ctypes.c_void_p(base))
     if rc != 0:
-        raise RuntimeError(f"hipIpcGetMemHandle failed for a stock KV allocation (hip error {rc})")
+        raise RuntimeError(f"hipIpcGetMemHandle refused a stock KV allocation (error {rc})")
     return handle.raw
 
 
-@dataclass
-class _DeviceKVExportTable:
-    signature: tuple[tuple[int, int, int], ...]  # (data_ptr, allocation base, allocation size) per cache
+@dataclass(frozen=True)
+class _Exports:
     source_bytes: int
     source_offsets: tuple[int, ...]
     keys: tuple[bytes, ...]
 
 
-def _device_exports(worker: Any, caches: list) -> _DeviceKVExportTable:
-    """Export every allocation holding a stock cache once per worker
-    lifetime (kv_transfer.py:266-319): a HIP IPC handle stays valid while
-    the allocation lives, so it is reused until the caches move."""
-    entries = []
-    for layer in caches:
-        for tensor in layer[:2]:
-            if not getattr(tensor, "is_cuda", False) or not tensor.is_contiguous():
-                raise RuntimeError("stock KV cache entries must be contiguous device tensors for IPC export")
-            ptr = int(tensor.data_ptr())
-            base, size = _allocation_of(ptr)
-            if ptr + tensor.numel() * tensor.element_size() > base + size:
-                raise RuntimeError("stock KV cache entry extends past its device allocation")
-            entries.append((ptr, base, size))
-    sizes = {size for _, _, size in entries}
-    if len(sizes) != 1:
-        raise RuntimeError("key/value KV allocations do not have a common size")
-    signature = tuple(entries)
-    current = getattr(worker, "_resident_epoch_device_kv_exports", None)
-    if isinstance(current, _DeviceKVExportTable) and current.signature == signature:
-        return current
-    handles: dict[int, bytes] = {}
-    for _, base, _ in entries:
-        if base not in handles:
-            handles[base] = _ipc_handle(base)
-    table = _DeviceKVExportTable(
-        signature=signature,
-        source_bytes=sizes.pop(),
-        source_offsets=tuple(ptr - base for ptr, base, _ in entries),
-        keys=tuple(handles[base] for _, base, _ in entries),
-    )
-    worker._resident_epoch_device_kv_exports = table
-    return table
+class _ExportRegistry:
+    """IPC exports of stock KV allocations, one handle per allocation.
+
+    Entries are keyed by every cache's (address, allocation base, allocation
+    size), so caches that move or whose memory is reallocated get new
+    handles; a handle stays valid while its allocation lives.  The registry
+    keeps the most recent few cache sets."""
+
+    def __init__(self, limit: int = 4):
+        self.limit = limit
+        self.entries: OrderedDict[tuple, _Exports] = OrderedDict()
+
+    @staticmethod
+    def _placement(tensors: list[Any]) -> tuple[tuple[int, int, int], ...]:
+        placement = []
+        for t in tensors:
+            if not getattr(t, "is_cuda", False) or not t.is_contiguous():
+                raise RuntimeError("IPC export needs contiguous device tensors for the stock KV caches")
+            address = int(t.data_ptr())
+            base, size = _allocation_of(address)
+            if address + t.numel() * t.element_size() > base + size:
+                raise RuntimeError("a stock KV cache runs past the end of its allocation")
+            placement.append((address, base, size))
+        return tuple(placement)
+
+    def exports(self, tensors: list[Any]) -> _Exports:
+        placement = self._placement(tensors)
+        found = self.entries.get(placement)
+        if found is not None:
+            self.entries.move_to_end(placement)
+            return found
+        sizes = {size for _, _, size in placement}
+        if len(sizes) != 1:
+            raise RuntimeError("the stock KV allocations differ in size; the record carries one size")
+        handles = {base: _ipc_handle(base) for base in dict.fromkeys(base for _, base, _ in placement)}
+        made = _Exports(sizes.pop(), tuple(a - b for a, b, _ in placement), tuple(handles[b] for _, b, _ in placement))
+        self.entries[placement] = made
+        while len(self.entries) > self.limit:
+            self.entries.popitem(last=False)
+        return made
+
+    def forget(self, tensors: list[Any]) -> None:
+        addresses = tuple(int(t.data_ptr()) for t in tensors)
+        for placement in [p for p in self.entries if tuple(a for a, _, _ in p) == addresses]:
+            del self.entries[placement]
+
+
+_REGISTRY = _ExportRegistry()
+
+
+def _flat_caches(pairs: list[tuple[Any, Any]]) -> list[Any]:
+    return [t for pair in pairs for t in pair]
 
 
 def capture_kv_device_transfer(worker: Any, plan: Any, batch: int | None = None) -> DeviceKVTransfer:
-    """IPC metadata for importing the plan's rows, every KV byte staying on
-    the device (kv_transfer.py:322-352)."""
-    rows = _import_rows(plan, "device KV transfer")
-    caches = _stock_caches(worker)
-    g = _geometry_of(caches, batch or plan.graph_batch_size)
-    table = _device_exports(worker, caches)
-    blocks = [0] * g.batch
-    gens = [0] * g.batch
-    for r in rows:
-        blocks[r.row] = int(r.scheduler_block_ids[0])
-        gens[r.row] = int(r.generation)
-    transfer = DeviceKVTransfer(
-        transfer_id=secrets.randbits(63) or 1,
-        import_mask=sum(1 << r.row for r in rows),
-        row_generations=tuple(gens),
-        block_ids=tuple(blocks),
-        source_bytes=table.source_bytes,
-        source_offsets=table.source_offsets,
-        keys=table.keys,
-        geometry=g,
-    )
+    """The IPC record that imports the plan's rows; no KV byte leaves the
+    device."""
+    imports = _imports_of(plan, "device KV transfer")
+    pairs = _cache_pairs(worker)
+    g = _geometry(pairs, batch or plan.graph_batch_size)
+    exports = _REGISTRY.exports(_flat_caches(pairs))
+    mask, gens, blocks = _import_fields(imports, g.batch)
+    transfer = DeviceKVTransfer(_fresh_transfer_id(), mask, gens, blocks, exports.source_bytes,
+                                exports.source_offsets, exports.keys, g)
     transfer.validate()
     return transfer
 
 
 def release_kv_device_exports(worker: Any) -> None:
-    """Forget the worker's exports (HIP IPC handles need no close on the
-    exporting side; importers close their mappings)."""
-    worker._resident_epoch_device_kv_exports = None
+    """Drop the exports of the worker's current caches (the exporting side
+    closes nothing; importers unmap their own mappings)."""
+    with contextlib.suppress(RuntimeError):
+        _REGISTRY.forget(_flat_caches(_cache_pairs(worker)))

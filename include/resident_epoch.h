@@ -165,7 +165,9 @@ int32_t resident_epoch_prefill_batch(void *engine, int32_t n_rows,
  * the engine's grown-on-demand buffer, and the projections always run on
  * the hand-written GEMM (hipBLASLt keeps a workspace of its own).  Calls on
  * one GPU share the array and are serialized; a call leaves its contents
- * behind.  Return 0, -1 bad arguments, -2 HIP failure, -3 the pass does not
+ * behind.  The array's device address is resolved on the first call on a
+ * device (no allocation).  Return 0, -1 bad arguments, -2 HIP failure
+ * (including an unresolvable array address), -3 the pass does not
  * fit the array (about 145 KB per prompt token at Qwen2.5-7B's shape, so
  * some 460 tokens at most; prompts of one token need none). */
 int32_t resident_epoch_prefill_batch_noalloc(void *engine, int32_t n_rows,
@@ -225,8 +227,10 @@ int32_t resident_epoch_time_ops(void *engine, int32_t begin, int32_t end, int32_
  * resident_epoch_time_ops.  Each launch streams another layer's weights, so
  * none of them is left in the memory-side cache by the launch before (at
  * Qwen2.5-7B's shape a layer's gate/up weights are 272 MB, the cache 256 MB).
- * *avg_ms receives the mean time per launch.  Return 0, -1 bad arguments,
- * -2 HIP failure. */
+ * *avg_ms receives the mean time per launch.  Return 0, -1 bad arguments
+ * or an op that launches nothing under the engine's plan (the o- and
+ * down-reduce entries unless that projection runs split-K on the row-tiled
+ * path), -2 HIP failure. */
 int32_t resident_epoch_time_layer_op(void *engine, int32_t which, int32_t passes, float *avg_ms);
 
 #ifdef __cplusplus

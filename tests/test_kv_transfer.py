@@ -1,9 +1,11 @@
 """KV transfer records and capture (cruise_amd.kv_transfer), on the CPU.
 
-Restates the reference's tests/test_kv_transfer.py: the IPC record carries
-only metadata in its fixed layout; exports are made once per allocation with
-each cache's offset in it; a snapshot takes each imported row's scheduler
-block into the row's slot.  The checksum is pinned against zlib.adler32 run
+The behaviours the reference's tests/test_kv_transfer.py checks: the IPC
+record carries only metadata in its fixed layout; exports are made once per
+allocation with each cache's offset in it; a snapshot takes each imported
+row's scheduler block into the row's slot.  Every validation rule is broken
+once and named by the error; a damaged snapshot file is refused and a failed
+write leaves no file behind.  The checksum is pinned against zlib.adler32 run
 over the blocks the reference's loop selects (kv_transfer.py:159-174),
 computed here by slicing a numpy view instead of by offsets, and against a
 brute-force Adler-32 of the concatenated bytes.
@@ -33,6 +35,7 @@ from cruise_amd.kv_transfer import (
     PAYLOAD_BYTES,
     TRANSFER_HEADER_BYTES,
     DeviceKVTransfer,
+    TransferError,
     KVGeometry,
     ResidentKVSnapshot,
     capture_kv_device_transfer,
@@ -107,26 +110,33 @@ def test_small_geometry_record_zero_pads_unused_layers():
 
 
 @pytest.mark.parametrize(
-    ("change", "message"),
+    ("change", "rule"),
     [
-        ({"transfer_id": 0}, "id must be positive"),
-        ({"import_mask": 0}, "at least one row"),
-        ({"row_generations": (0, 0, 0, 0)}, "need generation and block"),
-        ({"block_ids": (2, 1, 5, 0)}, "must be zeroed"),
-        ({"source_bytes": 5 * BLOCK_ELEMENTS * ELEMENT_BYTES}, "outside its exported allocation"),
-        ({"keys": (b"short",) * IPC_KEY_COUNT}, "does not fit the wire contract"),
-        ({"keys": (bytes(IPC_KEY_BYTES),) * IPC_KEY_COUNT}, "does not fit the wire contract"),
-        ({"source_offsets": (0,)}, "source offsets"),
+        ({"transfer_id": 0}, "transfer-id"),
+        ({"import_mask": 0}, "mask-range"),
+        ({"import_mask": 0b10000}, "mask-range"),
+        ({"row_generations": (11, 0, 13)}, "generation-count"),
+        ({"row_generations": (0, 0, 0, 0)}, "row-fields"),
+        ({"block_ids": (2, 1, 5, 0)}, "row-fields"),
+        ({"block_ids": (2, 0, 5)}, "block-count"),
+        ({"source_bytes": 5 * BLOCK_ELEMENTS * ELEMENT_BYTES}, "block-range"),
+        ({"source_bytes": 0}, "source-size"),
+        ({"keys": (b"short",) * IPC_KEY_COUNT}, "key-format"),
+        ({"keys": (bytes(IPC_KEY_BYTES),) * IPC_KEY_COUNT}, "key-format"),
+        ({"keys": (b"\x01" * IPC_KEY_BYTES,)}, "key-count"),
+        ({"source_offsets": (0,)}, "offset-count"),
     ],
 )
-def test_device_kv_transfer_validation(change, message):
+def test_device_kv_transfer_validation(change, rule):
     block = BLOCK_ELEMENTS * ELEMENT_BYTES
     fields = dict(transfer_id=7, import_mask=0b0101, row_generations=(11, 0, 13, 0), block_ids=(2, 0, 5, 0),
                   source_bytes=8 * block, source_offsets=(0, block) * (IPC_KEY_COUNT // 2),
                   keys=tuple(b"\x01" * IPC_KEY_BYTES for _ in range(IPC_KEY_COUNT)))
+    DeviceKVTransfer(**fields).validate()
     fields.update(change)
-    with pytest.raises(ValueError, match=message):
+    with pytest.raises(TransferError) as raised:
         DeviceKVTransfer(**fields).validate()
+    assert raised.value.rule == rule and isinstance(raised.value, ValueError)
 
 
 def test_device_kv_export_uses_allocation_base_offsets(monkeypatch):
@@ -163,6 +173,7 @@ def test_device_kv_export_uses_allocation_base_offsets(monkeypatch):
         key, value = FakeTensor(base), FakeTensor(base + view_bytes)
         bases[key.ptr] = bases[value.ptr] = base
         caches.append((key, value))
+    monkeypatch.setattr(kvt, "_REGISTRY", kvt._ExportRegistry())
     monkeypatch.setattr(kvt, "_allocation_of", lambda ptr: (bases[ptr], allocation))
     monkeypatch.setattr(kvt, "_ipc_handle", lambda base: exported.append(base) or base.to_bytes(8, "little") * 8)
     worker = SimpleNamespace(model_runner=SimpleNamespace(kv_caches=caches))
@@ -206,7 +217,8 @@ def test_device_kv_export_rejects_unequal_allocations(monkeypatch):
 
     monkeypatch.setattr(kvt, "_allocation_of", lambda ptr: (ptr, 1 << 20 if ptr < 100 else 2 << 20))
     worker = SimpleNamespace(model_runner=SimpleNamespace(kv_caches=[(T(1), T(2)), (T(200), T(300))]))
-    with pytest.raises(RuntimeError, match="common size"):
+    monkeypatch.setattr(kvt, "_REGISTRY", kvt._ExportRegistry())
+    with pytest.raises(RuntimeError, match="differ in size"):
         capture_kv_device_transfer(worker, plan_of(importing(0, 7, 0)))
 
 
@@ -260,24 +272,66 @@ def test_snapshot_file_round_trip_and_header(tmp_path):
         assert read_kv_snapshot(path) == snap
     finally:
         os.unlink(path)
-    with pytest.raises(ValueError, match="under /dev/shm"):
+    with pytest.raises(TransferError) as raised:
         write_kv_snapshot(tmp_path / "x", snap)
+    assert raised.value.rule == "location"
 
 
 @pytest.mark.parametrize(
-    ("change", "message"),
+    ("change", "rule"),
     [
-        ({"transfer_id": 0}, "id must be positive"),
-        ({"import_mask": 0b10000}, "at least one row"),
-        ({"row_generations": (4, 1, 0, 6)}, "mask and generations disagree"),
-        ({"payload": b"x"}, "payload must be"),
-        ({"checksum": 1}, "checksum does not match"),
+        ({"transfer_id": 0}, "transfer-id"),
+        ({"import_mask": 0b10000}, "mask-range"),
+        ({"row_generations": (4, 1, 0, 6)}, "generation-selects-row"),
+        ({"row_generations": (4, 0, 0, -6)}, "generation-sign"),
+        ({"payload": b"x"}, "payload-size"),
+        ({"checksum": 1}, "checksum"),
     ],
 )
-def test_snapshot_validation(change, message):
+def test_snapshot_validation(change, rule):
     payload = bytes(SMALL.payload_bytes)
     fields = dict(transfer_id=1, import_mask=0b1001, row_generations=(4, 0, 0, 6), payload=payload,
                   checksum=kv_payload_checksum(payload, 0b1001, SMALL), geometry=SMALL)
+    ResidentKVSnapshot(**fields).validate()
     fields.update(change)
-    with pytest.raises(ValueError, match=message):
+    with pytest.raises(TransferError) as raised:
         ResidentKVSnapshot(**fields).validate()
+    assert raised.value.rule == rule
+
+
+def test_snapshot_file_rejects_a_damaged_header_or_size():
+    if not os.path.isdir("/dev/shm"):
+        pytest.skip("no /dev/shm")
+    payload = bytes(range(256)) * (SMALL.payload_bytes // 256)
+    snap = ResidentKVSnapshot(9, 0b0010, (0, 3, 0, 0), payload, kv_payload_checksum(payload, 0b0010, SMALL), SMALL)
+    raw = snap.header() + payload
+    assert ResidentKVSnapshot.parse(raw) == snap
+    for damaged, rule in ((raw[:40], "file-size"), (raw[:-1], "file-size"), (b"\0" + raw[1:], "magic")):
+        with pytest.raises(TransferError) as raised:
+            ResidentKVSnapshot.parse(damaged)
+        assert raised.value.rule == rule
+    flipped = bytearray(raw)
+    flipped[TRANSFER_HEADER_BYTES + 5 * SMALL.block_bytes] ^= 1  # row 1's K block of layer 1
+    with pytest.raises(TransferError, match="checksum"):
+        ResidentKVSnapshot.parse(bytes(flipped))
+
+
+def test_snapshot_writer_leaves_no_partial_file_on_failure(monkeypatch):
+    if not os.path.isdir("/dev/shm"):
+        pytest.skip("no /dev/shm")
+    payload = bytes(SMALL.payload_bytes)
+    snap = ResidentKVSnapshot(5, 0b0001, (2, 0, 0, 0), payload, kv_payload_checksum(payload, 1, SMALL), SMALL)
+    folder = f"/dev/shm/cruise-kvt-fail-{os.getpid()}"
+    os.makedirs(folder, exist_ok=True)
+    try:
+        def boom(fd):
+            raise OSError("disk gone")
+
+        monkeypatch.setattr(kvt.os, "fsync", boom)
+        with pytest.raises(OSError, match="disk gone"):
+            write_kv_snapshot(f"{folder}/snap", snap)
+        assert os.listdir(folder) == []
+    finally:
+        for name in os.listdir(folder):
+            os.unlink(os.path.join(folder, name))
+        os.rmdir(folder)
