@@ -442,14 +442,17 @@ def epoch_trace_copies():
 
 
 def traffic_bytes():
-    """HBM bytes per launch of the reported kernel from the committed
-    rocprofv3 PMC passes (FETCH_SIZE and WRITE_SIZE, each scaled by what the
-    counter reads for a plain copy of known size), or None without them."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_qwen7b_b4_traffic.json")
+    """HBM bytes per launch of the reported kernel (gate/up) from the
+    committed rocprofv3 PMC passes over the decoder step's kernels
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a
+    plain copy of known size; cruise_amd/pmcsummary.py), or None without
+    them."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_kernels_qwen7b_b4_traffic.json")
     try:
         with open(path) as f:
-            return int(json.load(f)["traffic_bytes_per_launch"])
-    except (OSError, KeyError, ValueError):
+            rows = json.load(f)["kernels"]
+        return int(next(r["traffic_bytes"] for r in rows if r["op"] == "gate_up"))
+    except (OSError, KeyError, ValueError, StopIteration):
         return None
 
 
