@@ -2,7 +2,8 @@
 
 ``python -m cruise_amd.build`` compiles ``cruise_amd/csrc/*.hip`` into
 ``cruise_amd/lib/libresident_epoch.so``.  The library links the HIP runtime
-and hipBLASLt (the batched-prefill GEMMs): PyTorch is never linked into it.
+only: every kernel, the batched-prefill GEMMs included, is hand-written, and
+PyTorch is never linked into it.
 """
 from __future__ import annotations
 
@@ -20,8 +21,8 @@ LIBRARY = LIBDIR / "libresident_epoch.so"
 SERVER = LIBDIR / "resident_epoch_server"
 SERVER_SOURCE = "re_server.cpp"
 INCLUDE = PACKAGE.parent / "include"
-SOURCES = ("re_step.hip", "re_attn.hip", "re_ctrl.hip", "re_prefill.hip", "re_blas.hip", "re_mfma.hip", "re_engine.hip")
-LINK_LIBS = ("-lhipblaslt",)  # batched-prefill GEMMs (re_blas.hip)
+SOURCES = ("re_step.hip", "re_attn.hip", "re_ctrl.hip", "re_prefill.hip", "re_mfma.hip", "re_engine.hip")
+LINK_LIBS: tuple[str, ...] = ()
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

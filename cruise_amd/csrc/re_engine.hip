@@ -143,9 +143,6 @@ struct Engine {
   // Batched prefill scratch (grown on demand, freed with the engine).
   uint8_t* pf_mem = nullptr;
   size_t pf_bytes = 0;
-  PrefillBlas* pf_blas = nullptr;  // created on the first bf16 batched prefill
-  bool pf_blas_tried = false;
-  bool prefill_blas_allowed = true;  // "tuning": {"prefill_blas": 0} keeps the hand-written GEMM
   bool pf_ready = false;
   // Device-IPC import: mapped source allocations, keyed by the 64-byte
   // handle, with their mapped sizes; closed when the engine is destroyed.
@@ -382,7 +379,6 @@ bool make_plan(Engine& e, const Json& cfg) {
     p.attn_split = split_tiles;
   }
   if (const Json* t = cfg.get("tuning")) {
-    e.prefill_blas_allowed = t->number_or("prefill_blas", 1) != 0;
     // "down_whole": 0 keeps the split-K down projection and its reduce launch
     if (t->number_or("down_whole", 1) == 0) p.down_whole_grid = 0;
   }
@@ -802,7 +798,6 @@ void free_engine(Engine* e) {
   if (e->h_fetch) (void)hipHostFree(e->h_fetch);
   for (auto& kv : e->ipc_maps) (void)hipIpcCloseMemHandle(kv.second.ptr);
   if (e->pf_mem) (void)hipFree(e->pf_mem);
-  prefill_blas_destroy(e->pf_blas);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -1394,8 +1389,7 @@ namespace {
 // a row's tokens are consecutive and start at position 0.
 // Scratch: the engine's own buffer, grown on demand, or (fixed != nullptr)
 // the caller's fixed buffer of fixed_bytes, in which case nothing is
-// allocated, the GEMMs are the hand-written ones (hipBLASLt keeps a
-// workspace of its own) and a pass that does not fit returns -3.
+// allocated and a pass that does not fit returns -3.
 int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector<int32_t>& gens,
                       const std::vector<std::vector<int64_t>>& prompts, const std::vector<int32_t>& tables,
                       uint8_t* fixed = nullptr, size_t fixed_bytes = 0) {
@@ -1433,7 +1427,11 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
     return at;
   };
   const size_t o_hidden = take(M * H * T), o_xn = take(M * H * T), o_qkv = take((size_t)M * d.qkv_rows() * T);
-  const size_t o_attn = take((size_t)M * d.q_dim() * T), o_gate = take(M * I * T), o_up = take(M * I * T);
+  // bf16: gate, up and SwiGLU in one GEMM (no gate/up buffers); fp32: two
+  // GEMMs and the elementwise SwiGLU
+  const bool fused_mlp = d.dtype_bytes == 2;
+  const size_t o_attn = take((size_t)M * d.q_dim() * T), o_gate = fused_mlp ? 0 : take(M * I * T);
+  const size_t o_up = fused_mlp ? 0 : take(M * I * T);
   const size_t o_mlp = take(M * I * T), o_rope = take((size_t)M * d.head_dim * sizeof(float));
   const size_t o_tok = take(8 * (size_t)M), o_pos = take(4 * (size_t)M), o_slot = take(4 * (size_t)M);
   const size_t o_tiles = take(sizeof(int4) * tiles.size()), o_blocks = take(4 * tables.size());
@@ -1454,11 +1452,6 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
                                         hipMemcpyHostToDevice) == hipSuccess)) &&
                   hipMemcpy(b + o_blocks, tables.data(), 4 * tables.size(), hipMemcpyHostToDevice) == hipSuccess;
   if (!ok) return -2;
-  if (fixed == nullptr && d.dtype_bytes == 2 && !e.pf_blas_tried) {
-    e.pf_blas_tried = true;
-    if (e.prefill_blas_allowed) e.pf_blas = prefill_blas_create();
-  }
-  PrefillBlas* blas = fixed == nullptr ? e.pf_blas : nullptr;
   const KernelEnv env = e.env();
   if (launch_clear_blocks(env, e.key_cache, e.value_cache, reinterpret_cast<const int32_t*>(b + o_blocks),
                           static_cast<int>(tables.size()), s) != hipSuccess)
@@ -1496,19 +1489,6 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
         g.lda = lda;
         g.ldw = K;
         g.ldo = ldo;
-        if (blas != nullptr) {
-          // hipBLASLt: a store GEMM directly; a residual GEMM into the free
-          // normalized-row buffer, then h = T(h + T(A W^T))
-          GemmArgs y = g;
-          if (epi == kGemmResidual) {
-            y.out = b + o_xn;
-            y.ldo = N;
-          }
-          if (prefill_blas_gemm(blas, y, s)) {
-            if (epi == kGemmResidual) run(launch_prefill_residual(b + out_off, b + o_xn, M, N, ldo, N, s));
-            return;
-          }
-        }
         run(launch_gemm(g, epi, d.dtype_bytes, s));
       };
       run(launch_prefill_rmsnorm(b + o_hidden, e.weights + lo.input_norm, b + o_xn, M, d.hidden, d.rms_eps,
@@ -1541,9 +1521,24 @@ int32_t prefill_batch(Engine& e, const std::vector<int>& rows, const std::vector
       gemm(o_attn, d.q_dim(), lo.o_w, SIZE_MAX, o_hidden, d.hidden, d.hidden, d.q_dim(), kGemmResidual);
       run(launch_prefill_rmsnorm(b + o_hidden, e.weights + lo.post_norm, b + o_xn, M, d.hidden, d.rms_eps,
                                  d.dtype_bytes, s));
-      gemm(o_xn, d.hidden, lo.gate_w, SIZE_MAX, o_gate, d.intermediate, d.intermediate, d.hidden, kGemmStore);
-      gemm(o_xn, d.hidden, lo.up_w, SIZE_MAX, o_up, d.intermediate, d.intermediate, d.hidden, kGemmStore);
-      run(launch_prefill_swiglu(b + o_gate, b + o_up, b + o_mlp, (long long)M * d.intermediate, d.dtype_bytes, s));
+      if (fused_mlp) {
+        GemmArgs g{};
+        g.A = b + o_xn;
+        g.W = e.weights + lo.gate_w;
+        g.W2 = e.weights + lo.up_w;
+        g.out = b + o_mlp;
+        g.M = M;
+        g.N = d.intermediate;
+        g.K = d.hidden;
+        g.lda = d.hidden;
+        g.ldw = d.hidden;
+        g.ldo = d.intermediate;
+        run(launch_gemm(g, kGemmSwiGlu, d.dtype_bytes, s));
+      } else {
+        gemm(o_xn, d.hidden, lo.gate_w, SIZE_MAX, o_gate, d.intermediate, d.intermediate, d.hidden, kGemmStore);
+        gemm(o_xn, d.hidden, lo.up_w, SIZE_MAX, o_up, d.intermediate, d.intermediate, d.hidden, kGemmStore);
+        run(launch_prefill_swiglu(b + o_gate, b + o_up, b + o_mlp, (long long)M * d.intermediate, d.dtype_bytes, s));
+      }
       gemm(o_mlp, d.intermediate, lo.down_w, SIZE_MAX, o_hidden, d.hidden, d.hidden, d.intermediate, kGemmResidual);
     }
     if (err != hipSuccess) return -2;

@@ -305,7 +305,10 @@ struct PrefillAttn {           // causal attention within each row's prompt
   const int4* tiles;           // MFMA path: {first query token, row's first token, queries, first position}
   int M, ld, heads, kv_heads, head_dim;
 };
-enum GemmEpilogue : int { kGemmStore = 0, kGemmResidual = 1 };
+// Store: out = T(acc + bias); Residual: out = T(out + T(acc)); SwiGlu (bf16
+// only): W holds the gate rows and W2 the up rows, and out[m, n] =
+// T(T(silu(T(gate))) * T(up)) over N output columns.
+enum GemmEpilogue : int { kGemmStore = 0, kGemmResidual = 1, kGemmSwiGlu = 2 };
 struct GemmArgs {              // out[M,N] (epilogue) A[M,K] W[N,K]^T
   const void* A;
   const void* W;
@@ -313,6 +316,7 @@ struct GemmArgs {              // out[M,N] (epilogue) A[M,K] W[N,K]^T
   const void* bias;            // [N] or null (store epilogue)
   int M, N, K;
   long long lda, ldw, ldo;
+  const void* W2;              // [N,K] up rows of the SwiGLU epilogue (W: the gate rows)
 };
 hipError_t launch_prefill_embed(const PrefillRows& a, int dtype_bytes, hipStream_t stream);
 hipError_t launch_prefill_rmsnorm(const void* x, const void* w, void* y, int M, int H, float eps, int dtype_bytes,
@@ -321,13 +325,6 @@ hipError_t launch_prefill_swiglu(const void* gate, const void* up, void* out, lo
                                  hipStream_t stream);
 hipError_t launch_prefill_qkv_post(const PrefillQkv& a, int dtype_bytes, hipStream_t stream);
 hipError_t launch_gemm(const GemmArgs& a, int epi, int dtype_bytes, hipStream_t stream);
-// hipBLASLt for the bf16 prefill projections (re_blas.hip).
-struct PrefillBlas;
-PrefillBlas* prefill_blas_create();  // nullptr when hipBLASLt is unusable
-void prefill_blas_destroy(PrefillBlas* b);
-bool prefill_blas_gemm(PrefillBlas* b, const GemmArgs& g, hipStream_t stream);  // out = T(A W^T (+ bias))
-hipError_t launch_prefill_residual(void* h, const void* y, long long rows, int N, long long ldh, long long ldy,
-                                   hipStream_t stream);  // h = T(h + y)
 // The MFMA attention serves bf16 models with head_dim 128 (64-query tiles).
 bool prefill_attention_mfma(const Dims& d);
 size_t prefill_attention_lds(const Dims& d, int max_keys);

@@ -8,15 +8,18 @@
 //              bf16: MFMA v_mfma_f32_32x32x16_bf16, 256x256 workgroup tiles
 //              (eight waves of 128x64), K in steps of 64 through two LDS
 //              stages filled by direct global -> LDS loads, fp32
-//              accumulation; epilogues "T(acc + bias)" and the residual
-//              "T(h + T(acc))".  fp32 models: an LDS-tiled FMA GEMM.
+//              accumulation; epilogues "T(acc + bias)", the residual
+//              "T(h + T(acc))", and gate/up with SwiGLU in one GEMM (the
+//              tile's W rows half gate, half up).  fp32 models: an
+//              LDS-tiled FMA GEMM.
 //   qkv post   RoPE of q and k in place, K/V rows to their paged slots
 //   attention  causal within each row's prompt.  bf16, head_dim 128: MFMA
 //              for Q K^T and P V per (64-query tile, head), the bf16 scores of
 //              the whole tile kept in LDS so the softmax is the exact
 //              two-pass one of the decode step; otherwise one workgroup per
 //              (token, head).
-//   SwiGLU     elementwise on the gate and up products
+//   SwiGLU     elementwise on the gate and up products (fp32 models; bf16
+//              models take it in the gate/up GEMM's epilogue)
 #include <algorithm>
 #include <type_traits>
 
@@ -206,12 +209,17 @@ __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int mt, nt;
   gemm_tile_of(blockIdx.x, nM, nN, mt, nt);
-  const int m0 = mt * kGm, n0 = nt * kGn;
+  // The SwiGLU epilogue's tile covers 128 output columns: W tile rows 0..127
+  // are their gate rows, rows 128..255 their up rows.
+  constexpr bool kSwiGlu = EPI == kGemmSwiGlu;
+  constexpr int kTileN = kSwiGlu ? kGn / 2 : kGn;
+  const int m0 = mt * kGm, n0 = nt * kTileN;
   // Loads: waves 0-3 bring W rows 0..255, waves 4-7 A rows 0..255.  Rows past
   // M or N read a valid row (clamped) whose results are never stored.
   const int row0 = wave * kGdmaRows;
   const bool loads_w = row0 < kGn;
-  const char* gbase = loads_w ? static_cast<const char*>(a.W) + (size_t)n0 * a.ldw * 2
+  const void* wsrc = kSwiGlu && row0 >= kTileN ? a.W2 : a.W;
+  const char* gbase = loads_w ? static_cast<const char*>(wsrc) + (size_t)n0 * a.ldw * 2
                               : static_cast<const char*>(a.A) + (size_t)m0 * a.lda * 2;
   const long long ld = loads_w ? a.ldw : a.lda;
   const int rows_left = loads_w ? a.N - n0 : a.M - m0;
@@ -221,7 +229,8 @@ __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, 
     // lane l of instruction i writes slot l % 8 of row row0 + 8 i + l / 8
     const int row = row0 + i * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ gemm_swz(row);
-    goff[i] = static_cast<uint32_t>(min(row & 255, rows_left - 1) * ld * 2 + chunk * 16);
+    const int local = loads_w ? row % kTileN : row & 255;  // the row within its source matrix
+    goff[i] = static_cast<uint32_t>(min(local, rows_left - 1) * ld * 2 + chunk * 16);
   }
   const int nk = a.K / kGk;
   auto issue = [&](int kt) {  // the last stage is re-read past the end (clamped, never used)
@@ -310,6 +319,28 @@ __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, 
       }
   gemm_stage_barrier();
   bf16_t* out = static_cast<bf16_t*>(a.out);
+  if constexpr (kSwiGlu) {
+    // columns c of the gate half and 128 + c of the up half give output
+    // column n0 + c: silu as the decode step computes it, rounded, then the
+    // rounded product
+#pragma unroll 4
+    for (int idx = tid; idx < kGm * kTileN / 8; idx += kGthreads) {
+      const int r = idx / (kTileN / 8), c = idx % (kTileN / 8);
+      const int m = m0 + r, n = n0 + c * 8;
+      if (m >= a.M || n >= a.N) continue;
+      const Vec8<bf16_t> gv = Vec8<bf16_t>::load_cached(T + r * kGoutLd + c * 8);
+      const Vec8<bf16_t> uv = Vec8<bf16_t>::load_cached(T + r * kGoutLd + kTileN + c * 8);
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = gv.get(e);
+        const float sg = round_bf16(x / (1.0f + expf(-x)));
+        y[e] = round_bf16(sg * uv.get(e));
+      }
+      *reinterpret_cast<Vec8<bf16_t>*>(out + (size_t)m * a.ldo + n) = Vec8<bf16_t>::from_floats(y);
+    }
+    return;
+  }
 #pragma unroll 4
   for (int idx = tid; idx < kGm * kGn / 8; idx += kGthreads) {
     const int r = idx / (kGn / 8), c = idx % (kGn / 8);
@@ -734,27 +765,32 @@ hipError_t launch_prefill_qkv_post(const PrefillQkv& a, int dtype_bytes, hipStre
 hipError_t launch_gemm(const GemmArgs& a, int epi, int dtype_bytes, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (dtype_bytes == 2) {
+    const bool swiglu = epi == kGemmSwiGlu;
     const bool aligned = ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W) |
-                           reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
+                           reinterpret_cast<uintptr_t>(a.out) | reinterpret_cast<uintptr_t>(swiglu ? a.W2 : a.W)) &
+                          15) == 0;
     if (a.K <= 0 || a.K % kGk != 0 || a.N % 8 != 0 || a.lda % 8 != 0 || a.ldw % 8 != 0 || a.ldo % 8 != 0 ||
-        !aligned)
+        !aligned || (swiglu && a.W2 == nullptr))
       return hipErrorInvalidValue;
     static const hipError_t attr = [] {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_bf16<kGemmStore>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, kGsmem);
-      if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_bf16<kGemmResidual>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kGsmem);
+      hipError_t e = hipSuccess;
+      for (const void* k : {reinterpret_cast<const void*>(k_gemm_bf16<kGemmStore>),
+                            reinterpret_cast<const void*>(k_gemm_bf16<kGemmResidual>),
+                            reinterpret_cast<const void*>(k_gemm_bf16<kGemmSwiGlu>)})
+        if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kGsmem);
       return e;
     }();
     if (attr != hipSuccess) return attr;
-    const int nM = (a.M + kGm - 1) / kGm, nN = (a.N + kGn - 1) / kGn;
+    const int tile_n = swiglu ? kGn / 2 : kGn;
+    const int nM = (a.M + kGm - 1) / kGm, nN = (a.N + tile_n - 1) / tile_n;
     if (epi == kGemmStore)
       k_gemm_bf16<kGemmStore><<<nM * nN, kGthreads, kGsmem, stream>>>(a, nM, nN);
-    else
+    else if (epi == kGemmResidual)
       k_gemm_bf16<kGemmResidual><<<nM * nN, kGthreads, kGsmem, stream>>>(a, nM, nN);
+    else
+      k_gemm_bf16<kGemmSwiGlu><<<nM * nN, kGthreads, kGsmem, stream>>>(a, nM, nN);
   } else {
-    if (a.K <= 0) return hipErrorInvalidValue;
+    if (a.K <= 0 || epi == kGemmSwiGlu) return hipErrorInvalidValue;
     const dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
     if (epi == kGemmStore)
       k_gemm_f32<kGemmStore><<<grid, 256, 0, stream>>>(a);

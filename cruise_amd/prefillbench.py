@@ -39,7 +39,7 @@ def main(argv=None) -> None:
     p.add_argument("--iters", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--seed", type=int, default=7)
-    p.add_argument("--tuning", default="{}", help='launch-plan overrides as JSON, e.g. {"prefill_blas": 0}')
+    p.add_argument("--tuning", default="{}", help='launch-plan overrides as JSON, e.g. {"attention_split": 1}')
     args = p.parse_args(argv)
     if args.window % 128 or not 2 <= args.len <= args.window:
         raise SystemExit("--window must be a multiple of 128 and 2 <= --len <= --window")

@@ -162,14 +162,13 @@ int32_t resident_epoch_prefill_batch(void *engine, int32_t n_rows,
  * Same arguments, checks and resulting state as resident_epoch_prefill_batch,
  * but the pass's activations and token tables live in a fixed 64 MiB device
  * array of the library (one per GPU, held until the process ends) instead of
- * the engine's grown-on-demand buffer, and the projections always run on
- * the hand-written GEMM (hipBLASLt keeps a workspace of its own).  Calls on
+ * the engine's grown-on-demand buffer.  Calls on
  * one GPU share the array and are serialized; a call leaves its contents
  * behind.  The array's device address is resolved on the first call on a
  * device (no allocation).  Return 0, -1 bad arguments, -2 HIP failure
  * (including an unresolvable array address), -3 the pass does not
- * fit the array (about 145 KB per prompt token at Qwen2.5-7B's shape, so
- * some 460 tokens at most; prompts of one token need none). */
+ * fit the array (about 69 KB per prompt token at Qwen2.5-7B's shape, so
+ * some 970 tokens at most; prompts of one token need none). */
 int32_t resident_epoch_prefill_batch_noalloc(void *engine, int32_t n_rows,
                                              const int32_t *rows,
                                              const int32_t *generations,

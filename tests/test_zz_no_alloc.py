@@ -2,10 +2,8 @@
 both through the C-ABI, on the same inputs from the same zeroed state: the
 resident caches bit for bit and the resident rows exactly, for two calls in a
 row of which the second is smaller (the fixed scratch keeps the first call's
-contents).  The engines run the hand-written GEMM on both paths (the tiny
-fp32 model has no other; the bf16 layer is configured with
-"prefill_blas": 0), so the two paths compute the same values in the same
-order.  Also: device memory does not grow across a no-allocation call, and a
+contents).  Both paths run the same hand-written kernels, so they compute
+the same values in the same order.  Also: device memory does not grow across a no-allocation call, and a
 pass larger than the fixed scratch is refused (-3) before anything runs.
 """
 from __future__ import annotations
@@ -59,7 +57,7 @@ def compare_calls(W, rt, calls, check_memory=False):
         assert same_bits(v, v_ref), "values differ from resident_epoch_prefill_batch"
         np.testing.assert_array_equal(rows_got, rows_ref)
         if check_memory:
-            # the grown-on-demand scratch of this pass would take M x ~145 KB
+            # the grown-on-demand scratch of this pass would take M x ~69 KB
             assert free_before - free_after < (4 << 20), (free_before, free_after)
 
 
@@ -74,10 +72,10 @@ def test_noalloc_prefill_matches_tiny_fp32():
 
 def test_noalloc_prefill_matches_bf16_layer_and_refuses_oversize():
     dev = generate_weights(C2.dims, C2.seed, device="cuda")
-    rt = make_runtime(C2, dev, tuning={"prefill_blas": 0})
+    rt = make_runtime(C2, dev)
     try:
         compare_calls(C2, rt, [([70, 41, 5, 1], 7103), ([12, 2], 7104)], check_memory=True)
-        # 4 x 250 tokens need ~140 MiB of scratch: refused before any launch
+        # 4 x 250 tokens need ~66 MiB of scratch (more than the 64 MiB array): refused before any launch
         rng = np.random.default_rng(7105)
         prompts = [list(map(int, rng.integers(0, C2.dims.vocab, size=250))) for _ in range(4)]
         table = random_tables(rng, 4, C2.geometry.blocks_per_row, C2.geometry.physical_blocks)
