@@ -284,33 +284,11 @@ bool make_plan(Engine& e, const Json& cfg) {
   // cache offsets of one layer are 32-bit in the attention kernel
   if ((long long)d.slots() * d.kv_dim() >= (1LL << 31)) return false;
   plan_grids(p, d, e.cus);
-  // Optional overrides for tuning sweeps ("tuning": {"qkv_grid": n, ...}).
-  if (const Json* t = cfg.get("tuning")) {
-    // "slot_weights": [w0, w1, w2, w3] (positive), or [] for equal ranges
-    if (const Json* sw = t->get("slot_weights"); sw != nullptr && sw->kind == Json::kArray && p.slot_cus > 0) {
-      bool ok = sw->arr.size() == 4;
-      for (const Json& v : sw->arr) ok = ok && v.kind == Json::kNumber && v.num >= 1 && v.num <= 1e6;
-      if (ok) {
-        for (int s = 0; s < 4; ++s) p.slot_w[s] = static_cast<int>(sw->arr[s].num);
-      } else {
-        p.slot_cus = 0;
-        p.gu_grid = p.gu_grid_eq;
-        p.lm_grid = p.lm_grid_eq;
-      }
-    }
-    // "qkv_ksplit": 0 keeps qkv as one row pair per wave over the whole K
+  // "tuning": {"qkv_ksplit": 0} runs qkv as one row pair per wave over the
+  // whole K (the general path) where the K-split kernel applies: a
+  // cross-check of the two, whose fp32 sums run in different orders.
+  if (const Json* t = cfg.get("tuning"))
     if (t->number_or("qkv_ksplit", 1) == 0) p.qkv_ksplit = 0;
-    // "qkv_waves": 4 or 9 waves per qkv workgroup (one row pair per wave)
-    const int qw = static_cast<int>(t->number_or("qkv_waves", p.qkv_waves));
-    if ((qw == 4 || qw == 9) && qw != p.qkv_waves) {
-      p.qkv_waves = qw;
-      p.qkv_grid = (d.qkv_rows() / 2 + qw - 1) / qw;
-    }
-    p.qkv_grid = std::max(1, static_cast<int>(t->number_or("qkv_grid", p.qkv_grid)));
-    p.gu_grid = std::max(1, static_cast<int>(t->number_or("gu_grid", p.gu_grid)));
-    p.lm_grid = std::max(1, static_cast<int>(t->number_or("lm_grid", p.lm_grid)));
-    p.lm_wg = p.lm_grid;
-  }
   // 64 bf16 rows of Qwen2.5-7B's shape: projections on the matrix cores
   // ("tuning": {"mfma": 0} keeps the row-tiled kernels)
   const Json* tune = cfg.get("tuning");
@@ -377,10 +355,6 @@ bool make_plan(Engine& e, const Json& cfg) {
   } else if (p.grouped_attn == 2 && group_attention_msplit_fits(d) && tune != nullptr &&
              tune->number_or("attention_split", 0) != 0) {
     p.attn_split = split_tiles;
-  }
-  if (const Json* t = cfg.get("tuning")) {
-    // "down_whole": 0 keeps the split-K down projection and its reduce launch
-    if (t->number_or("down_whole", 1) == 0) p.down_whole_grid = 0;
   }
   p.o_grid = (d.hidden / 2 + p.waves - 1) / p.waves;
   p.down_grid = p.o_grid;

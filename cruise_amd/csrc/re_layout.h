@@ -143,7 +143,7 @@ struct LaunchPlan {
   int row_tiles;   // ceil(B / mb)
   int waves;       // waves per GEMV workgroup
   int qkv_grid, o_grid, gu_grid, down_grid, lm_grid;
-  int qkv_waves;          // waves per qkv workgroup (one RoPE row pair each): 4, or 9
+  int qkv_waves;          // waves per qkv workgroup of the row-pair kernel (one RoPE row pair each)
   int qkv_ksplit;         // > 0: qkv as k_qkv_ksplit, K split over 7 waves (the grid); 0: k_proj
   int o_waves;            // waves per o-proj workgroup (one row pair each): 4, or 7
   int o_segments, down_segments;  // K-segments of 3584 elements
@@ -152,7 +152,6 @@ struct LaunchPlan {
   int argmax_row_major;  // 1: the partials of a row are contiguous (per-CU LM head)
   int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
   int slot_w[4];   // their per-slot weights
-  int gu_grid_eq, lm_grid_eq;  // the grids for equal ranges
   // Down projection with the whole K in one workgroup (re_step.hip
   // k_down_whole): 0 = split-K segments + reduce launch; else its grid.
   int down_whole_grid;

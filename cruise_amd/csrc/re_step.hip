@@ -814,11 +814,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
       } else if (sizeof(T) == 2 && MB == 4 && p.qkv_ksplit > 0) {
         k_qkv_ksplit<kQkvKsPairs><<<p.qkv_ksplit, kQkvKsWaves * 64, 0, stream>>>(q);
       } else {
-        if (p.qkv_waves == 9)
-          launch_proj<T, MB, 9, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), normed_lds_bytes(MB, d.hidden, sizeof(T), 9),
-                                      stream);
-        else
-          launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
+        launch_proj<T, MB, WAVES, kQkv>(q, dim3(p.qkv_grid, p.row_tiles), proj_smem, stream);
       }
     }
 
@@ -985,13 +981,6 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
   p.qkv_grid = fit(full ? k_proj<T, MB, WAVES, kQkv, true> : k_proj<T, MB, WAVES, kQkv, false>,
                    (d.qkv_rows() / 2 + WAVES - 1) / WAVES);
   p.qkv_waves = WAVES;
-  // Exactly nine RoPE row pairs per CU (Qwen2.5-7B: 2,304 pairs on 256 CUs):
-  // one 9-wave workgroup per CU, so every CU streams the same bytes (with
-  // 4-wave workgroups a quarter of the CUs run three, the rest two).
-  if (sizeof(T) == 2 && MB == 4 && d.qkv_rows() / 2 == 9 * cus) {
-    p.qkv_waves = 9;
-    p.qkv_grid = cus;
-  }
   // qkv with K split over 7 waves (k_qkv_ksplit): the hidden size is 7 x 512
   // and the pairs fill whole workgroups of kQkvKsPairs; the grid, or 0
   p.qkv_ksplit = 0;
@@ -1005,8 +994,6 @@ static void plan_grids_t(LaunchPlan& p, const Dims& d, int cus) {
                   (d.vocab / 2 + WAVES - 1) / WAVES);
   // Slot-weighted ranges for gate/up and the LM head at four workgroups per
   // CU (bf16, one row tile): 1 : 1 : 0.9 : 0.8 measured best on MI355X.
-  p.gu_grid_eq = p.gu_grid;
-  p.lm_grid_eq = p.lm_grid;
   int per_cu = 0;
   if (sizeof(T) == 2 && p.row_tiles == 1 &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(

@@ -74,8 +74,9 @@ class EngineConfig:
     model: ModelSpec = field(default_factory=ModelSpec)
     engine: EngineSpec = field(default_factory=EngineSpec)
     weights: WeightSpec = field(default_factory=WeightSpec)
-    # Launch-plan overrides for tuning sweeps: qkv_grid, gu_grid, lm_grid
-    # (workgroup counts of the projections).
+    # Launch-plan selections that cross-check alternative kernels of the
+    # same arithmetic (for example {"attention_split": 1}); the keys are
+    # listed where the engine reads them.
     tuning: dict = field(default_factory=dict)
 
     def to_json(self) -> str:

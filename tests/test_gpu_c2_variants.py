@@ -1,15 +1,13 @@
 """Launch-plan variants on one Qwen2.5-7B-shape bf16 layer: each must give
 exactly the default plan's logits, greedy tokens and cache writes.
 
-- {"qkv_waves": 4}: 4-wave qkv workgroups (576 of them) instead of the
-  default one 9-wave workgroup per 9 RoPE row pairs (one per CU on a 256-CU
-  MI355X); the per-pair code is the same, so the results must be too.
-- {"o_waves": 4}: the same for the o-projection (448 4-wave workgroups
-  against one 7-wave workgroup per 7 row pairs).
+- {"o_waves": 4}: 448 4-wave o-projection workgroups against the default
+  one 7-wave workgroup per 7 row pairs (one per CU on a 256-CU MI355X); the
+  per-pair code is the same, so the results must be too.
 
-The qkv comparisons hold the K-split qkv (k_qkv_ksplit, the default at this
-shape, whose sums run in another fp32 order and are checked against the
-oracle by the layer tests) off on both sides: {"qkv_ksplit": 0}.
+Both sides also run the row-pair qkv kernel ({"qkv_ksplit": 0}), so the
+comparison covers it next to the default K-split qkv, whose sums run in
+another fp32 order and are checked against the oracle by the layer tests.
 
 The engine allows one instance per process, so the runtimes run one after
 the other."""
@@ -39,7 +37,7 @@ def step_once(weights, tuning, inputs):
     tok, pos, length, slot, active, table, key, value = inputs
     rt = make_runtime(W, weights, tuning=tuning)
     try:
-        facts = {k: rt.info(k) for k in ("qkv_waves", "qkv_grid", "o_waves", "o_grid", "compute_units", "qkv_ksplit")}
+        facts = {k: rt.info(k) for k in ("o_waves", "o_grid", "compute_units", "qkv_ksplit")}
         gk, gv = key.clone().cuda(), value.clone().cuda()
         logits = torch.zeros(B, W.dims.vocab, dtype=torch.float32, device="cuda")
         nxt = torch.zeros(B, dtype=torch.int64, device="cuda")
@@ -50,8 +48,7 @@ def step_once(weights, tuning, inputs):
         rt.close()
 
 
-@pytest.mark.parametrize("tuning", [{"qkv_waves": 4}, {"o_waves": 4}, {"qkv_waves": 4, "o_waves": 4}],
-                         ids=["qkv4", "o4", "both4"])
+@pytest.mark.parametrize("tuning", [{"o_waves": 4}], ids=["o4"])
 def test_projection_workgroup_shapes_match_bit_for_bit(weights_dev, tuning):
     rng = np.random.default_rng(77)
     table = random_tables(rng, B, W.geometry.blocks_per_row, W.geometry.physical_blocks)
@@ -66,15 +63,10 @@ def test_projection_workgroup_shapes_match_bit_for_bit(weights_dev, tuning):
     base_facts, base = step_once(weights_dev, {"qkv_ksplit": 0}, inputs)
     facts, got = step_once(weights_dev, {"qkv_ksplit": 0, **tuning}, inputs)
     cus = base_facts["compute_units"]
-    qkv_pairs = (W.dims.num_heads + 2 * W.dims.num_kv_heads) * W.dims.head_dim // 2
     o_pairs = W.dims.hidden // 2
-    if qkv_pairs == 9 * cus:
-        assert base_facts["qkv_waves"] == 9 and base_facts["qkv_grid"] == cus
     if o_pairs == 7 * cus:
         assert base_facts["o_waves"] == 7 and base_facts["o_grid"] == cus
     assert base_facts["qkv_ksplit"] == 0 and facts["qkv_ksplit"] == 0
-    if "qkv_waves" in tuning:
-        assert facts["qkv_waves"] == 4 and facts["qkv_grid"] == (qkv_pairs + 3) // 4
     if "o_waves" in tuning:
         assert facts["o_waves"] == 4 and facts["o_grid"] == (o_pairs + 3) // 4
     for name, a, b in zip(("logits", "next", "key", "value"), base, got):
