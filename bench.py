@@ -51,6 +51,8 @@ def parse_args():
     p.add_argument("--kernel-passes", type=int, default=4, help="passes over the 28 layers' gate/up launches")
     p.add_argument("--sweep-epochs", type=int, default=20,
                    help="timed epochs at each of K=1, 2, 4 (the K sweep beside the K=8 headline; 0 skips it)")
+    p.add_argument("--tuning", default="", help="JSON object of launch-plan overrides (an A/B switch; the "
+                                                 "headline uses the default plan)")
     p.add_argument("--workload", choices=("qwen7b-b4", "scaled-b64"), default="qwen7b-b4",
                    help="qwen7b-b4: the headline line; scaled-b64: one Qwen2.5-7B layer at 64 rows, contexts "
                         "256-1016, K=8 (a separate line, not the headline)")
@@ -82,6 +84,7 @@ def main() -> int:
             batch=4, physical_blocks=8, block_size=128, blocks_per_row=2, logical_capacity=256
         ),
         weights=WeightSpec(source="synthetic", seed=args.seed, std=0.02),
+        tuning=json.loads(args.tuning) if args.tuning else {},
     )
     t0 = time.time()
     rt = ResidentEpochRuntime(cfg)
@@ -237,6 +240,7 @@ def main() -> int:
             "epoch_steps": K,
             "logical_capacity": capacity,
             "bench_step": "one K=8 epoch (8 decoder steps, 4 rows)",
+            **({"tuning": json.loads(args.tuning)} if args.tuning else {}),
         },
         "ms_per_decoder_step": round(ms_per_decoder_step, 4),
         "step_weight_stream_gbs": round(step_gbs, 1),
