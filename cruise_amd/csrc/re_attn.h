@@ -37,28 +37,21 @@ struct AttnShape {
   static constexpr int kLoads = kLpr;        // loads per lane per tile (64 rows per wave)
 };
 
-// Halving exchange over the N lanes of a group (lane offset c = lane % N):
-// afterwards lane c holds the total over the group of value c.
+// Halving exchange over the N lanes of a group (lane offset c = lane % N,
+// N a power of two from 2 to 32): afterwards lane c holds the total over the
+// group of value c.  The levels at masks N/2, ..., 1 are re_device.h's
+// reduce_step (DPP moves inside 16-lane rows, a permlane16 swap across).
+template <int N, int M>
+__device__ __forceinline__ void group_levels(float (&v)[N], int c) {
+  if constexpr (M >= 1) {
+    reduce_step<M, 2 * M>(v, c);
+    group_levels<N, M / 2>(v, c);
+  }
+}
 template <int N>
 __device__ __forceinline__ void group_reduce_transpose(float (&v)[N], int c) {
-  int mask = N >> 1;
-#pragma unroll
-  for (int n = N; n > 1; n >>= 1) {
-    const int h = n >> 1;
-    const bool upper = (c & mask) != 0;
-#pragma unroll
-    for (int i = 0; i < h; ++i) {
-      // Opaque copies keep the selects on registers: a select between two
-      // elements of v is otherwise folded into a read of v at a runtime
-      // index, which lowers to a compare-and-select chain over all of v.
-      float lo = v[i], hi = v[i + h];
-      asm("" : "+v"(lo), "+v"(hi));
-      const float send = upper ? lo : hi;
-      const float keep = upper ? hi : lo;
-      v[i] = keep + __shfl_xor(send, mask, 64);
-    }
-    mask >>= 1;
-  }
+  static_assert(N >= 2 && N <= 32 && (N & (N - 1)) == 0, "N must be a power of two in [2, 32]");
+  group_levels<N, N / 2>(v, c);
 }
 
 // Position of load i of lane group r in wave w of tile t.

@@ -279,7 +279,7 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
 #pragma unroll
       for (int h = 0; h < kGrpMaxG; ++h) part[h] = off[i] >= 0 ? dot8(kr[i], qv[h], 0.f) : 0.f;  // missing row: zero key
 #pragma unroll
-      for (int h = 0; h < kGrpMaxG; ++h) part[h] += __shfl_xor(part[h], 8, 64);
+      for (int h = 0; h < kGrpMaxG; ++h) part[h] = xor_add<8>(part[h], lane);
       group_reduce_transpose<kGrpMaxG>(part, c & 7);
       const int j = t * kGrpTile + i * kGrpSlots + r;
       float s = round_bf16(part[0]);  // ExactQk output is bf16
@@ -379,8 +379,8 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
   for (int h = 0; h < kGrpMaxG; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      acc[h][e] += __shfl_xor(acc[h][e], 16, 64);
-      acc[h][e] += __shfl_xor(acc[h][e], 32, 64);
+      acc[h][e] = xor_add<16>(acc[h][e], lane);
+      acc[h][e] = xor_add<32>(acc[h][e], lane);
     }
   if (lane < 16) {
 #pragma unroll
@@ -462,19 +462,29 @@ size_t mgroup_smem_bytes(int G, int window, int blocks_per_row) { return mgroup_
 
 // Wave-wide max / sum of N values at once: the N exchanges of a step are
 // independent, so they wait together.
+template <int S, int N>
+__device__ __forceinline__ void wave_max_steps(float (&v)[N], int lane) {
+  if constexpr (S >= 1) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_max<S>(v[i], lane);
+    wave_max_steps<S / 2>(v, lane);
+  }
+}
+template <int S, int N>
+__device__ __forceinline__ void wave_sum_steps(float (&v)[N], int lane) {
+  if constexpr (S >= 1) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_add<S>(v[i], lane);
+    wave_sum_steps<S / 2>(v, lane);
+  }
+}
 template <int N>
 __device__ __forceinline__ void wave_max_n(float (&v)[N]) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1)
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __shfl_xor(v[i], s, 64));
+  wave_max_steps<32>(v, static_cast<int>(threadIdx.x & 63));
 }
 template <int N>
 __device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1)
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], s, 64);
+  wave_sum_steps<32>(v, static_cast<int>(threadIdx.x & 63));
 }
 
 template <bool P2>

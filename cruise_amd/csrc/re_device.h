@@ -171,16 +171,80 @@ __device__ __forceinline__ float dot8(const Vec8<float>& w, const Vec8<float>& x
   return acc;
 }
 
-// Sum N values (a power of two <= 64) over the 64 lanes of a wavefront by
-// halving exchanges: afterwards lane (64/N)*i holds the total of value i.
-template <int N>
-__device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
-  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
-  int mask = 32;
+// Lane exchanges without the LDS crossbar.  Within a 16-lane row, the value
+// of lane l ^ M (M = 1, 2, 4, 8) comes from DPP moves: quad permutations for
+// 1 and 2, a rotation by 8 for 8, and for 4 a rotation by 4 or by 12 picked
+// by bit 2 of the lane.  Across rows, gfx950's permlane swaps exchange whole
+// halves of two registers: permlane32_swap(x, y) trades x's lanes 32-63 with
+// y's lanes 0-31, permlane16_swap(x, y) x's odd 16-lane rows with y's even
+// ones.  (All checked lane for lane against ds_bpermute on the device.)
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowRor12 = 0x12C;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int M>
+__device__ __forceinline__ float lane_xor_in_row(float v, int lane) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "in-row masks only");
+  if constexpr (M == 1) return dpp_move<kDppQuadXor1>(v);
+  else if constexpr (M == 2) return dpp_move<kDppQuadXor2>(v);
+  else if constexpr (M == 8) return dpp_move<kDppRowRor8>(v);
+  else {
+    const float a = dpp_move<kDppRowRor4>(v), b = dpp_move<kDppRowRor12>(v);
+    return (lane & 4) ? a : b;
+  }
+}
+
+// x, y -> x + y after the swap of permlane32_swap (M = 32) or permlane16_swap
+// (M = 16): lanes whose bit log2(M) is clear get x[l] + x[l + M], the others
+// y[l - M] + y[l] -- one level of the transposing reduction below for a pair
+// of values, and (with x = y) the step v[l] + v[l ^ M] of a plain sum.
+template <int M>
+__device__ __forceinline__ float swap_add(float x, float y) {
+  static_assert(M == 16 || M == 32, "cross-row masks only");
+  const auto r = M == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false)
+                         : __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// v + (v of lane l ^ M) and max(v, v of lane l ^ M), M a power of two <= 32.
+template <int M>
+__device__ __forceinline__ float xor_add(float v, int lane) {
+  if constexpr (M >= 16) return swap_add<M>(v, v);
+  else return v + lane_xor_in_row<M>(v, lane);
+}
+template <int M>
+__device__ __forceinline__ float xor_max(float v, int lane) {
+  if constexpr (M >= 16) {
+    const auto r = M == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                           : __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    return fmaxf(v, lane_xor_in_row<M>(v, lane));
+  }
+}
+
+// One level of the halving exchange at mask M over the first NV values: a
+// lane whose bit log2(M) is set keeps the upper half and sends the lower one,
+// and adds what its partner l ^ M sends (keep + received).  Once one value is
+// left (NV == 1) the step is the plain sum v[0] + v[0] of lane l ^ M.
+template <int M, int NV, int N>
+__device__ __forceinline__ void reduce_step(float (&v)[N], int lane) {
+  constexpr int h = NV / 2;
+  if constexpr (NV == 1) {
+    v[0] = xor_add<M>(v[0], lane);
+  } else if constexpr (M >= 16) {
 #pragma unroll
-  for (int n = N; n > 1; n >>= 1) {
-    const int h = n >> 1;
-    const bool upper = (lane & mask) != 0;
+    for (int i = 0; i < h; ++i) v[i] = swap_add<M>(v[i], v[i + h]);
+  } else {
+    const bool upper = (lane & M) != 0;
 #pragma unroll
     for (int i = 0; i < h; ++i) {
       // Opaque copies keep the selects on registers: a select between two
@@ -188,15 +252,26 @@ __device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
       // index, which lowers to a compare-and-select chain over all of v.
       float lo = v[i], hi = v[i + h];
       asm("" : "+v"(lo), "+v"(hi));
-      float send = upper ? lo : hi;
-      float keep = upper ? hi : lo;
-      float recv = __shfl_xor(send, mask, 64);
-      v[i] = keep + recv;
+      const float send = upper ? lo : hi;
+      const float keep = upper ? hi : lo;
+      v[i] = keep + lane_xor_in_row<M>(send, lane);
     }
-    mask >>= 1;
   }
-#pragma unroll
-  for (; mask >= 1; mask >>= 1) v[0] += __shfl_xor(v[0], mask, 64);
+}
+
+// Sum N values (a power of two <= 64) over the 64 lanes of a wavefront by
+// halving exchanges: afterwards lane (64/N)*i holds the total of value i.
+// Each level halves the values (masks 32, 16, ..., 1); once one is left the
+// remaining masks add it across lanes.
+template <int N>
+__device__ __forceinline__ void wave_reduce_transpose(float (&v)[N], int lane) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+  reduce_step<32, N>(v, lane);
+  reduce_step<16, (N >= 2 ? N / 2 : 1)>(v, lane);
+  reduce_step<8, (N >= 4 ? N / 4 : 1)>(v, lane);
+  reduce_step<4, (N >= 8 ? N / 8 : 1)>(v, lane);
+  reduce_step<2, (N >= 16 ? N / 16 : 1)>(v, lane);
+  reduce_step<1, (N >= 32 ? N / 32 : 1)>(v, lane);
 }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also orders global
@@ -251,23 +326,15 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // The same reductions with the steps inside 16-lane rows on DPP moves (quad
 // swaps, then the 8- and 16-lane mirrors: a few cycles each, no LDS round
-// trip) and only the two steps across rows through ds_bpermute.  Every lane
-// ends with the same value (each step adds or compares a pair symmetrically).
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1, 0, 3, 2]
-constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2, 3, 0, 1]
-constexpr int kDppRowHalfMirror = 0x141;
-constexpr int kDppRowMirror = 0x140;
+// trip) and the two steps across rows on permlane swaps.  Every lane ends
+// with the same value (each step adds or compares a pair symmetrically).
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_move<kDppQuadXor1>(v);
   v += dpp_move<kDppQuadXor2>(v);
   v += dpp_move<kDppRowHalfMirror>(v);
   v += dpp_move<kDppRowMirror>(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
+  v = swap_add<16>(v, v);
+  v = swap_add<32>(v, v);
   return v;
 }
 __device__ __forceinline__ float wave_max_dpp(float v) {
@@ -275,7 +342,7 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, dpp_move<kDppQuadXor2>(v));
   v = fmaxf(v, dpp_move<kDppRowHalfMirror>(v));
   v = fmaxf(v, dpp_move<kDppRowMirror>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  v = xor_max<16>(v, 0);
+  v = xor_max<32>(v, 0);
   return v;
 }
