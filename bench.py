@@ -336,10 +336,11 @@ def bench_scaled(args) -> int:
     step_bytes = rt.info("streamed_weight_bytes") + kv_bytes + B * rt.vocab * 4
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
     # the LM head op (its RMSNorm and the matrix-core projection with its
-    # argmax partials, plus a fold launch on the alternative plan), launched
-    # alone between HIP events on the engine stream
-    lm_kernel = ("k_mf_norm + k_mf_lm_cu (per-CU argmax partials)" if rt.info("lm_cu")
-                 else "k_mf_norm + k_mgemv<2,4,LmHead> + k_mf_fold")
+    # per-CU argmax partials), launched alone between HIP events on the
+    # engine stream
+    if not rt.info("mfma"):
+        raise RuntimeError("the 64-row workload expects the matrix-core plan")
+    lm_kernel = "k_mf_norm + k_mf_lm_cu (per-CU argmax partials)"
     lm_op = rt.info("step_ops") - 1
     lm_ms = rt.time_ops(lm_op, lm_op + 1, iters=20)
     hidden = rt.info("hidden")

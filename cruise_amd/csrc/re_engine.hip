@@ -289,34 +289,22 @@ bool make_plan(Engine& e, const Json& cfg) {
   // cross-check of the two, whose fp32 sums run in different orders.
   if (const Json* t = cfg.get("tuning"))
     if (t->number_or("qkv_ksplit", 1) == 0) p.qkv_ksplit = 0;
-  // 64 bf16 rows of Qwen2.5-7B's shape: projections on the matrix cores
-  // ("tuning": {"mfma": 0} keeps the row-tiled kernels)
   const Json* tune = cfg.get("tuning");
+  // 64 bf16 rows of Qwen2.5-7B's shape: projections on the matrix cores,
+  // gate/up and the LM head one workgroup per CU, qkv, o and down split over
+  // (strip group, K range) (re_mfma.hip); "tuning": {"mfma": 0} keeps the
+  // row-tiled kernels
   p.mfma = 0;
-  p.lm_cu = 0;
-  p.mf_split = 0;
   p.gu_cu = 0;
-  p.part_cu = 0;
-  p.qkv_split = 0;
-  if (mfma_step_supported(d) && (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
+  if (mfma_step_supported(d) && mfma_lm_cu_fits(d, e.cus) && mfma_gu_cu_fits(d, e.cus) && mfma_qkv_split_fits(d) &&
+      (tune == nullptr || tune->number_or("mfma", 1) != 0) && prepare_mfma() == hipSuccess) {
     p.mfma = 1;
-    p.lm_wg = mfma_lm_partials(d);
-    // "tuning": {"lm_cu": 0} keeps the 4-wave LM head and its fold launch
-    p.lm_cu = mfma_lm_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("lm_cu", 1) != 0) ? 1 : 0;
-    // "tuning": {"mf_split": 0} keeps o and down as one workgroup per strip
-    p.mf_split = mfma_split_fits(d) && (tune == nullptr || tune->number_or("mf_split", 1) != 0) ? 1 : 0;
-    // "tuning": {"gu_cu": 0} keeps gate/up as 4-wave workgroups
-    p.gu_cu = mfma_gu_cu_fits(d, e.cus) && (tune == nullptr || tune->number_or("gu_cu", 1) != 0) ? e.cus : 0;
-    // "tuning": {"part_cu": 0} keeps the split o and down projections' waves
-    // fetching their activation fragments each on its own
-    p.part_cu = p.mf_split && (tune == nullptr || tune->number_or("part_cu", 1) != 0) ? 1 : 0;
-    // "tuning": {"qkv_split": 0} keeps qkv as one workgroup per strip
-    p.qkv_split = p.part_cu && mfma_qkv_split_fits(d) && (tune == nullptr || tune->number_or("qkv_split", 1) != 0) ? 1 : 0;
+    p.gu_cu = e.cus;
+    p.lm_wg = e.cus;  // k_mf_lm_cu's workgroups
   }
-  // the 4-wave matrix-core LM head folds its partials to one per row itself;
-  // the per-CU one leaves one per CU
-  p.argmax_parts = p.mfma ? (p.lm_cu ? e.cus : 1) : p.lm_wg;
-  p.argmax_row_major = p.mfma && p.lm_cu ? 1 : 0;
+  // the matrix-core LM head leaves one argmax partial per (row, CU), row-major
+  p.argmax_parts = p.mfma ? e.cus : p.lm_wg;
+  p.argmax_row_major = p.mfma;
   // grouped decode attention: by default for many rows; "tuning":
   // {"grouped_attention": 0 or 1} forces it where the shape allows it
   p.grouped_attn = group_attention_default(d) ? 1 : 0;
@@ -361,14 +349,9 @@ bool make_plan(Engine& e, const Json& cfg) {
   p.o_segments = (d.q_dim() + k_segment_elems() - 1) / k_segment_elems();
   p.down_segments = (d.intermediate + k_segment_elems() - 1) / k_segment_elems();
   // o-proj with exactly seven row pairs per CU (Qwen2.5-7B: 1,792 on 256
-  // CUs): one 7-wave workgroup per CU; "tuning": {"o_waves": 4} keeps
-  // 4-wave workgroups
+  // CUs): one 7-wave workgroup per CU; otherwise 4-wave workgroups
   p.o_waves = p.waves;
   if (d.dtype_bytes == 2 && p.mb == 4 && p.o_segments == 1 && d.hidden / 2 == 7 * e.cus) p.o_waves = 7;
-  if (tune != nullptr) {
-    const int ow = static_cast<int>(tune->number_or("o_waves", p.o_waves));
-    if ((ow == 4 || (ow == 7 && d.dtype_bytes == 2 && p.mb == 4)) && ow != p.o_waves) p.o_waves = ow;
-  }
   p.o_grid = (d.hidden / 2 + p.o_waves - 1) / p.o_waves;
   return true;
 }
@@ -526,7 +509,7 @@ bool alloc_state(Engine& e) {
       {reinterpret_cast<void**>(&e.scratch.inv_freq), (size_t)d.head_dim / 2 * sizeof(float)},
       {reinterpret_cast<void**>(&e.scratch.rope), (size_t)B * d.head_dim * sizeof(float)},
       {&e.scratch.xn, p.mfma ? (size_t)B * d.hidden * T : 0},
-      {reinterpret_cast<void**>(&e.scratch.mf_part), p.mf_split ? mfma_split_partial_bytes(d) : 0},
+      {reinterpret_cast<void**>(&e.scratch.mf_part), p.mfma ? mfma_split_partial_bytes(d) : 0},
       {reinterpret_cast<void**>(&e.scratch.sp_scores), (size_t)p.attn_split * 256 * B * d.heads * sizeof(float)},
       {reinterpret_cast<void**>(&e.scratch.sp_stats), (size_t)p.attn_split * 2 * B * d.heads * sizeof(float)},
       {reinterpret_cast<void**>(&e.scratch.sp_part),
@@ -1729,11 +1712,8 @@ extern "C" int32_t resident_epoch_info(void* engine, const char* key, int64_t* v
       {"qkv_waves", e->plan.qkv_waves},
       {"qkv_ksplit", e->plan.qkv_ksplit},
       {"o_waves", e->plan.o_waves},
-      {"lm_cu", e->plan.lm_cu},
-      {"mf_split", e->plan.mf_split},
+      {"mfma", e->plan.mfma},
       {"gu_cu", e->plan.gu_cu},
-      {"part_cu", e->plan.part_cu},
-      {"qkv_split", e->plan.qkv_split},
       {"grouped_attention", e->plan.grouped_attn},
       {"attention_split", e->plan.attn_split},
       {"argmax_parts", e->plan.argmax_parts},

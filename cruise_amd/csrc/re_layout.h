@@ -148,7 +148,7 @@ struct LaunchPlan {
   int o_waves;            // waves per o-proj workgroup (one row pair each): 4, or 7
   int o_segments, down_segments;  // K-segments of 3584 elements
   int lm_wg;       // workgroups of the LM head (= argmax partial count)
-  int argmax_parts;  // partials per row k_ctrl_step reduces: lm_wg, 1 once folded, or one per CU
+  int argmax_parts;  // partials per row k_ctrl_step reduces: lm_wg, or one per CU (matrix-core LM head)
   int argmax_row_major;  // 1: the partials of a row are contiguous (per-CU LM head)
   int slot_cus;    // > 0: gate/up and LM head use slot-weighted unit ranges (re_step.hip)
   int slot_w[4];   // their per-slot weights
@@ -157,16 +157,8 @@ struct LaunchPlan {
   int down_whole_grid;
   // 1: the projections run on the matrix cores (re_mfma.hip, 64 rows)
   int mfma;
-  // 1 (with mfma): the LM head runs one workgroup per CU (k_mf_lm_cu) and its
-  // per-CU argmax partials go straight to k_ctrl_step
-  int lm_cu;
-  // 1 (with mfma): o and down run split over (7-strip group, K range), their
-  // partials added by the next RMSNorm launch (re_mfma.hip kMfPart)
-  int mf_split;
   // > 0 (with mfma): gate/up runs one workgroup per CU (k_mf_gu_cu), this grid
   int gu_cu;
-  int part_cu;     // 64-row o and down splits with their activations staged in LDS (re_mfma.hip k_mf_part_cu)
-  int qkv_split;   // 64-row qkv split over (9-strip group, K range), epilogue in k_mf_qkv_finish
   // 1: decode attention per (row, KV head) for all query heads of the group
   int grouped_attn;
   int attn_split;  // > 0: decode attention split over the window in this many 256-position tiles

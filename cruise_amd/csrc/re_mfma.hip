@@ -2,19 +2,21 @@
 // 64 batch rows (the scaled-batch configuration): Y[B, N] = X[B, K] W[N, K]^T
 // with v_mfma_f32_16x16x32_bf16, the weights streamed from HBM once per step.
 //
-// Work layout.  A workgroup owns 16 output columns per strip (one strip, or two:
-// gate and up, or two adjacent column groups of the LM head) and splits K
-// evenly over its waves.  Each wave streams its K range of the strip's rows:
-// lane l holds row l % 16 of the strip and elements 8 (l / 16) ..+8 of each
-// 32-wide k step (a 64-byte run per row per load instruction), and the
-// matching activation fragments of the four 16-row batch tiles (read through
-// the cache: every workgroup reads the same activations).  The whole K range
-// is unrolled at compile time: weights are requested kRing steps ahead and
-// activations kXRing steps ahead, with no branch inside the loop.  At the end
-// the waves' accumulators meet in LDS and wave 0 adds them in wave order (a
-// fixed order: results do not depend on timing) and applies the projection's
-// epilogue -- the same operations and roundings as the four-row kernels of
-// re_step.hip:
+// Work layout.  Weights stream as 16-row column strips: lane l holds row
+// l % 16 of the strip and elements 8 (l / 16) ..+8 of each 32-wide k step (a
+// 64-byte run per row per load instruction; the packed copy makes a wave's
+// step one 1 KB run), against the matching activation fragments of the four
+// 16-row batch tiles, staged once per CU in LDS.  Weights are requested kRing
+// (or more) steps ahead with every wait count known at compile time.
+//   LM head, gate/up  one workgroup per CU, each wave a strip (two for
+//                     gate/up) over the whole K (k_mf_lm_cu, k_mf_gu_cu);
+//   o, down, qkv      split over (strip group, K range): each wave one strip
+//                     over one of 8 K ranges, fp32 partials added in range
+//                     order by the next launch (k_mf_part_cu; the next
+//                     RMSNorm for o and down, k_mf_qkv_finish for qkv) -- a
+//                     fixed order, so results do not depend on timing.
+// The epilogues apply the same operations and roundings as the four-row
+// kernels of re_step.hip:
 //   qkv     + bias, RoPE of q and k (the partner element j + d/2 sits in lane
 //           l ^ 8: a strip holds 8 pairs), q out, k and v to the paged slots
 //   gate/up silu(gate) * up
@@ -40,14 +42,9 @@ constexpr int kMfRows = 64;   // batch rows of the configuration
 constexpr int kMfTiles = kMfRows / 16;
 constexpr int kMfK = 32;      // k per MFMA step
 constexpr int kRing = 8;      // weight steps in flight per wave
-// activation steps in flight per wave: 4, or 2 at 16 waves (128 registers)
-template <int WAVES>
-constexpr int x_ring() { return WAVES >= 16 ? 2 : 4; }
 // Qwen2.5-7B's shape, the one these instantiations are compiled for
 constexpr int kMfHidden = 3584;
 constexpr int kMfInter = 18944;
-
-enum MfKind { kMfQkv = 0, kMfGateUp = 1, kMfLm = 2, kMfResid = 3, kMfPart = 4 };
 
 struct MfArgs {
   const int32_t* done;
@@ -69,7 +66,7 @@ struct MfArgs {
   bf16_t* out;
   bf16_t* hidden;
   int hidden_dim;
-  // partial sums (kMfPart): [gridDim.y][B][N] fp32, N = hidden_dim
+  // partial sums of the split launches: [gridDim.y][B][N] fp32, N = hidden_dim
   float* part;
   // LM head
   float* logits;
@@ -88,251 +85,18 @@ __device__ __forceinline__ int qkv_strip_row(int head_dim, int g, int c) {
   return head * head_dim + 8 * t + (c & 7) + (c >= 8 ? half : 0);
 }
 
-// Weight row of column c (0..15) of strip j in workgroup g.
-template <int KIND>
-__device__ __forceinline__ int strip_row(const MfArgs& a, int g, int j, int c) {
-  if constexpr (KIND == kMfQkv) {
-    return qkv_strip_row(a.head_dim, g, c);
-  } else if constexpr (KIND == kMfLm) {
-    return g * 32 + j * 16 + c;
-  } else {
-    return g * 16 + c;  // gate/up: both strips are the same columns
-  }
-}
+// Packed activations: xpack_index (re_device.h).
 
-// Packed activations (XP): xpack_index (re_device.h).
-
-// Waves of a workgroup split K (KSPLIT: qkv, o and down, whose few column
-// strips would not fill the chip otherwise) or N (gate/up and the LM head:
-// every wave owns its columns over the whole K, and the waves of a workgroup
-// read the same activation fragments at about the same time, which the L1
-// cache then serves once).
-template <int KIND>
-constexpr bool k_split() { return KIND == kMfQkv || KIND == kMfResid; }
-
-// kMfPart: the o and down projections split over (strip group, K range):
-// workgroup (x, y) runs strips x * WAVES + wave over the y-th K range of
-// STEPS steps, one strip per wave, and stores its fp32 partial sums.  The
-// K ranges are the ones k_mgemv<..., kMfResid> gives its 8 waves, and the
-// next RMSNorm launch adds the 8 partials in range order (the order wave 0
-// adds the waves' sums there) and the residual: the same results, while a
-// CU fetches one K range of the activations instead of all of them.
-
-template <int NS, int WAVES, int KIND, int STEPS, bool XP>
-__global__ void __launch_bounds__(WAVES * 64) k_mgemv(MfArgs a) {
-  constexpr int kXRing = x_ring<WAVES>();
-  constexpr bool KSPLIT = k_split<KIND>();
-  extern __shared__ __align__(16) float mf_red[];  // KSPLIT: [WAVES - 1][NS * kMfTiles * 4][64]
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  const int c = lane & 15, kq = (lane >> 4) * 8;
-  // column group of this wave: the workgroup's (KSPLIT) or the wave's own
-  const int g = KSPLIT ? blockIdx.x : blockIdx.x * WAVES + wave;
-  const int kstep0 = KSPLIT ? wave * STEPS : (KIND == kMfPart ? (int)blockIdx.y * STEPS : 0);  // first k step
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
-  if (stop != 0) return;  // uniform
-
-  const int kbase = kstep0 * kMfK + kq;
-  // packed weights: tile (strip, step) at ((strip * K/32 + step) * 64 + lane) * 8
-  const bf16_t* wp[NS];
-#pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const bf16_t* base = (KIND == kMfGateUp && j == 1) ? a.p1 : a.p0;
-    const int strip = KIND == kMfLm ? 2 * g + j : g;
-    wp[j] = base + ((size_t)strip * (a.K / kMfK) + kstep0) * 512 + lane * 8;
-  }
-  const bf16_t* xp[kMfTiles];
-  constexpr int kXStep = XP ? 512 : kMfK;  // elements between a fragment's consecutive k steps
-#pragma unroll
-  for (int t = 0; t < kMfTiles; ++t)
-    xp[t] = XP ? a.x + ((size_t)t * (a.K / kMfK) + kstep0) * 512 + lane * 8
-               : a.x + (size_t)min(t * 16 + c, a.B - 1) * a.K + kbase;
-
-  mf_f32x4 acc[NS][kMfTiles];
-#pragma unroll
-  for (int j = 0; j < NS; ++j)
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t) acc[j][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-  re_u32x4 wr[kRing][NS];
-  re_u32x4 xr[kXRing][kMfTiles];
-#pragma unroll
-  for (int s = 0; s < kRing && s < STEPS; ++s)
-#pragma unroll
-    for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * 512));
-#pragma unroll
-  for (int s = 0; s < kXRing && s < STEPS; ++s)
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t) xr[s][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + s * kXStep);
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const int rw = s % kRing, rx = s % kXRing;
-#pragma unroll
-    for (int j = 0; j < NS; ++j)
-#pragma unroll
-      for (int t = 0; t < kMfTiles; ++t)
-        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8, xr[rx][t]),
-                                                            __builtin_bit_cast(mf_bf16x8, wr[rw][j]), acc[j][t], 0,
-                                                            0, 0);
-    if (s + kRing < STEPS) {
-#pragma unroll
-      for (int j = 0; j < NS; ++j)
-        wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + (s + kRing) * 512));
-    }
-    if (s + kXRing < STEPS) {
-#pragma unroll
-      for (int t = 0; t < kMfTiles; ++t) xr[rx][t] = *reinterpret_cast<const re_u32x4*>(xp[t] + (s + kXRing) * kXStep);
-    }
-    // Keep each step's refill where it is: left free, the scheduler sinks the
-    // loads next to their products and every step then waits for memory.
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  if constexpr (KSPLIT) {
-    // The waves' partial sums, added by wave 0 in wave order.
-    constexpr int R = NS * kMfTiles * 4;
-    if (wave > 0) {
-#pragma unroll
-      for (int j = 0; j < NS; ++j)
-#pragma unroll
-        for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) mf_red[((wave - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane] = acc[j][t][v];
-    }
-    lds_barrier();
-    if (wave != 0) return;
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w)
-#pragma unroll
-      for (int j = 0; j < NS; ++j)
-#pragma unroll
-        for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[j][t][v] += mf_red[((w - 1) * R + (j * kMfTiles + t) * 4 + v) * 64 + lane];
-  }
-
-  const int mrow = 4 * (lane >> 4);  // + 16 t + v
-  if constexpr (KIND == kMfQkv) {
-    const int row = strip_row<KIND>(a, g, 0, c);
-    const int half = a.head_dim >> 1;
-    const int head = row / a.head_dim, jj = row - head * a.head_dim;  // jj < half for c < 8
-    const int jpair = c < 8 ? jj : jj - half;
-    const float bias = Elt<bf16_t>::f(a.w1[row]);
-    const bool roped = head < a.heads + a.kv_heads;
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = t * 16 + mrow + v;
-        // F.linear with bias: fp32 sum + bias, one rounding (g4a_linear_t_bias.py:18-21)
-        const float y = Elt<bf16_t>::r(acc[0][t][v] + bias);
-        const float p = __shfl_xor(y, 8, 64);
-        if (m >= a.B) continue;
-        float o = y;
-        if (roped) {
-          // q' = q*cos + rotate_half(q)*sin, each product and the sum rounded
-          // (batched_decoder_step.py:231-240, 323-324)
-          const float cs = a.rope[((size_t)m * half + jpair) * 2], sn = a.rope[((size_t)m * half + jpair) * 2 + 1];
-          o = c < 8 ? Elt<bf16_t>::r(Elt<bf16_t>::r(y * cs) + Elt<bf16_t>::r(-p * sn))
-                    : Elt<bf16_t>::r(Elt<bf16_t>::r(y * cs) + Elt<bf16_t>::r(p * sn));
-        }
-        if (head < a.heads) {
-          a.q[((size_t)m * a.heads + head) * a.head_dim + jj] = Elt<bf16_t>::t(o);
-        } else {
-          // paged slot write, active rows only (batched_decoder_step.py:250-264)
-          const int s = a.slot[m];
-          if (a.active[m] != 0 && s >= 0 && s < a.slots) {
-            const bool is_key = head < a.heads + a.kv_heads;
-            const int kvh = is_key ? head - a.heads : head - a.heads - a.kv_heads;
-            bf16_t* cache = is_key ? a.key_cache : a.value_cache;
-            cache[((size_t)s * a.kv_heads + kvh) * a.head_dim + jj] = Elt<bf16_t>::t(o);
-          }
-        }
-      }
-  } else if constexpr (KIND == kMfGateUp) {
-    const int n = strip_row<KIND>(a, g, 0, c);
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = t * 16 + mrow + v;
-        if (m >= a.B) continue;
-        // silu(gate) * up, each result rounded (batched_decoder_step.py:391-398)
-        const float gt = Elt<bf16_t>::r(acc[0][t][v]);
-        const float up = Elt<bf16_t>::r(acc[1][t][v]);
-        const float sg = Elt<bf16_t>::r(gt / (1.0f + expf(-gt)));
-        a.out[xpack_index(m, n, a.hidden_dim)] = Elt<bf16_t>::t(Elt<bf16_t>::r(sg * up));
-      }
-  } else if constexpr (KIND == kMfPart) {
-    const int n = strip_row<KIND>(a, g, 0, c);
-    float* part = a.part + (size_t)blockIdx.y * a.B * a.hidden_dim;
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = t * 16 + mrow + v;
-        if (m < a.B) part[(size_t)m * a.hidden_dim + n] = acc[0][t][v];
-      }
-  } else if constexpr (KIND == kMfResid) {
-    const int n = strip_row<KIND>(a, g, 0, c);
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = t * 16 + mrow + v;
-        if (m >= a.B) continue;
-        bf16_t* h = a.hidden + (size_t)m * a.hidden_dim + n;
-        *h = f_to_bf16(bf16_to_f(*h) + round_bf16(acc[0][t][v]));
-      }
-  } else {
-    // LM head in T, then .float() (batched_decoder_step.py:405-408); the
-    // first index of the maximum over this workgroup's 32 columns (CTRL:99-119)
-#pragma unroll
-    for (int t = 0; t < kMfTiles; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = t * 16 + mrow + v;
-        const int n0 = strip_row<KIND>(a, g, 0, c), n1 = n0 + 16;
-        const float l0 = Elt<bf16_t>::r(acc[0][t][v]), l1 = Elt<bf16_t>::r(acc[1][t][v]);
-        const bool mine = m < a.B;
-        if (mine) {
-          a.logits[(size_t)m * a.vocab + n0] = l0;
-          a.logits[(size_t)m * a.vocab + n1] = l1;
-        }
-        int bad = (!isfinite(l0) || !isfinite(l1)) ? 1 : 0;
-        float bv = l0;
-        int bi = n0;
-        if (l1 > bv) {
-          bv = l1;
-          bi = n1;
-        }
-#pragma unroll
-        for (int x = 1; x < 16; x <<= 1) {
-          const float ov = __shfl_xor(bv, x, 64);
-          const int oi = __shfl_xor(bi, x, 64);
-          bad |= __shfl_xor(bad, x, 64);
-          if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
-        if (mine && c == 0) {
-          a.am_val[(size_t)g * a.B + m] = bv;
-          a.am_idx[(size_t)g * a.B + m] = bi;
-          a.am_bad[(size_t)g * a.B + m] = bad;
-        }
-      }
-  }
-}
-
-// LM head with one workgroup per CU (the default for 64 rows).  k_mgemv's
-// 4-wave workgroups (4.6 per CU) each fetch the whole 64 x K activation block,
-// 0.7 GB per step on top of the 1.09 GB of weights; here the 8 waves of a CU's
-// one workgroup share one copy, staged through LDS in blocks of 16 k steps
+// LM head with one workgroup per CU.  Workgroups of a few waves would each
+// fetch the whole 64 x K activation block (with 4-wave workgroups, 0.7 GB per
+// step on top of the 1.09 GB of weights); here the 8 waves of a CU's one
+// workgroup share one copy, staged through LDS in blocks of 16 k steps
 // (64 KB, two buffers, filled by global -> LDS loads).  Workgroup g owns
 // strips [g T / G, (g + 1) T / G) of the T = V / 16 column strips; wave w
 // owns strips w, w + 8, ... of that range (NS = 4 or 5 of them) over the whole
 // K, with kLcRing k steps of weights in flight.  Per step a wave reads the
-// four batch tiles' fragments from LDS and runs NS x 4 products.  The logits
-// are those of k_mgemv; the argmax partial of (workgroup, row) is the first
+// four batch tiles' fragments from LDS and runs NS x 4 products, every logit
+// one chain of MFMA steps in k order; the argmax partial of (workgroup, row) is the first
 // index of the maximum over the workgroup's columns (CTRL:99-119), combined
 // over the waves in wave order, stored row-major ([row][G]).
 constexpr int kLcWaves = 8;
@@ -511,9 +275,9 @@ __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_lm_cu(MfArgs a) {
 
 // gate/up with one workgroup per CU (64 rows): the I / 16 column strips are
 // split over the CUs (4-5 each for Qwen2.5-7B), wave w < that count streams
-// strip s_begin + w of the gate and of the up matrix over the whole K -- the
-// step chains of k_mgemv's gate/up waves -- sharing the LDS-staged
-// activations with the other waves; the SiLU * up epilogue is k_mgemv's.
+// strip s_begin + w of the gate and of the up matrix over the whole K,
+// sharing the LDS-staged activations with the other waves, then the SiLU *
+// up epilogue.
 constexpr int kGcRing = 16;  // weight steps in flight per wave (few waves stream)
 
 __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_gu_cu(MfArgs a) {
@@ -548,14 +312,14 @@ __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_gu_cu(MfArgs a) {
 }
 
 // o, down and qkv split over (strip group, K range) with the range's
-// activations staged in LDS: k_mgemv<..., kMfPart, ...> lets each of its
-// waves fetch the range's fragments (4 tiles x 1 KB per k step) on its own;
-// here the waves copy them to LDS together (global -> LDS, one 1 KB fragment
-// per instruction), in blocks of BLK steps through two buffers, and each wave
-// reads them from LDS while it streams its strip's weights with kRing steps
-// in flight.  Every count is known at compile time, so each wait is exact.
-// Each strip is k_mgemv's chain of MFMA steps in the same order, so the
-// partials are the same bits.  QKV: the partial of column c of strip g goes
+// activations staged in LDS: workgroup (x, y) runs strips x * WAVES + wave
+// over the y-th of 8 K ranges, one strip per wave.  The waves copy the
+// range's activation fragments (4 tiles x 1 KB per k step) to LDS together
+// (global -> LDS, one 1 KB fragment per instruction), in blocks of BLK steps
+// through two buffers, and each wave reads them from LDS while it streams its
+// strip's weights with kRing steps in flight.  Every count is known at
+// compile time, so each wait is exact.  A CU fetches one K range of the
+// activations instead of all of them.  QKV: the partial of column c of strip g goes
 // to qkv row qkv_strip_row(g, c) (N = the qkv rows, k_mf_qkv_finish adds
 // them up); otherwise to column 16 g + c (N = hidden, the next norm adds them).
 template <int STEPS, int BLK>
@@ -670,8 +434,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_mf_part_cu(MfArgs a) {
 }
 
 // The qkv epilogue after k_mf_part_cu: the 8 K-range partials added in range
-// order (the order k_mgemv's wave 0 adds its waves' sums), then bias, RoPE
-// and the q / paged K/V writes exactly as k_mgemv<..., kMfQkv, ...> does them.
+// order, then bias, RoPE and the q / paged K/V writes (the four-row qkv
+// epilogue's roundings).
 // Thread: one (row, head, pair j < d/2), both elements of the RoPE pair.
 template <int RANGES>
 __global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a) {
@@ -724,11 +488,6 @@ __global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a) {
       cache[j + half] = Elt<bf16_t>::t(o1);
     }
   }
-}
-
-template <int NS, int WAVES, int KIND>
-constexpr size_t mgemv_lds() {
-  return k_split<KIND>() ? (size_t)(WAVES - 1) * NS * kMfTiles * 4 * 64 * sizeof(float) : 0;
 }
 
 // RMSNorm of each row into a normalized copy, packed like the activations the
@@ -795,58 +554,8 @@ __global__ void __launch_bounds__(256) k_mf_norm(const int32_t* done, bf16_t* h,
   }
 }
 
-// The LM head's per-workgroup argmax partials folded to one per row, written
-// over partial 0 of the row: the first index of the maximum (CTRL:99-119),
-// any non-finite flag kept.  One workgroup per row; every partial is read
-// before thread 0 overwrites the first.
-__global__ void __launch_bounds__(256) k_mf_fold(const int32_t* done, float* val, int32_t* idx, int32_t* bad,
-                                               int parts, int B) {
-  __shared__ float sv[4];
-  __shared__ int si[4], sb[4];
-  if (done != nullptr && __builtin_nontemporal_load(done) != 0) return;
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  float bv = 0.f;
-  int bi = -1, bb = 0;
-  for (int w = tid; w < parts; w += 256) {
-    const float v = val[(size_t)w * B + b];
-    const int i = idx[(size_t)w * B + b];
-    bb |= bad[(size_t)w * B + b];
-    if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
-      bv = v;
-      bi = i;
-    }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(bv, m, 64);
-    const int oi = __shfl_xor(bi, m, 64);
-    bb |= __shfl_xor(bb, m, 64);
-    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-      bv = ov;
-      bi = oi;
-    }
-  }
-  if (lane == 0) {
-    sv[wave] = bv;
-    si[wave] = bi;
-    sb[wave] = bb;
-  }
-  __syncthreads();
-  if (tid != 0) return;
-  for (int w = 1; w < 4; ++w) {
-    bb |= sb[w];
-    if (si[w] >= 0 && (bi < 0 || sv[w] > bv || (sv[w] == bv && si[w] < bi))) {
-      bv = sv[w];
-      bi = si[w];
-    }
-  }
-  val[b] = bv;
-  idx[b] = bi;
-  bad[b] = bb;
-}
-
 // The packed copy of one [rows, K] matrix: 16-byte unit u = (strip * K/32 +
-// step) * 64 + lane holds row strip_row(strip, lane % 16), elements
+// step) * 64 + lane holds row strip * 16 + lane % 16 (qkv: qkv_strip_row), elements
 // step * 32 + 8 (lane / 16) ..+8.
 __global__ void k_mf_pack(const bf16_t* src, bf16_t* dst, int rows, int K, int qkv_head_dim) {
   const long long units = (long long)rows / 16 * (K / kMfK) * 64;
@@ -863,37 +572,23 @@ __global__ void k_mf_pack(const bf16_t* src, bf16_t* dst, int rows, int K, int q
   }
 }
 
-// The launches of one projection: (strips per workgroup, waves per
-// workgroup, kind, k steps per wave).
-constexpr int kQkvWaves = 8, kOWaves = 8, kGuWaves = 4, kDownWaves = 8, kLmWaves = 4;
-constexpr int kHidSteps(int waves) { return kMfHidden / kMfK / waves; }
-constexpr int kHidAll = kMfHidden / kMfK;  // the whole K of the N-split projections
-constexpr int kInterSteps = kMfInter / kMfK / kDownWaves;
-// split o / down: 7 strips (one per wave) by the 8 K ranges of the kernels above
-constexpr int kPartWaves = 7, kPartRanges = 8;
+// The split launches: K in 8 ranges of kHidSteps(8) (hidden) or kInterSteps
+// (intermediate) k steps; o / down run 7 strips (one per wave) per workgroup.
+constexpr int kPartRanges = 8;
+constexpr int kHidSteps(int ranges) { return kMfHidden / kMfK / ranges; }
+constexpr int kInterSteps = kMfInter / kMfK / kPartRanges;
+constexpr int kPartWaves = 7;
 // the staged split kernels: o and qkv stage their 14-step K range at once,
 // down its 74 steps in blocks of 16
 constexpr int kQkvPartWaves = 9;  // qkv strips per workgroup: 288 = 32 x 9
 constexpr int kDownBlk = 16;
-static_assert(kOWaves == kPartRanges && kDownWaves == kPartRanges, "split ranges follow the K-split waves");
-
-template <int NS, int WAVES, int KIND, int STEPS, bool XP>
-hipError_t mgemv_prepare() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_mgemv<NS, WAVES, KIND, STEPS, XP>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mgemv_lds<NS, WAVES, KIND>()));
-}
-
-template <int NS, int WAVES, int KIND, int STEPS, bool XP>
-void mgemv_launch(const MfArgs& a, dim3 grid, hipStream_t stream) {
-  k_mgemv<NS, WAVES, KIND, STEPS, XP><<<grid, WAVES * 64, mgemv_lds<NS, WAVES, KIND>(), stream>>>(a);
-}
 
 }  // namespace
 
 bool mfma_step_supported(const Dims& d) {
   return d.dtype_bytes == 2 && d.batch == kMfRows && d.hidden == kMfHidden && d.q_dim() == kMfHidden &&
          d.intermediate == kMfInter && d.head_dim % 16 == 0 && d.qkv_rows() % 16 == 0 &&
-         d.vocab % (32 * kLmWaves) == 0 && d.hidden % 16 == 0;
+         d.vocab % 32 == 0 && d.hidden % 16 == 0;
 }
 
 int mfma_lm_partials(const Dims& d) { return d.vocab / 32; }
@@ -957,22 +652,14 @@ static void part_cu_launch(const MfArgs& a, int groups, hipStream_t stream) {
 }
 
 hipError_t prepare_mfma() {
-  hipError_t e = mgemv_prepare<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>();
-  if (e == hipSuccess) e = mgemv_prepare<1, kOWaves, kMfResid, kHidSteps(kOWaves), true>();
-  if (e == hipSuccess) e = mgemv_prepare<2, kGuWaves, kMfGateUp, kHidAll, true>();
-  if (e == hipSuccess) e = mgemv_prepare<1, kDownWaves, kMfResid, kInterSteps, true>();
-  if (e == hipSuccess) e = mgemv_prepare<2, kLmWaves, kMfLm, kHidAll, true>();
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_lm_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(kLcLds));
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_lm_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(kLcLds));
   if (e == hipSuccess)
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_mf_gu_cu), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(kLcLds));
-  if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kHidSteps(kOWaves), true>();
-  if (e == hipSuccess) e = mgemv_prepare<1, kPartWaves, kMfPart, kInterSteps, true>();
-  if (e == hipSuccess) e = part_cu_prepare<kHidSteps(kOWaves), kPartWaves, kHidSteps(kOWaves), false>();
+  if (e == hipSuccess) e = part_cu_prepare<kHidSteps(kPartRanges), kPartWaves, kHidSteps(kPartRanges), false>();
   if (e == hipSuccess) e = part_cu_prepare<kInterSteps, kPartWaves, kDownBlk, false>();
-  if (e == hipSuccess) e = part_cu_prepare<kHidSteps(kOWaves), kQkvPartWaves, kHidSteps(kOWaves), true>();
+  if (e == hipSuccess) e = part_cu_prepare<kHidSteps(kPartRanges), kQkvPartWaves, kHidSteps(kPartRanges), true>();
   return e;
 }
 
@@ -999,7 +686,8 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
   auto wt = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.weights + off); };
   auto pk = [&](size_t off) { return reinterpret_cast<const bf16_t*>(env.packed + off); };
   if (op == MfmaOp::kLmHead) {
-    mf_norm(env, st, env.final_norm_off, env.plan.mf_split != 0, stream);
+    // the last layer's down projection is still in partials
+    mf_norm(env, st, env.final_norm_off, true, stream);
     a.x = static_cast<const bf16_t*>(sc.xn);
     a.p0 = pk(env.packed_lm_off);
     a.K = d.hidden;
@@ -1008,22 +696,17 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
     a.am_idx = sc.am_idx;
     a.am_bad = sc.am_bad;
     a.vocab = d.vocab;
-    if (env.plan.lm_cu) {
-      // one workgroup per CU; its argmax partials go straight to k_ctrl_step
-      k_mf_lm_cu<<<env.plan.argmax_parts, kLcWaves * 64, kLcLds, stream>>>(a);
-      return hipGetLastError();
-    }
-    mgemv_launch<2, kLmWaves, kMfLm, kHidAll, true>(a, d.vocab / 32 / kLmWaves, stream);
-    k_mf_fold<<<d.batch, 256, 0, stream>>>(st.done, sc.am_val, sc.am_idx, sc.am_bad, d.vocab / 32, d.batch);
+    // one workgroup per CU; its argmax partials go straight to k_ctrl_step
+    k_mf_lm_cu<<<env.plan.argmax_parts, kLcWaves * 64, kLcLds, stream>>>(a);
     return hipGetLastError();
   }
   const LayerOffsets& lo = env.layer_off[layer];
   const PackedOffsets& po = env.packed_off[layer];
   const size_t cache_layer_elems = (size_t)d.slots() * d.kv_dim();
   switch (op) {
-    case MfmaOp::kQkv:
+    case MfmaOp::kQkv: {
       // layer > 0: the previous layer's down projection is still in partials
-      mf_norm(env, st, lo.input_norm, env.plan.mf_split != 0 && layer > 0, stream);
+      mf_norm(env, st, lo.input_norm, layer > 0, stream);
       a.x = static_cast<const bf16_t*>(sc.xn);
       a.p0 = pk(po.qkv);
       a.w1 = wt(lo.qkv_b);
@@ -1038,62 +721,42 @@ hipError_t launch_mfma_op(MfmaOp op, const KernelEnv& env, const StepPtrs& st, i
       a.heads = d.heads;
       a.kv_heads = d.kv_heads;
       a.head_dim = d.head_dim;
-      if (env.plan.qkv_split) {
-        // 8 K-range partials per qkv row, then the epilogue in k_mf_qkv_finish
-        a.part = sc.mf_part;
-        a.hidden_dim = d.qkv_rows();
-        part_cu_launch<kHidSteps(kOWaves), kQkvPartWaves, kHidSteps(kOWaves), true>(a, d.qkv_rows() / 16 / kQkvPartWaves,
-                                                                                   stream);
-        const int threads = d.batch * (d.qkv_rows() / d.head_dim) * (d.head_dim / 2);
-        k_mf_qkv_finish<kPartRanges><<<(threads + 255) / 256, 256, 0, stream>>>(a);
-      } else {
-        mgemv_launch<1, kQkvWaves, kMfQkv, kHidSteps(kQkvWaves), true>(a, d.qkv_rows() / 16, stream);
-      }
+      // 8 K-range partials per qkv row, then the epilogue in k_mf_qkv_finish
+      a.part = sc.mf_part;
+      a.hidden_dim = d.qkv_rows();
+      part_cu_launch<kHidSteps(kPartRanges), kQkvPartWaves, kHidSteps(kPartRanges), true>(
+          a, d.qkv_rows() / 16 / kQkvPartWaves, stream);
+      const int threads = d.batch * (d.qkv_rows() / d.head_dim) * (d.head_dim / 2);
+      k_mf_qkv_finish<kPartRanges><<<(threads + 255) / 256, 256, 0, stream>>>(a);
       break;
+    }
     case MfmaOp::kO:
       // the attention writes its output packed on this path (AttnArgs::packed_out)
       a.x = static_cast<const bf16_t*>(sc.attn);
       a.p0 = pk(po.o);
       a.K = d.q_dim();
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      if (env.plan.mf_split && env.plan.part_cu) {
-        a.part = sc.mf_part;
-        part_cu_launch<kHidSteps(kOWaves), kPartWaves, kHidSteps(kOWaves), false>(a, d.hidden / 16 / kPartWaves, stream);
-      } else if (env.plan.mf_split) {
-        a.part = sc.mf_part;
-        mgemv_launch<1, kPartWaves, kMfPart, kHidSteps(kOWaves), true>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges),
-                                                                        stream);
-      } else {
-        mgemv_launch<1, kOWaves, kMfResid, kHidSteps(kOWaves), true>(a, d.hidden / 16, stream);
-      }
+      a.part = sc.mf_part;
+      part_cu_launch<kHidSteps(kPartRanges), kPartWaves, kHidSteps(kPartRanges), false>(a, d.hidden / 16 / kPartWaves,
+                                                                                         stream);
       break;
     case MfmaOp::kGateUp:
-      mf_norm(env, st, lo.post_norm, env.plan.mf_split != 0, stream);
+      mf_norm(env, st, lo.post_norm, true, stream);
       a.x = static_cast<const bf16_t*>(sc.xn);
       a.p0 = pk(po.gate);
       a.p1 = pk(po.up);
       a.K = d.hidden;
       a.out = static_cast<bf16_t*>(sc.mlp);
       a.hidden_dim = d.intermediate;
-      if (env.plan.gu_cu > 0)
-        k_mf_gu_cu<<<env.plan.gu_cu, kLcWaves * 64, kLcLds, stream>>>(a);
-      else
-        mgemv_launch<2, kGuWaves, kMfGateUp, kHidAll, true>(a, d.intermediate / 16 / kGuWaves, stream);
+      k_mf_gu_cu<<<env.plan.gu_cu, kLcWaves * 64, kLcLds, stream>>>(a);
       break;
     case MfmaOp::kDown:
       a.x = static_cast<const bf16_t*>(sc.mlp);
       a.p0 = pk(po.down);
       a.K = d.intermediate;
       a.hidden = static_cast<bf16_t*>(sc.hidden);
-      if (env.plan.mf_split && env.plan.part_cu) {
-        a.part = sc.mf_part;
-        part_cu_launch<kInterSteps, kPartWaves, kDownBlk, false>(a, d.hidden / 16 / kPartWaves, stream);
-      } else if (env.plan.mf_split) {
-        a.part = sc.mf_part;
-        mgemv_launch<1, kPartWaves, kMfPart, kInterSteps, true>(a, dim3(d.hidden / 16 / kPartWaves, kPartRanges), stream);
-      } else {
-        mgemv_launch<1, kDownWaves, kMfResid, kInterSteps, true>(a, d.hidden / 16, stream);
-      }
+      a.part = sc.mf_part;
+      part_cu_launch<kInterSteps, kPartWaves, kDownBlk, false>(a, d.hidden / 16 / kPartWaves, stream);
       break;
     default:
       return hipErrorInvalidValue;
