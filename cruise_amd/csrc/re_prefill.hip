@@ -5,7 +5,7 @@
 //   embed      token rows + per-token RoPE table
 //   rmsnorm    one workgroup per token
 //   GEMM       C[M,N] = A[M,K] W[N,K]^T, both operands K-contiguous.
-//              bf16: MFMA v_mfma_f32_32x32x16_bf16, 256x256 workgroup tiles
+//              bf16: MFMA v_mfma_f32_16x16x32_bf16, 256x256 workgroup tiles
 //              (eight waves of 128x64), K in steps of 64 through two LDS
 //              stages filled by direct global -> LDS loads, fp32
 //              accumulation; epilogues "T(acc + bias)", the residual
@@ -30,6 +30,7 @@ namespace re {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ bf16x8_t lds_frag(const bf16_t* p) {
@@ -149,13 +150,19 @@ __global__ void __launch_bounds__(256) k_pf_qkv_post(PrefillQkv a) {
 // rows 0..255, then A tile rows 256..511, 128 bytes (one K step) per row.
 // Chunk c (16 bytes) of row r sits in slot c ^ gemm_swz(r), so the fragment
 // reads below hit distinct banks for 8 and for 16 consecutive rows.  The
-// products run as C^T = W A^T on v_mfma_f32_32x32x16_bf16: wave (wn, wm) owns
-// n 128 x m 64 (4 x 2 tiles of 32 x 32), and a lane's accumulator holds four
-// consecutive output columns of one row.  While the waves multiply stage kt,
-// stage kt + 1 is in flight; each wave waits only for its own loads, then
-// the barrier publishes the stage.  The epilogue rounds the tile to bf16 in
-// LDS (rows padded to 264 elements) and writes it as row-contiguous 16-byte
-// vectors: "T(acc + bias)" (qkv), or the residual "T(h + T(acc))".
+// products run as C^T = W A^T on v_mfma_f32_16x16x32_bf16: wave (wn, wm) owns
+// n 128 x m 64 (8 x 4 tiles of 16 x 16), and a lane's accumulator holds four
+// consecutive output columns of one row.  A stage is two sub-steps of K = 32;
+// each sub-step's 12 fragments are read under the previous sub-step's 32
+// products, one read per two products.  The stage's one barrier sits between
+// its sub-steps: before it each wave waits for its own loads of stage kt + 1
+// and its reads of stage kt, so after it stage kt + 1 is complete in LDS and
+// stage kt's buffer is free.  The loads of stage kt + 2 go out right after
+// the barrier, and stage kt + 1's first fragments are read under the second
+// sub-step's products, so no wave waits on LDS at a stage boundary.  The
+// epilogue rounds the tile to bf16 in LDS (rows padded to 264 elements) and
+// writes it as row-contiguous 16-byte vectors: "T(acc + bias)" (qkv), or the
+// residual "T(h + T(acc))".
 //
 // Workgroups are dispatched round-robin over the 8 XCDs; workgroup b runs
 // tile t = (b % 8) * ceil(T / 8) + b / 8 of a grouped order (4 M tiles by
@@ -233,7 +240,7 @@ __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, 
     goff[i] = static_cast<uint32_t>(min(local, rows_left - 1) * ld * 2 + chunk * 16);
   }
   const int nk = a.K / kGk;
-  auto issue = [&](int kt) {  // the last stage is re-read past the end (clamped, never used)
+  auto issue = [&](int kt) {  // stages past the end re-read the last one (clamped, never used)
     const char* g = gbase + (size_t)min(kt, nk - 1) * kGrowBytes;
     unsigned char* l = gsm + (kt & 1) * kGstage + row0 * kGrowBytes;
 #pragma unroll
@@ -241,82 +248,82 @@ __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, 
       __builtin_amdgcn_global_load_lds((gemm_gptr)(g + goff[i]), (gemm_lptr)(l + i * 1024), 16, 0, 0);
   };
   const int wn = wave & 1, wm = wave >> 1;
-  f32x16_t acc[4][2];
+  f32x4_t acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  // lane l supplies row l % 32 of a 32-row operand tile, K elements
-  // 8 (l / 32) ..+8 of the 16-wide sub-step
-  const int fr = lane & 31, fh = lane >> 5;
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
+  // lane l supplies row l % 16 of a 16-row operand tile, K elements
+  // 8 (l / 16) ..+8 of the 32-wide sub-step
+  const int fr = lane & 15, fq = lane >> 4;
   auto frag = [&](int st, int row, int ks) -> bf16x8_t {
-    const int c = (2 * ks + fh) ^ gemm_swz(row);
+    const int c = (4 * ks + fq) ^ gemm_swz(row);
     return lds_frag(reinterpret_cast<const bf16_t*>(gsm + st * kGstage + row * kGrowBytes + c * 16));
   };
+  // fragment sets: [set][0..7] W rows (n), [set][8..11] A rows (m)
+  bf16x8_t f[2][12];
+  auto read_set = [&](int set, int st, int ks) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[set][i] = frag(st, wn * 128 + i * 16 + fr, ks);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[set][8 + j] = frag(st, kGn + wm * 64 + j * 16 + fr, ks);
+  };
+  auto products = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[set][i], f[set][8 + j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 12; ++r) {  // one fragment read per two products
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
   issue(0);
-  gemm_stage_barrier();
+  issue(1);
+  __builtin_amdgcn_s_waitcnt(gemm_wait_vm(kGdmaInsts));  // this wave's stage 0
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  read_set(0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & 1;
-    issue(kt + 1);
-    // fragments of sub-step ks + 1 are read while the products of ks run
-    bf16x8_t fa[2][4], fb[2][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[0][i] = frag(st, wn * 128 + i * 32 + fr, 0);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) fb[0][j] = frag(st, kGn + wm * 64 + j * 32 + fr, 0);
+    read_set(1, st, 1);
+    products(0);
+    gemm_stage_barrier();  // stage kt + 1 complete, stage kt's buffer free
+    issue(kt + 2);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ks = 0; ks < kGk / 16; ++ks) {
-      const int c = ks & 1, n = c ^ 1;
-      if (ks + 1 < kGk / 16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) fa[n][i] = frag(st, wn * 128 + i * 32 + fr, ks + 1);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) fb[n][j] = frag(st, kGn + wm * 64 + j * 32 + fr, ks + 1);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][i], fb[c][j], acc[i][j], 0, 0, 0);
-      if (ks + 1 < kGk / 16) {
-#pragma unroll
-        for (int r = 0; r < 6; ++r) {  // one fragment read per product
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    gemm_stage_barrier();
+    read_set(0, st ^ 1, 0);  // past the last stage: a buffer in flight, never used
+    products(1);
   }
-  // acc[i][j] value v of lane l: n = 32 i + 8 (v / 4) + 4 (l / 32) + v % 4,
-  // m = 32 j + l % 32 within the wave's block
+  gemm_stage_barrier();
+  // acc[i][j] value v of lane l: n = 16 i + 4 (l / 16) + v, m = 16 j + l % 16
+  // within the wave's block
   bf16_t* T = reinterpret_cast<bf16_t*>(gsm);
   const bf16_t* bias = static_cast<const bf16_t*>(a.bias);
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i) {
+      const int ml = wm * 64 + j * 16 + fr, nl = wn * 128 + i * 16 + 4 * fq;
+      float y[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int ml = wm * 64 + j * 32 + fr, nl = wn * 128 + i * 32 + 8 * q + 4 * fh;
-        float y[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = acc[i][j][4 * q + e];
-        if (EPI == kGemmStore && bias != nullptr) {
-          const uint2 b = *reinterpret_cast<const uint2*>(bias + min(n0 + nl, a.N - 4));
-          y[0] += __uint_as_float(b.x << 16);
-          y[1] += __uint_as_float(b.x & 0xffff0000u);
-          y[2] += __uint_as_float(b.y << 16);
-          y[3] += __uint_as_float(b.y & 0xffff0000u);
-        }
-        *reinterpret_cast<uint2*>(T + ml * kGoutLd + nl) =
-            make_uint2(f_to_bf16(y[0]) | ((uint32_t)f_to_bf16(y[1]) << 16),
-                       f_to_bf16(y[2]) | ((uint32_t)f_to_bf16(y[3]) << 16));
+      for (int e = 0; e < 4; ++e) y[e] = acc[i][j][e];
+      if (EPI == kGemmStore && bias != nullptr) {
+        const uint2 b = *reinterpret_cast<const uint2*>(bias + min(n0 + nl, a.N - 4));
+        y[0] += __uint_as_float(b.x << 16);
+        y[1] += __uint_as_float(b.x & 0xffff0000u);
+        y[2] += __uint_as_float(b.y << 16);
+        y[3] += __uint_as_float(b.y & 0xffff0000u);
       }
+      *reinterpret_cast<uint2*>(T + ml * kGoutLd + nl) =
+          make_uint2(f_to_bf16(y[0]) | ((uint32_t)f_to_bf16(y[1]) << 16),
+                     f_to_bf16(y[2]) | ((uint32_t)f_to_bf16(y[3]) << 16));
+    }
   gemm_stage_barrier();
   bf16_t* out = static_cast<bf16_t*>(a.out);
   if constexpr (kSwiGlu) {
