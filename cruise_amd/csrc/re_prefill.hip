@@ -157,9 +157,11 @@ __global__ void __launch_bounds__(256) k_pf_qkv_post(PrefillQkv a) {
 // products, one read per two products.  The stage's one barrier sits between
 // its sub-steps: before it each wave waits for its own loads of stage kt + 1
 // and its reads of stage kt, so after it stage kt + 1 is complete in LDS and
-// stage kt's buffer is free.  The loads of stage kt + 2 go out right after
-// the barrier, and stage kt + 1's first fragments are read under the second
-// sub-step's products, so no wave waits on LDS at a stage boundary.  The
+// stage kt's buffer is free.  The loads of stage kt + 2 go out during the
+// second sub-step (waves 0-3 at its start, waves 4-7 after 12 of their 32
+// products, so the two waves of a SIMD do not stall on them together), and
+// stage kt + 1's first fragments are read under the second sub-step's
+// products, so no wave waits on LDS at a stage boundary.  The
 // epilogue rounds the tile to bf16 in LDS (rows padded to 264 elements) and
 // writes it as row-contiguous 16-byte vectors: "T(acc + bias)" (qkv), or the
 // residual "T(h + T(acc))".
@@ -213,7 +215,8 @@ __device__ __forceinline__ void gemm_tile_of(int b, int nM, int nN, int& mt, int
 template <int EPI>
 __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, int nN) {
   extern __shared__ __align__(16) unsigned char gsm[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave-uniform, so the load base lives in SGPRs (32-bit per-lane offsets)
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
   int mt, nt;
   gemm_tile_of(blockIdx.x, nM, nN, mt, nt);
   // The SwiGLU epilogue's tile covers 128 output columns: W tile rows 0..127
@@ -295,10 +298,28 @@ __global__ void __launch_bounds__(kGthreads, 1) k_gemm_bf16(GemmArgs a, int nM, 
     read_set(1, st, 1);
     products(0);
     gemm_stage_barrier();  // stage kt + 1 complete, stage kt's buffer free
-    issue(kt + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    read_set(0, st ^ 1, 0);  // past the last stage: a buffer in flight, never used
-    products(1);
+    // Second sub-step, in a fixed order: the 32 products row block by row
+    // block, the next stage's 12 first fragments one per two products (past
+    // the last stage: a buffer in flight, never used), and the loads of
+    // stage kt + 2.  The two waves of a SIMD (w and w + 4) issue their loads
+    // apart: an issuing wave waits while the memory pipeline takes its
+    // eight 1 KB requests, and meanwhile the other wave's products run.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i == 0 && wave < 4) issue(kt + 2);
+      if (i == 3 && wave >= 4) issue(kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[1][i], f[1][8 + j], acc[i][j], 0, 0, 0);
+        if (i < 6 && (j & 1)) {
+          const int idx = 2 * i + (j >> 1);
+          f[0][idx] = idx < 8 ? frag(st ^ 1, wn * 128 + idx * 16 + fr, 0)
+                              : frag(st ^ 1, kGn + wm * 64 + (idx - 8) * 16 + fr, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
   gemm_stage_barrier();
   // acc[i][j] value v of lane l: n = 16 i + 4 (l / 16) + v, m = 16 j + l % 16
