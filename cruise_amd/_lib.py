@@ -94,6 +94,10 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int32,
         [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_float)],
     ),
+    "resident_epoch_gemm": (
+        ctypes.c_int32,
+        [ctypes.c_void_p] * 5 + [ctypes.c_int32] * 5,
+    ),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -1795,6 +1795,36 @@ extern "C" int32_t resident_epoch_time_layer_op(void* engine, int32_t which, int
   return 0;
 }
 
+extern "C" int32_t resident_epoch_gemm(const void* A, const void* W, const void* W2, const void* bias, void* out,
+                                       int32_t M, int32_t N, int32_t K, int32_t epilogue, int32_t dtype_bytes) {
+  using namespace re;
+  if (A == nullptr || W == nullptr || out == nullptr || M < 0 || N <= 0 || K <= 0 || epilogue < kGemmStore ||
+      epilogue > kGemmSwiGlu || (dtype_bytes != 2 && dtype_bytes != 4) || (epilogue == kGemmSwiGlu && W2 == nullptr))
+    return -1;
+  // the bf16 kernel reads the bias four elements at a time
+  if (dtype_bytes == 2 && epilogue == kGemmStore && bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 7) != 0)
+    return -1;
+  GemmArgs g{};
+  g.A = A;
+  g.W = W;
+  g.W2 = W2;
+  g.out = out;
+  g.bias = epilogue == kGemmStore ? bias : nullptr;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = K;
+  g.ldw = K;
+  g.ldo = N;
+  const hipError_t e = launch_gemm(g, epilogue, dtype_bytes, nullptr);
+  if (e == hipErrorInvalidValue) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  if (e != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess) return -2;
+  return 0;
+}
+
 extern "C" int32_t resident_epoch_kernel_timing(void* engine, int32_t enable) {
   Engine* e = static_cast<Engine*>(engine);
   if (e == nullptr) return -1;

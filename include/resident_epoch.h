@@ -232,6 +232,22 @@ int32_t resident_epoch_time_ops(void *engine, int32_t begin, int32_t end, int32_
  * path), -2 HIP failure. */
 int32_t resident_epoch_time_layer_op(void *engine, int32_t which, int32_t passes, float *avg_ms);
 
+/* The batched-prefill GEMM on caller buffers, for checking it against a plain
+ * matrix product (no reference counterpart: the reference's prompts are
+ * prefilled by stock vLLM).  out[M,N] from A[M,K] and W[N,K], both operands
+ * K-contiguous, leading dimensions K, K and N:
+ *   epilogue 0: out = T(A W^T + bias)           (bias [N], or null)
+ *   epilogue 1: out = T(out + T(A W^T))         (the residual add)
+ *   epilogue 2: out = T(T(silu(T(A W^T))) T(A W2^T))  (W gate rows, W2 up rows)
+ * T is the rounding to the element type.  dtype_bytes 2: bf16 on the matrix
+ * cores (K % 64 == 0, N % 8 == 0, 16-byte aligned buffers, an 8-byte
+ * aligned bias); 4: fp32
+ * (epilogues 0 and 1).  Device pointers; runs on the null stream and waits
+ * for it.  Return 0, -1 bad arguments or a shape the kernel refuses, -2 HIP
+ * failure. */
+int32_t resident_epoch_gemm(const void *A, const void *W, const void *W2, const void *bias, void *out,
+                            int32_t M, int32_t N, int32_t K, int32_t epilogue, int32_t dtype_bytes);
+
 #ifdef __cplusplus
 }
 #endif
