@@ -528,14 +528,38 @@ constexpr int kAvld = kAk + 8;  // transposed V tile row stride
 // the prompt length.
 constexpr int kFlashLds = kAk * kAkld * 2 + kAd * kAvld * 2;
 
-__global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a) {
+// Workgroup order: the (KV head, query tile) pairs P = g * ntiles + t are cut
+// into chunks of kFlashChunk consecutive tiles (a 1000-token prompt's tiles
+// are one chunk); chunk c runs on XCD c % 8 (workgroup b runs on XCD b % 8),
+// an XCD takes its chunks in order, a chunk's tiles in order, and the G
+// query heads that share the KV head back to back.  The keys and values of a
+// row and KV head are then read from one XCD's L2 by all of its tiles and
+// heads, instead of from the memory-side cache once per head.
+constexpr int kFlashChunk = 16;
+
+int flash_grid(int ntiles, int heads, int kv_heads) {
+  const int chunks = (ntiles * kv_heads + kFlashChunk - 1) / kFlashChunk;
+  return (chunks + 7) / 8 * 8 * kFlashChunk * (heads / kv_heads);
+}
+
+__global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a, int ntiles) {
   __shared__ __align__(16) unsigned char smem[kFlashLds];
   __shared__ float stat[2][2][32][2];  // [query half][key half][query][max, sum]
   bf16_t* Ks = reinterpret_cast<bf16_t*>(smem);  // [64 keys][136]
   bf16_t* Vt = Ks + kAk * kAkld;                  // [128 d][72 keys]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int4 tile = a.tiles[blockIdx.x];  // first query token, first token of the row, queries, first query's position
-  const int h = blockIdx.y;
+  int tix, h;
+  {
+    const int G = a.heads / a.kv_heads;
+    const int x = blockIdx.x & 7, s = blockIdx.x >> 3;
+    const int k = s / (kFlashChunk * G), rem = s - k * (kFlashChunk * G);
+    const int P = (k * 8 + x) * kFlashChunk + rem / G;
+    if (P >= ntiles * a.kv_heads) return;  // padding of the last chunks (uniform)
+    const int g = P / ntiles;
+    tix = P - g * ntiles;
+    h = g * G + rem % G;
+  }
+  const int4 tile = a.tiles[tix];  // first query token, first token of the row, queries, first query's position
   const int m_start = tile.x, r0 = tile.y, nqt = tile.z, p0 = tile.w;
   const int nq = a.heads, kvh = h / (a.heads / a.kv_heads);
   const bf16_t* qkv = static_cast<const bf16_t*>(a.qkv);
@@ -852,7 +876,8 @@ hipError_t launch_prefill_attention(const PrefillAttn& a, const Dims& d, int nti
   if (a.M <= 0) return hipSuccess;
   if (prefill_attention_mfma(d)) {
     if (ntiles <= 0) return hipErrorInvalidValue;
-    k_pf_attn_flash<<<dim3(ntiles, d.heads), 256, 0, stream>>>(a);
+    if (d.heads % d.kv_heads != 0) return hipErrorInvalidValue;
+    k_pf_attn_flash<<<flash_grid(ntiles, d.heads, d.kv_heads), 256, 0, stream>>>(a, ntiles);
   } else {
     if (256 % d.head_dim != 0 || d.head_dim % 8 != 0) return hipErrorInvalidValue;
     const size_t bytes = (size_t)d.capacity * sizeof(float);
