@@ -112,30 +112,53 @@ __global__ void __launch_bounds__(256) k_pf_swiglu(const void* gate, const void*
 // RoPE of q and k (rows already rounded with their bias) in place, and the
 // paged slot write of k and v (batched_decoder_step.py:231-264, 323-324).
 template <typename T>
+__device__ __forceinline__ void store8(T* p, const Vec8<T>& v);
+template <>
+__device__ __forceinline__ void store8<bf16_t>(bf16_t* p, const Vec8<bf16_t>& v) {
+  *reinterpret_cast<re_u32x4*>(p) = v.v;
+}
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const Vec8<float>& v) {
+  reinterpret_cast<re_f32x4*>(p)[0] = v.a;
+  reinterpret_cast<re_f32x4*>(p)[1] = v.b;
+}
+
+// One workgroup per token; a thread takes 8 consecutive pair indices j of one
+// head (16-byte accesses of both halves, the RoPE table's 8 cos/sin pairs),
+// head_dim a multiple of 16.
+template <typename T>
 __global__ void __launch_bounds__(256) k_pf_qkv_post(PrefillQkv a) {
   const int m = blockIdx.x;
-  const int half = a.head_dim / 2;
+  const int half = a.head_dim / 2, hv = half / 8;
   const int nq = a.heads, nkv = a.kv_heads;
   T* row = static_cast<T*>(a.qkv) + (size_t)m * a.ld;
   const int s = a.slot[m];
-  for (int idx = threadIdx.x; idx < (nq + 2 * nkv) * half; idx += blockDim.x) {
-    const int hg = idx / half, j = idx - hg * half;
+  const bool to_cache = s >= 0 && s < a.slots;
+  const float* rope = a.rope + (size_t)m * half * 2;
+  for (int idx = threadIdx.x; idx < (nq + 2 * nkv) * hv; idx += blockDim.x) {
+    const int hg = idx / hv, j = (idx - hg * hv) * 8;
     T* p = row + (size_t)hg * a.head_dim;
-    float oa = Elt<T>::f(p[j]), ob = Elt<T>::f(p[j + half]);
+    Vec8<T> va = Vec8<T>::load_cached(p + j), vb = Vec8<T>::load_cached(p + j + half);
     if (hg < nq + nkv) {
-      const float c = a.rope[((size_t)m * half + j) * 2], sn = a.rope[((size_t)m * half + j) * 2 + 1];
-      const float qa = oa, qb = ob;
-      oa = Elt<T>::r(Elt<T>::r(qa * c) + Elt<T>::r(-qb * sn));
-      ob = Elt<T>::r(Elt<T>::r(qb * c) + Elt<T>::r(qa * sn));
-      p[j] = Elt<T>::t(oa);
-      p[j + half] = Elt<T>::t(ob);
+      float oa[8], ob[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float c = rope[(j + e) * 2], sn = rope[(j + e) * 2 + 1];
+        const float qa = va.get(e), qb = vb.get(e);
+        oa[e] = Elt<T>::r(Elt<T>::r(qa * c) + Elt<T>::r(-qb * sn));
+        ob[e] = Elt<T>::r(Elt<T>::r(qb * c) + Elt<T>::r(qa * sn));
+      }
+      va = Vec8<T>::from_floats(oa);
+      vb = Vec8<T>::from_floats(ob);
+      store8<T>(p + j, va);
+      store8<T>(p + j + half, vb);
     }
-    if (hg >= nq && s >= 0 && s < a.slots) {
+    if (hg >= nq && to_cache) {
       const bool is_key = hg < nq + nkv;
       const int kvh = is_key ? hg - nq : hg - nq - nkv;
       T* cache = static_cast<T*>(is_key ? a.key_cache : a.value_cache) + ((size_t)s * nkv + kvh) * a.head_dim;
-      cache[j] = Elt<T>::t(oa);
-      cache[j + half] = Elt<T>::t(ob);
+      store8<T>(cache + j, va);
+      store8<T>(cache + j + half, vb);
     }
   }
 }
@@ -807,6 +830,7 @@ hipError_t launch_prefill_swiglu(const void* gate, const void* up, void* out, lo
 
 hipError_t launch_prefill_qkv_post(const PrefillQkv& a, int dtype_bytes, hipStream_t stream) {
   if (a.M <= 0) return hipSuccess;
+  if (a.head_dim % 16 != 0 || a.ld % 8 != 0) return hipErrorInvalidValue;
   if (dtype_bytes == 2)
     k_pf_qkv_post<bf16_t><<<a.M, 256, 0, stream>>>(a);
   else
