@@ -125,13 +125,17 @@ __device__ __forceinline__ void cu_stream(const MfArgs& a, unsigned char* lds, c
   static_assert(RING * NS + 8 <= 63, "vmcnt holds at most 63");
   static_assert(kLcBlock % RING == 0, "ring slots are compile-time within a block");
   const int ksteps = a.K / kMfK, nblocks = ksteps / kLcBlock;
-  // activation block b, tile t, steps 8 (w & 1) ..+8 go to LDS by wave w's 8 loads
-  auto issue_x = [&](int b) {
+  // activation block b, tile t, steps 8 (w & 1) ..+8 go to LDS by wave w's 8
+  // loads (load i: step s0 + i)
+  auto issue_x1 = [&](int b, int i) {
     const int t = wave >> 1, s0 = (wave & 1) * 8;
-    const bf16_t* src = a.x + ((size_t)t * ksteps + b * kLcBlock + s0) * 512 + lane * 8;
-    unsigned char* dst = lds + (b & 1) * kLcBlockBytes + (t * kLcBlock + s0) * 1024;
+    const bf16_t* src = a.x + ((size_t)t * ksteps + b * kLcBlock + s0 + i) * 512 + lane * 8;
+    unsigned char* dst = lds + (b & 1) * kLcBlockBytes + (t * kLcBlock + s0 + i) * 1024;
+    __builtin_amdgcn_global_load_lds((lc_gptr)src, (lc_lptr)dst, 16, 0, 0);
+  };
+  auto issue_x = [&](int b) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) __builtin_amdgcn_global_load_lds((lc_gptr)(src + i * 512), (lc_lptr)(dst + i * 1024), 16, 0, 0);
+    for (int i = 0; i < 8; ++i) issue_x1(b, i);
   };
   if constexpr (NS > 0) {
 #pragma unroll
@@ -147,13 +151,26 @@ __device__ __forceinline__ void cu_stream(const MfArgs& a, unsigned char* lds, c
 #pragma unroll
       for (int j = 0; j < NS; ++j) wr[s][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + s * 512));
   }
-  issue_x(1);
-  // block 0 in LDS (the ring and block 1 may still be in flight)
+  // Block b + 1 goes to LDS during block b (its buffer was freed by the
+  // barrier that ended block b - 1).  SPREAD (a ring no deeper than the
+  // block's last 8 steps): one load per step over the block's first 8
+  // steps, so no wave stalls on a burst of eight requests, and at least RING
+  // steps of refills follow the last one, so the block-end wait (all but the
+  // last RING * NS loads) covers it; a wave without strips issues them at
+  // the block's start.  Otherwise (a deeper ring, whose block-end wait
+  // leaves loads of the whole block in flight): block b + 2 in one burst
+  // after the barrier that ends block b.
+  constexpr bool SPREAD = RING <= kLcBlock - 8;
+  if constexpr (!SPREAD) issue_x(1);
+  // block 0 in LDS (the ring, and block 1 without SPREAD, may still be in flight)
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(lc_wait(RING * NS + 8));
+  __builtin_amdgcn_s_waitcnt(lc_wait(RING * NS + (SPREAD ? 0 : 8)));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   for (int b = 0; b < nblocks; ++b) {
+    if constexpr (SPREAD && NS == 0) {
+      if (b + 1 < nblocks) issue_x(b + 1);
+    }
     if constexpr (NS > 0) {
       const unsigned char* xb = lds + (b & 1) * kLcBlockBytes + lane * 16;
 #pragma unroll
@@ -172,16 +189,17 @@ __device__ __forceinline__ void cu_stream(const MfArgs& a, unsigned char* lds, c
         const int nxt = min(S + RING, ksteps - 1);
 #pragma unroll
         for (int j = 0; j < NS; ++j) wr[rw][j] = __builtin_nontemporal_load(reinterpret_cast<const re_u32x4*>(wp[j] + nxt * 512));
+        if (SPREAD && s < 8 && b + 1 < nblocks) issue_x1(b + 1, s);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // Every wave is done with buffer b & 1, and block b + 1 (requested before
-    // this block's refills) has landed: only the ring may still be in flight.
+    // Every wave is done with buffer b & 1, and block b + 1 has landed: only
+    // the ring may still be in flight.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(lc_wait(RING * NS));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (b + 2 < nblocks) issue_x(b + 2);
+    if (!SPREAD && b + 2 < nblocks) issue_x(b + 2);
   }
   __builtin_amdgcn_s_waitcnt(lc_wait(0));
 }
@@ -278,7 +296,7 @@ __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_lm_cu(MfArgs a) {
 // strip s_begin + w of the gate and of the up matrix over the whole K,
 // sharing the LDS-staged activations with the other waves, then the SiLU *
 // up epilogue.
-constexpr int kGcRing = 16;  // weight steps in flight per wave (few waves stream)
+constexpr int kGcRing = 8;  // weight steps in flight per wave (few waves stream)
 
 __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_gu_cu(MfArgs a) {
   extern __shared__ __align__(16) unsigned char lc_smem[];
