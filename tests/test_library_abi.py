@@ -12,6 +12,7 @@ No test here calls into the GPU.
 """
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -163,3 +164,20 @@ def test_engine_config_json_keys():
     assert set(cfg) == {"model", "engine", "weights"}
     assert cfg["model"]["hidden"] == 3584 and cfg["engine"]["batch"] == 4
     assert cfg["engine"]["configured_eos"] == 151645
+
+
+def test_gemm_entry_point_rejects_bad_arguments_before_any_device_work(lib):
+    # every refusal below happens before the library touches a device
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
+    null = None
+    f = lib.resident_epoch_gemm
+    assert f(null, p, null, null, p, 8, 8, 64, 0, 2) == -1  # no A
+    assert f(p, null, null, null, p, 8, 8, 64, 0, 2) == -1  # no W
+    assert f(p, p, null, null, null, 8, 8, 64, 0, 2) == -1  # no out
+    assert f(p, p, null, null, p, -1, 8, 64, 0, 2) == -1  # M < 0
+    assert f(p, p, null, null, p, 8, 0, 64, 0, 2) == -1  # N = 0
+    assert f(p, p, null, null, p, 8, 8, 0, 0, 2) == -1  # K = 0
+    assert f(p, p, null, null, p, 8, 8, 64, 3, 2) == -1  # no such epilogue
+    assert f(p, p, null, null, p, 8, 8, 64, 0, 3) == -1  # element size
+    assert f(p, p, null, null, p, 8, 8, 64, 2, 2) == -1  # SwiGLU without the up rows
+    assert f(p, p, null, ctypes.c_void_p(20), p, 8, 8, 64, 0, 2) == -1  # bias not 8-byte aligned
