@@ -30,6 +30,8 @@ namespace re {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short lds_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) lds_v4i16* lds_v4i16_ptr;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -528,8 +530,8 @@ __global__ void __launch_bounds__(256) k_pf_attn_rows(PrefillAttn a) {
 // Tile shapes of the MFMA attention below (keys per tile, head dim; the
 // query tiles of up to 64 come from the launch's tile list).
 constexpr int kAk = 64, kAd = 128;
-constexpr int kAkld = kAd + 8;  // K tile row stride (elements)
-constexpr int kAvld = kAk + 8;  // transposed V tile row stride
+constexpr int kAkld = kAd + 8;   // K tile row stride (elements)
+constexpr int kAvld = kAd + 16;  // V tile row stride: 4 key rows of a transposing read cover 4 x 32 bytes of distinct banks
 
 // bf16, head_dim 128: one workgroup per (tile of up to 64 queries of one row,
 // head), two passes over the key tiles of 64, no score tile in LDS.
@@ -545,11 +547,11 @@ constexpr int kAvld = kAk + 8;  // transposed V tile row stride
 //     registers: for each 16-key block the MFMA's k index runs over the keys
 //     in the order the accumulator layout holds them (j 0-7 from lanes 0-31:
 //     keys +0..3 and +8..11; j 8-15 from lanes 32-63: keys +4..7 and
-//     +12..15), and the value rows are read from the transposed V tile in
-//     the same order.  The two key halves' partial O are added at the end.
-// LDS: one K tile and one transposed V tile (about 36 KB), independent of
-// the prompt length.
-constexpr int kFlashLds = kAk * kAkld * 2 + kAd * kAvld * 2;
+//     +12..15), and the value operand is read in the same order from the
+//     row-major V tile by transposing LDS reads.  The two key halves'
+//     partial O are added at the end.
+// LDS: one K tile and one V tile (35 KB), independent of the prompt length.
+constexpr int kFlashLds = kAk * kAkld * 2 + kAk * kAvld * 2;
 
 // Workgroup order: the (KV head, query tile) pairs P = g * ntiles + t are cut
 // into chunks of kFlashChunk consecutive tiles (a 1000-token prompt's tiles
@@ -569,7 +571,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a, int nti
   __shared__ __align__(16) unsigned char smem[kFlashLds];
   __shared__ float stat[2][2][32][2];  // [query half][key half][query][max, sum]
   bf16_t* Ks = reinterpret_cast<bf16_t*>(smem);  // [64 keys][136]
-  bf16_t* Vt = Ks + kAk * kAkld;                  // [128 d][72 keys]
+  bf16_t* Vs = Ks + kAk * kAkld;                  // [64 keys][144]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int tix, h;
   {
@@ -604,9 +606,8 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a, int nti
     for (int ks = 0; ks < kAd / 16; ++ks) qf[ks] = lds_frag(qrow + ks * 16);
   }
   // Key tile in registers: vector v = tid + 256 i is key v / 16, elements
-  // (v % 16) * 8 ..+8.  Value tile: key v % 64, elements (v / 64) * 8 ..+8
-  // (the transposed LDS writes of one instruction cover 64 consecutive keys
-  // of one row).  Keys past the row read the last one.
+  // (v % 16) * 8 ..+8.  Value tile: key v % 64, elements (v / 64) * 8 ..+8.
+  // Both go to LDS row-major.  Keys past the row read the last one.
   re_u32x4 kpre[4], vpre[4];
   auto load_k = [&](int kt) {
 #pragma unroll
@@ -635,12 +636,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a, int nti
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i, key = v & 63, c = (v >> 6) * 8;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w = vpre[i][e];
-        Vt[(c + 2 * e) * kAvld + key] = static_cast<bf16_t>(w & 0xffffu);
-        Vt[(c + 2 * e + 1) * kAvld + key] = static_cast<bf16_t>(w >> 16);
-      }
+      *reinterpret_cast<re_u32x4*>(&Vs[key * kAvld + c]) = vpre[i];
     }
   };
   // Scores of key tile kt for this lane's query: s[v] is key
@@ -750,12 +746,18 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn_flash(PrefillAttn a, int nti
       for (int e = 0; e < 4; ++e) pw[e] = f2_to_bf16x2(pv[2 * e], pv[2 * e + 1]);
       const bf16x8_t af = __builtin_bit_cast(bf16x8_t, pw);
       const int kb = sn * 32 + 16 * b + 4 * hi;
+      // Value operand by transposing LDS reads (ds_read_b64_tr_b16): in each
+      // 16-lane group, lane q + 4 r names the 8 bytes of dims 4 q .. 4 q + 3
+      // of key row kb + r, and lane i receives dim i's values of the 4 keys
+      // in key order -- the 4 keys lane i's MFMA column needs.
+      const int gi = lane & 15, q4 = (gi & 3) * 4, rr = gi >> 2, d16 = ((lane >> 4) & 1) * 16;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const bf16_t* vr = &Vt[(t * 32 + (lane & 31)) * kAvld + kb];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 up = *reinterpret_cast<const uint2*>(vr + 8);
-        const re_u32x4 bw = {lo.x, lo.y, up.x, up.y};
+        const bf16_t* vr = &Vs[(kb + rr) * kAvld + t * 32 + d16 + q4];
+        const lds_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)vr);
+        const lds_v4i16 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(vr + 8 * kAvld));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), u2 = __builtin_bit_cast(uint2, up);
+        const re_u32x4 bw = {l2.x, l2.y, u2.x, u2.y};
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8_t, bw), o[t], 0, 0, 0);
       }
     }
