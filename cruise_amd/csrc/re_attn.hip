@@ -420,11 +420,12 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
 //             are interleaved (one wait per exchange step); then
 //             p = bf16(exp(s - max) / sum) into a bf16 array, zero past the
 //             context;
-//   P.V       per tile the value rows are transposed into LDS (a lane holds
-//             one 16-byte chunk of 8 consecutive rows and writes 8 16-byte
-//             runs of Vᵀ), then wave w accumulates output columns 16 w ..+16
-//             of all heads: A = p (head l % 16, 8 positions, one 16-byte LDS
-//             read), B = Vᵀ (column l % 16, the same 8 positions), 8 k steps.
+//   P.V       per tile the value rows go to LDS as they are (a lane stores
+//             its 16-byte chunks of 8 consecutive rows), then wave w
+//             accumulates output columns 16 w ..+16 of all heads: A = p (head
+//             l % 16, 8 positions, one 16-byte LDS read), B = V (column
+//             l % 16, the same 8 positions, two transposing LDS reads), 8 k
+//             steps.
 // Same rounding points as k_attn_group; only fp32 summation orders differ.
 // Rows whose slot is outside the cache are zero keys (score 0) and zero
 // values.  Every key and value request is unconditional (a row past the
@@ -435,15 +436,47 @@ typedef __bf16 mg_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float mg_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMgThreads = 512, kMgWaves = 8, kMgTile = 256, kMgD = 128, kMgMaxG = 8;
 constexpr int kMgChunk = 4;           // tiles whose keys are requested together
-constexpr int kMgVtLd = kMgTile + 8;  // Vᵀ row stride (bf16): 16-byte reads of 16 rows hit distinct banks
+
+// A 256-position value tile in LDS: row-major, 256 bytes a row, the row's
+// 32-byte chunks XOR-swizzled (chunk c of row R at c ^ mg_vswz(R)) so that
+// each half wave of mg_read_v's transposing reads covers the 64 banks once.
+constexpr size_t kMgVTileBytes = (size_t)kMgTile * kMgD * sizeof(bf16_t);
+__device__ __forceinline__ int mg_vswz(int R) { return (R & 3) | (((R >> 3) & 1) << 2); }
+
+// Rows p0 .. p0+7 of the tile, elements 8 l16 ..+8 of each; rows whose mask
+// bit is clear (past the context, or a slot outside the cache) as zeros.
+__device__ __forceinline__ void mg_store_v(bf16_t* vt, const Vec8<bf16_t> (&v)[8], int mask, int p0, int l16) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int R = p0 + i;
+    const re_u32x4 x = (mask >> i) & 1 ? v[i].v : re_u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<re_u32x4*>(vt + R * kMgD + ((l16 >> 1) ^ mg_vswz(R)) * 16 + (l16 & 1) * 8) = x;
+  }
+}
+
+// The B operand of P.V step k for wave w: dim 16 w + l % 16 of positions
+// 32 k + 8 (l / 16) ..+8, by two transposing LDS reads (ds_read_b64_tr_b16):
+// in each 16-lane group lane q + 4 r names the 8 bytes of dims 4 q ..+4 of
+// row kb + r, and lane i receives dim i's values of the 4 rows in row order.
+typedef short mg_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) mg_v4i16* mg_v4i16_lds;
+__device__ __forceinline__ mg_bf16x8 mg_read_v(const bf16_t* vt, int k, int wave, int lane) {
+  const int gi = lane & 15, r = gi >> 2;
+  const int R = k * 32 + (lane >> 4) * 8 + r;  // rows R and R + 4 share mg_vswz
+  const bf16_t* p = vt + R * kMgD + (wave ^ mg_vswz(R)) * 16 + (gi & 3) * 4;
+  const mg_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mg_v4i16_lds)p);
+  const mg_v4i16 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mg_v4i16_lds)(p + 4 * kMgD));
+  const uint2 l2 = __builtin_bit_cast(uint2, lo), u2 = __builtin_bit_cast(uint2, up);
+  return __builtin_bit_cast(mg_bf16x8, re_u32x4{l2.x, l2.y, u2.x, u2.y});
+}
 
 // The window's tiles rounded up to whole chunks.
 __host__ __device__ int mgroup_tiles(int window) {
   const int t = (window + kMgTile - 1) / kMgTile;
   return (t + kMgChunk - 1) / kMgChunk * kMgChunk;
 }
-// LDS: scores [window][8] fp32, probabilities [8][tiles * 256] bf16, Vᵀ
-// [128][kMgVtLd] bf16, row offsets [tiles * 256] int, the block table.
+// LDS: scores [window][8] fp32, probabilities [8][tiles * 256] bf16, a
+// value tile [256][128] bf16, row offsets [tiles * 256] int, the block table.
 struct MgLayout {
   size_t pb, vt, roff, tabs, total;
 };
@@ -453,7 +486,7 @@ __host__ __device__ MgLayout mgroup_layout(int G, int window, int blocks_per_row
   (void)G;
   l.pb = (size_t)window * kMgMaxG * sizeof(float);
   l.vt = l.pb + (size_t)kMgMaxG * span * sizeof(bf16_t);
-  l.roff = l.vt + (size_t)kMgD * kMgVtLd * sizeof(bf16_t);
+  l.roff = l.vt + kMgVTileBytes;
   l.tabs = l.roff + span * sizeof(int);
   l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
   return l;
@@ -499,7 +532,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   const int span = mgroup_tiles(W) * kMgTile;
   float* sc = reinterpret_cast<float*>(mg_smem);            // [W][kMgMaxG]
   bf16_t* pb = reinterpret_cast<bf16_t*>(mg_smem + L.pb);   // [kMgMaxG][span]
-  bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + L.vt);   // [D][kMgVtLd]
+  bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + L.vt);   // value tile [256][D], swizzled
   int* roff = reinterpret_cast<int*>(mg_smem + L.roff);     // [span]
   int* tabs = reinterpret_cast<int*>(mg_smem + L.tabs);
   const bf16_t* KC = static_cast<const bf16_t*>(a.key_cache);
@@ -688,18 +721,8 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   // P.V: wave w owns output columns 16 w ..+16 of every head.
   mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
   auto pv_tile = [&](const Vec8<bf16_t>(&v)[8], int mask, int t) {
-    lds_barrier();  // the probabilities are written and the previous tile's Vᵀ reads are done
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      re_u32x4 col;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = (mask >> (2 * i)) & 1 ? (v[2 * i].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
-        const uint32_t hi = (mask >> (2 * i + 1)) & 1 ? (v[2 * i + 1].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
-        col[i] = lo | (hi << 16);
-      }
-      *reinterpret_cast<re_u32x4*>(vt + (size_t)(l16 * 8 + e) * kMgVtLd + p0) = col;
-    }
+    lds_barrier();  // the probabilities are written and the previous tile's value reads are done
+    mg_store_v(vt, v, mask, p0, l16);
     lds_barrier();
 #pragma unroll
     for (int k = 0; k < kMgTile / 32; ++k) {
@@ -707,8 +730,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
       re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
                                                         k * 32 + lq * 8);
       if (l16 >= G) pa = re_u32x4{0u, 0u, 0u, 0u};
-      const re_u32x4 vb4 = *reinterpret_cast<const re_u32x4*>(vt + (size_t)(wave * 16 + l16) * kMgVtLd + k * 32 + lq * 8);
-      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, vb4),
+      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), mg_read_v(vt, k, wave, lane),
                                                      oacc, 0, 0, 0);
     }
   };
@@ -751,15 +773,16 @@ struct MsLayout {
   size_t roff, sc, pb, vt, stat, tabs, total;
 };
 // LDS of the two kernels: row offsets [256] int, then the scores kernel's
-// scores [256][8] fp32, or the P.V kernel's probabilities [8][256] bf16, Vᵀ
-// [128][kMgVtLd] bf16 and head statistics [2][8] fp32; the block table last.
+// scores [256][8] fp32, or the P.V kernel's probabilities [8][256] bf16, a
+// value tile [256][128] bf16 and head statistics [2][8] fp32; the block
+// table last.
 __host__ __device__ MsLayout msplit_layout(int blocks_per_row, bool pv) {
   MsLayout l;
   l.roff = 0;
   l.sc = l.roff + kMsRows * sizeof(int);
   l.pb = l.sc;
   l.vt = l.pb + (size_t)kMgMaxG * kMsRows * sizeof(bf16_t);
-  l.stat = l.vt + (size_t)kMgD * kMgVtLd * sizeof(bf16_t);
+  l.stat = l.vt + kMgVTileBytes;
   l.tabs = pv ? l.stat + 2 * kMgMaxG * sizeof(float) : l.sc + (size_t)kMsRows * kMgMaxG * sizeof(float);
   l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
   return l;
@@ -915,7 +938,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
   const MsLayout L = msplit_layout(a.blocks_per_row, true);
   int* roff = reinterpret_cast<int*>(ms_smem + L.roff);
   bf16_t* pb = reinterpret_cast<bf16_t*>(ms_smem + L.pb);  // [kMgMaxG][256]
-  bf16_t* vt = reinterpret_cast<bf16_t*>(ms_smem + L.vt);  // [D][kMgVtLd]
+  bf16_t* vt = reinterpret_cast<bf16_t*>(ms_smem + L.vt);  // value tile [256][D], swizzled
   float* stat = reinterpret_cast<float*>(ms_smem + L.stat);  // [max, 1 / sum][kMgMaxG]
   int* tabs = reinterpret_cast<int*>(ms_smem + L.tabs);
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
@@ -964,18 +987,8 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
     if (h < G && j < neff) p = round_bf16(expf(a.sp_scores[(row0 + h) * W + j] - stat[h]) * stat[kMgMaxG + h]);
     pb[(size_t)h * kMsRows + jl] = f_to_bf16(p);  // exact: p is bf16
   }
-  // Vᵀ of the tile, then P.V: wave w owns output columns 16 w ..+16 of every head.
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    re_u32x4 col;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = (mask >> (2 * i)) & 1 ? (vr[2 * i].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
-      const uint32_t hi = (mask >> (2 * i + 1)) & 1 ? (vr[2 * i + 1].v[e >> 1] >> ((e & 1) * 16)) & 0xffffu : 0u;
-      col[i] = lo | (hi << 16);
-    }
-    *reinterpret_cast<re_u32x4*>(vt + (size_t)(l16 * 8 + e) * kMgVtLd + p0) = col;
-  }
+  // The value tile, then P.V: wave w owns output columns 16 w ..+16 of every head.
+  mg_store_v(vt, vr, mask, p0, l16);
   lds_barrier();
   mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -983,9 +996,8 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
     // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past G)
     re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * kMsRows + k * 32 + lq * 8);
     if (l16 >= G) pa = re_u32x4{0u, 0u, 0u, 0u};
-    const re_u32x4 vb4 = *reinterpret_cast<const re_u32x4*>(vt + (size_t)(wave * 16 + l16) * kMgVtLd + k * 32 + lq * 8);
-    oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, vb4),
-                                                   oacc, 0, 0, 0);
+    oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), mg_read_v(vt, k, wave, lane), oacc,
+                                                   0, 0, 0);
   }
   // value v of lane l: head 4 (l / 16) + v, column 16 w + l % 16
 #pragma unroll
