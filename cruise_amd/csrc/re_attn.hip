@@ -271,7 +271,6 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
   // register sets: the next tile's rows are in flight while a tile is
   // computed (a tile past the context loads one valid line per lane and is
   // dropped).
-  const float scale_div = sqrtf(static_cast<float>(kGrpD));
   auto score_tile = [&](const Vec8<bf16_t>(&kr)[kGrpRows], const int (&off)[kGrpRows], int t) {
 #pragma unroll
     for (int i = 0; i < kGrpRows; ++i) {
@@ -282,8 +281,8 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
       for (int h = 0; h < kGrpMaxG; ++h) part[h] = xor_add<8>(part[h], lane);
       group_reduce_transpose<kGrpMaxG>(part, c & 7);
       const int j = t * kGrpTile + i * kGrpSlots + r;
-      float s = round_bf16(part[0]);  // ExactQk output is bf16
-      s = round_bf16(s / scale_div);
+      // ExactQk output is bf16, then the bf16 quotient by sqrt(128)
+      float s = round_bf16(div_sqrt128_bf16(round_bf16(part[0])));
       if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
       if (c < G && j < neff) sc[(size_t)c * W + j] = s;
     }
@@ -446,11 +445,17 @@ __device__ __forceinline__ int mg_vswz(int R) { return (R & 3) | (((R >> 3) & 1)
 // Rows p0 .. p0+7 of the tile, elements 8 l16 ..+8 of each; rows whose mask
 // bit is clear (past the context, or a slot outside the cache) as zeros.
 __device__ __forceinline__ void mg_store_v(bf16_t* vt, const Vec8<bf16_t> (&v)[8], int mask, int p0, int l16) {
+  bf16_t* base = vt + p0 * kMgD + (l16 & 1) * 8;
+  if (__builtin_amdgcn_ballot_w64(mask != 0xff) == 0) {  // every row of the wave present
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int R = p0 + i;
-    const re_u32x4 x = (mask >> i) & 1 ? v[i].v : re_u32x4{0u, 0u, 0u, 0u};
-    *reinterpret_cast<re_u32x4*>(vt + R * kMgD + ((l16 >> 1) ^ mg_vswz(R)) * 16 + (l16 & 1) * 8) = x;
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<re_u32x4*>(base + i * kMgD + ((l16 >> 1) ^ mg_vswz(p0 + i)) * 16) = v[i].v;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const re_u32x4 x = (mask >> i) & 1 ? v[i].v : re_u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<re_u32x4*>(base + i * kMgD + ((l16 >> 1) ^ mg_vswz(p0 + i)) * 16) = x;
+    }
   }
 }
 
@@ -574,17 +579,19 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   }
   lds_barrier();
 
-  const float scale_div = sqrtf(static_cast<float>(kMgD));
-  auto load_k = [&](re_u32x4(&kf)[2][4], int t) {
+  // Keys of tile t: kvalid[q] bit r marks row r of position group 2 w + q
+  // present (lanes r and r + 16 k hold the same row).
+  auto load_k = [&](re_u32x4(&kf)[2][4], uint32_t(&kvalid)[2], int t) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int off = roff[t * kMgTile + (2 * wave + q) * 16 + l16];
+      kvalid[q] = static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(off >= 0)) & 0xffffu;
       const bf16_t* row = KC + (off >= 0 ? off : 0);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) kf[q][kk] = *reinterpret_cast<const re_u32x4*>(row + kk * 32 + lq * 8);
     }
   };
-  auto score_k = [&](const re_u32x4(&kf)[2][4], int t) {
+  auto score_k = [&](const re_u32x4(&kf)[2][4], const uint32_t(&kvalid)[2], int t) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       mg_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -592,14 +599,15 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
       for (int kk = 0; kk < 4; ++kk)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, kf[q][kk]), qf[kk], acc, 0, 0, 0);
       // value v of lane l: position 4 (l / 16) + v of the group, head l % 16
+      const uint32_t present = kvalid[q] >> (lq * 4);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int j = t * kMgTile + (2 * wave + q) * 16 + lq * 4 + v;
-        float s = round_bf16(acc[v]);  // ExactQk output is bf16
-        s = round_bf16(s / scale_div);
+        // ExactQk output is bf16, then the bf16 quotient by sqrt(128)
+        float s = round_bf16(div_sqrt128_bf16(round_bf16(acc[v])));
         if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
         // a missing row (slot outside the cache) is a zero key: score 0
-        if (l16 < G && j < neff) sc[(size_t)j * kMgMaxG + l16] = roff[j] >= 0 || uniform ? s : 0.f;
+        if (l16 < G && j < neff) sc[(size_t)j * kMgMaxG + l16] = (present >> v) & 1 || uniform ? s : 0.f;
       }
     }
   };
@@ -623,21 +631,23 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   int vmask[kMgChunk];
   for (int c = 0; c + 1 < nchunks; ++c) {
     re_u32x4 kf[kMgChunk][2][4];
+    uint32_t kvalid[kMgChunk][2];
 #pragma unroll
-    for (int i = 0; i < kMgChunk; ++i) load_k(kf[i], c * kMgChunk + i);
+    for (int i = 0; i < kMgChunk; ++i) load_k(kf[i], kvalid[i], c * kMgChunk + i);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < kMgChunk; ++i) score_k(kf[i], c * kMgChunk + i);
+    for (int i = 0; i < kMgChunk; ++i) score_k(kf[i], kvalid[i], c * kMgChunk + i);
   }
   {
     const int c = nchunks - 1;
     re_u32x4 kf[kMgChunk][2][4];
+    uint32_t kvalid[kMgChunk][2];
 #pragma unroll
-    for (int i = 0; i < kMgChunk; ++i) load_k(kf[i], c * kMgChunk + i);
+    for (int i = 0; i < kMgChunk; ++i) load_k(kf[i], kvalid[i], c * kMgChunk + i);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < kMgChunk; ++i) {
-      score_k(kf[i], c * kMgChunk + i);
+      score_k(kf[i], kvalid[i], c * kMgChunk + i);
       vmask[i] = load_v(vr[i], i);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -726,10 +736,11 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     lds_barrier();
 #pragma unroll
     for (int k = 0; k < kMgTile / 32; ++k) {
-      // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past G)
-      re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
-                                                        k * 32 + lq * 8);
-      if (l16 >= G) pa = re_u32x4{0u, 0u, 0u, 0u};
+      // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8.  Rows G..7
+      // are zero; rows 8..15 repeat 0..7, and an output row depends on its A
+      // row alone, so those rows land in output rows that are never stored.
+      const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
+                                                              k * 32 + lq * 8);
       oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), mg_read_v(vt, k, wave, lane),
                                                      oacc, 0, 0, 0);
     }
@@ -849,7 +860,6 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_scores(AttnArgs a) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) kf[q][kk] = *reinterpret_cast<const re_u32x4*>(row + kk * 32 + lq * 8);
   }
-  const float scale_div = sqrtf(static_cast<float>(kMgD));
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     mg_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -860,8 +870,8 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_scores(AttnArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int jl = (2 * wave + q) * 16 + lq * 4 + v;
-      float s = round_bf16(acc[v]);  // ExactQk output is bf16
-      s = round_bf16(s / scale_div);
+      // ExactQk output is bf16, then the bf16 quotient by sqrt(128)
+      float s = round_bf16(div_sqrt128_bf16(round_bf16(acc[v])));
       if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
       // a missing row (slot outside the cache) is a zero key: score 0
       if (l16 < kMgMaxG) sc[(size_t)jl * kMgMaxG + l16] = roff[jl] >= 0 || uniform ? s : 0.f;
@@ -993,9 +1003,9 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
   mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int k = 0; k < kMsRows / 32; ++k) {
-    // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (zero past G)
-    re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * kMsRows + k * 32 + lq * 8);
-    if (l16 >= G) pa = re_u32x4{0u, 0u, 0u, 0u};
+    // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (rows G..7
+    // zero, rows 8..15 only reach output rows that are never stored)
+    const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * kMsRows + k * 32 + lq * 8);
     oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), mg_read_v(vt, k, wave, lane), oacc,
                                                    0, 0, 0);
   }
