@@ -419,12 +419,12 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
 //             are interleaved (one wait per exchange step); then
 //             p = bf16(exp(s - max) / sum) into a bf16 array, zero past the
 //             context;
-//   P.V       per tile the value rows go to LDS as they are (a lane stores
-//             its 16-byte chunks of 8 consecutive rows), then wave w
-//             accumulates output columns 16 w ..+16 of all heads: A = p (head
-//             l % 16, 8 positions, one 16-byte LDS read), B = V (column
-//             l % 16, the same 8 positions, two transposing LDS reads), 8 k
-//             steps.
+//   P.V       wave w multiplies the value rows it loaded (its 32 positions
+//             of each tile) from registers: A = p (head l % 16, the lane's 8
+//             positions, one 16-byte LDS read), B = element e of the lane's
+//             8 rows (8 products per tile, output columns permuted to dims
+//             8 (l % 16) + e); the 8 waves' fp32 partials are added in wave
+//             order through LDS at the end.
 // Same rounding points as k_attn_group; only fp32 summation orders differ.
 // Rows whose slot is outside the cache are zero keys (score 0) and zero
 // values.  Every key and value request is unconditional (a row past the
@@ -480,18 +480,19 @@ __host__ __device__ int mgroup_tiles(int window) {
   const int t = (window + kMgTile - 1) / kMgTile;
   return (t + kMgChunk - 1) / kMgChunk * kMgChunk;
 }
-// LDS: scores [window][8] fp32, probabilities [8][tiles * 256] bf16, a
-// value tile [256][128] bf16, row offsets [tiles * 256] int, the block table.
+// LDS: scores [window][8] fp32, probabilities [8][tiles * 256] bf16, the
+// waves' partial outputs [8][8][128] fp32, row offsets [tiles * 256] int,
+// the block table.
 struct MgLayout {
-  size_t pb, vt, roff, tabs, total;
+  size_t pb, part, roff, tabs, total;
 };
 __host__ __device__ MgLayout mgroup_layout(int G, int window, int blocks_per_row) {
   MgLayout l;
   const size_t span = (size_t)mgroup_tiles(window) * kMgTile;
   (void)G;
   l.pb = (size_t)window * kMgMaxG * sizeof(float);
-  l.vt = l.pb + (size_t)kMgMaxG * span * sizeof(bf16_t);
-  l.roff = l.vt + kMgVTileBytes;
+  l.part = l.pb + (size_t)kMgMaxG * span * sizeof(bf16_t);
+  l.roff = l.part + (size_t)kMgWaves * kMgMaxG * kMgD * sizeof(float);
   l.tabs = l.roff + span * sizeof(int);
   l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
   return l;
@@ -537,7 +538,6 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   const int span = mgroup_tiles(W) * kMgTile;
   float* sc = reinterpret_cast<float*>(mg_smem);            // [W][kMgMaxG]
   bf16_t* pb = reinterpret_cast<bf16_t*>(mg_smem + L.pb);   // [kMgMaxG][span]
-  bf16_t* vt = reinterpret_cast<bf16_t*>(mg_smem + L.vt);   // value tile [256][D], swizzled
   int* roff = reinterpret_cast<int*>(mg_smem + L.roff);     // [span]
   int* tabs = reinterpret_cast<int*>(mg_smem + L.tabs);
   const bf16_t* KC = static_cast<const bf16_t*>(a.key_cache);
@@ -728,23 +728,41 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     }
   }
 
-  // P.V: wave w owns output columns 16 w ..+16 of every head.
-  mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
-  auto pv_tile = [&](const Vec8<bf16_t>(&v)[8], int mask, int t) {
-    lds_barrier();  // the probabilities are written and the previous tile's value reads are done
-    mg_store_v(vt, v, mask, p0, l16);
-    lds_barrier();
+  // P.V: wave w multiplies the value rows it loaded (its 32 positions of
+  // each tile) into partial outputs of every head over all 128 columns,
+  // straight from registers.  Lane (l / 16, l % 16) holds elements
+  // 8 (l % 16) + e of rows 8 (l / 16) + i; product e takes element e of its 8
+  // rows as the B operand (k = the lane's 8 positions, column l % 16 = dim
+  // 8 (l % 16) + e), so its 16 output columns are dims e, 8 + e, ..., 120 + e.
+  mg_f32x4 oacc[8];
 #pragma unroll
-    for (int k = 0; k < kMgTile / 32; ++k) {
-      // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8.  Rows G..7
-      // are zero; rows 8..15 repeat 0..7, and an output row depends on its A
-      // row alone, so those rows land in output rows that are never stored.
-      const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
-                                                              k * 32 + lq * 8);
-      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), mg_read_v(vt, k, wave, lane),
-                                                     oacc, 0, 0, 0);
+  for (int e = 0; e < 8; ++e) oacc[e] = mg_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto pv_tile = [&](const Vec8<bf16_t>(&v)[8], int mask, int t) {
+    re_u32x4 w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = v[i].v;
+    if (__builtin_amdgcn_ballot_w64(mask != 0xff) != 0) {  // some row of the wave absent: zeros
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (!((mask >> i) & 1)) w[i] = re_u32x4{0u, 0u, 0u, 0u};
+    }
+    // A: p of head l % 16 at the wave's positions 8 (l / 16) ..+8.  Rows G..7
+    // are zero; rows 8..15 repeat 0..7, and an output row depends on its A
+    // row alone, so those rows land in output rows that are never read.
+    const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
+                                                            wave * 32 + lq * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // word i: element e of rows 2 i (low half) and 2 i + 1 (high half)
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      re_u32x4 bw;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bw[i] = __builtin_amdgcn_perm(w[2 * i + 1][e >> 1], w[2 * i][e >> 1], sel);
+      oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa),
+                                                        __builtin_bit_cast(mg_bf16x8, bw), oacc[e], 0, 0, 0);
     }
   };
+  lds_barrier();  // the probabilities are written
 #pragma unroll
   for (int i = 0; i < kMgChunk; ++i) pv_tile(vr[i], vmask[i], i);
   for (int c = 1; c < nchunks; ++c) {
@@ -754,15 +772,26 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kMgChunk; ++i) pv_tile(vr[i], vmask[i], c * kMgChunk + i);
   }
-  // value v of lane l: head 4 (l / 16) + v, column 16 w + l % 16
+  // value v of lane l in oacc[e]: head 4 (l / 16) + v, dim 8 (l % 16) + e.
+  // Heads 0..7 of each wave go to LDS as fp32 [8][128], then the 8 waves'
+  // partials are added in wave order.
+  float* part = reinterpret_cast<float*>(mg_smem + L.part);  // [8 waves][8 heads][128]
+  if (lq < 2) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int h = lq * 4 + v;
-    if (h < G) {
-      const int k = (g * G + h) * kMgD + wave * 16 + l16;
-      static_cast<bf16_t*>(a.out)[a.packed_out ? xpack_index(b, k, a.heads * kMgD) : (size_t)b * a.heads * kMgD + k] =
-          f_to_bf16(oacc[v]);
+    for (int v = 0; v < 4; ++v) {
+      float* dst = part + ((size_t)wave * kMgMaxG + lq * 4 + v) * kMgD + l16 * 8;
+      *reinterpret_cast<re_f32x4*>(dst) = re_f32x4{oacc[0][v], oacc[1][v], oacc[2][v], oacc[3][v]};
+      *reinterpret_cast<re_f32x4*>(dst + 4) = re_f32x4{oacc[4][v], oacc[5][v], oacc[6][v], oacc[7][v]};
     }
+  }
+  lds_barrier();
+  for (int e = tid; e < G * kMgD; e += kMgThreads) {
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMgWaves; ++w) o += part[(size_t)w * kMgMaxG * kMgD + e];
+    const int k = g * G * kMgD + e;
+    static_cast<bf16_t*>(a.out)[a.packed_out ? xpack_index(b, k, a.heads * kMgD) : (size_t)b * a.heads * kMgD + k] =
+        f_to_bf16(o);
   }
 }
 
