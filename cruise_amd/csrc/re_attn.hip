@@ -529,7 +529,7 @@ __device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
 template <bool P2>
 __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   extern __shared__ __align__(16) unsigned char mg_smem[];
-  __shared__ float red[kMgWaves][kMgMaxG];
+  __shared__ float red[kMgWaves][kMgMaxG], red_sum[kMgWaves][kMgMaxG];
   const int G = a.heads / a.kv_heads, W = a.window;
   const int b = blockIdx.x / a.kv_heads, g = blockIdx.x - b * a.kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
@@ -579,6 +579,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   }
   lds_barrier();
 
+  float smax = -INFINITY;
   // Keys of tile t: kvalid[q] bit r marks row r of position group 2 w + q
   // present (lanes r and r + 16 k hold the same row).
   auto load_k = [&](re_u32x4(&kf)[2][4], uint32_t(&kvalid)[2], int t) {
@@ -607,7 +608,11 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
         float s = round_bf16(div_sqrt128_bf16(round_bf16(acc[v])));
         if (uniform) s = -3.38953139e38f;  // every position masked to bf16 min
         // a missing row (slot outside the cache) is a zero key: score 0
-        if (l16 < G && j < neff) sc[(size_t)j * kMgMaxG + l16] = (present >> v) & 1 || uniform ? s : 0.f;
+        if (l16 < G && j < neff) {
+          const float st = (present >> v) & 1 || uniform ? s : 0.f;
+          sc[(size_t)j * kMgMaxG + l16] = st;
+          smax = fmaxf(smax, st);
+        }
       }
     }
   };
@@ -626,7 +631,8 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   };
 
   // Scores, one chunk of key tiles at a time; the first chunk's values are
-  // requested as the last chunk's key tiles are consumed.
+  // requested as the last chunk's key tiles are consumed.  smax: the lane's
+  // running max of its head's stored scores.
   Vec8<bf16_t> vr[kMgChunk][8];
   int vmask[kMgChunk];
   for (int c = 0; c + 1 < nchunks; ++c) {
@@ -652,11 +658,16 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // each head's max over the wave (lanes l % 16 == h), published with the scores
+  smax = xor_max<16>(smax, lane);
+  smax = xor_max<32>(smax, lane);
+  if (lq == 0 && l16 < kMgMaxG) red[wave][l16] = smax;
   lds_barrier();
 
-  // Softmax per head over LDS: exact max and sum, then each probability
-  // rounded to bf16 (zero from the context's end to the requests' end).
-  // Head slots from G up hold no score: they are masked, not branched on.
+  // Softmax per head over LDS: the exact max (from the score pass) and sum,
+  // then each probability rounded to bf16 (zero from the context's end to
+  // the requests' end).  Head slots from G up hold no score: they are
+  // masked, not branched on.
   auto head_scores = [&](int j, float (&v)[kMgMaxG]) {
     const re_f32x4 lo = *reinterpret_cast<const re_f32x4*>(sc + (size_t)j * kMgMaxG);
     const re_f32x4 hi = *reinterpret_cast<const re_f32x4*>(sc + (size_t)j * kMgMaxG + 4);
@@ -667,29 +678,14 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     }
   };
   float mx[kMgMaxG], inv[kMgMaxG];
-  {
-    float m[kMgMaxG];
-#pragma unroll
-    for (int h = 0; h < kMgMaxG; ++h) m[h] = -INFINITY;
-    for (int j = tid; j < neff; j += kMgThreads) {
-      float v[kMgMaxG];
-      head_scores(j, v);
-#pragma unroll
-      for (int h = 0; h < kMgMaxG; ++h) m[h] = fmaxf(m[h], h < G ? v[h] : -INFINITY);
-    }
-    wave_max_n<kMgMaxG>(m);
-    if (lane == 0)
-#pragma unroll
-      for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = m[h];
-  }
-  lds_barrier();
 #pragma unroll
   for (int h = 0; h < kMgMaxG; ++h) {
     mx[h] = red[0][h];
 #pragma unroll
     for (int w = 1; w < kMgWaves; ++w) mx[h] = fmaxf(mx[h], red[w][h]);
   }
-  lds_barrier();  // every max read before red is reused
+  // e = exp(s - max) replaces the score in LDS (the thread reads it back for
+  // the probability), and the sums go to a second exchange array
   {
     float e[kMgMaxG];
 #pragma unroll
@@ -698,19 +694,24 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
       float v[kMgMaxG];
       head_scores(j, v);
 #pragma unroll
-      for (int h = 0; h < kMgMaxG; ++h) e[h] += h < G ? expf(v[h] - mx[h]) : 0.f;
+      for (int h = 0; h < kMgMaxG; ++h) {
+        v[h] = h < G ? expf(v[h] - mx[h]) : 0.f;
+        e[h] += v[h];
+      }
+      *reinterpret_cast<re_f32x4*>(sc + (size_t)j * kMgMaxG) = re_f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<re_f32x4*>(sc + (size_t)j * kMgMaxG + 4) = re_f32x4{v[4], v[5], v[6], v[7]};
     }
     wave_sum_n<kMgMaxG>(e);
     if (lane == 0)
 #pragma unroll
-      for (int h = 0; h < kMgMaxG; ++h) red[wave][h] = e[h];
+      for (int h = 0; h < kMgMaxG; ++h) red_sum[wave][h] = e[h];
   }
   lds_barrier();
 #pragma unroll
   for (int h = 0; h < kMgMaxG; ++h) {
     float total = 0.f;
 #pragma unroll
-    for (int w = 0; w < kMgWaves; ++w) total += red[w][h];
+    for (int w = 0; w < kMgWaves; ++w) total += red_sum[w][h];
     inv[h] = 1.0f / total;
   }
   for (int j = tid; j < padded; j += kMgThreads) {
@@ -723,7 +724,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     }
 #pragma unroll
     for (int h = 0; h < kMgMaxG; ++h) {
-      const float p = h < G && j < neff ? round_bf16(expf(v[h] - mx[h]) * inv[h]) : 0.f;
+      const float p = h < G && j < neff ? round_bf16(v[h] * inv[h]) : 0.f;
       pb[(size_t)h * span + j] = f_to_bf16(p);  // exact: p is bf16
     }
   }
