@@ -436,43 +436,56 @@ typedef float mg_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMgThreads = 512, kMgWaves = 8, kMgTile = 256, kMgD = 128, kMgMaxG = 8;
 constexpr int kMgChunk = 4;           // tiles whose keys are requested together
 
-// A 256-position value tile in LDS: row-major, 256 bytes a row, the row's
-// 32-byte chunks XOR-swizzled (chunk c of row R at c ^ mg_vswz(R)) so that
-// each half wave of mg_read_v's transposing reads covers the 64 banks once.
-constexpr size_t kMgVTileBytes = (size_t)kMgTile * kMgD * sizeof(bf16_t);
-__device__ __forceinline__ int mg_vswz(int R) { return (R & 3) | (((R >> 3) & 1) << 2); }
-
-// Rows p0 .. p0+7 of the tile, elements 8 l16 ..+8 of each; rows whose mask
-// bit is clear (past the context, or a slot outside the cache) as zeros.
-__device__ __forceinline__ void mg_store_v(bf16_t* vt, const Vec8<bf16_t> (&v)[8], int mask, int p0, int l16) {
-  bf16_t* base = vt + p0 * kMgD + (l16 & 1) * 8;
-  if (__builtin_amdgcn_ballot_w64(mask != 0xff) == 0) {  // every row of the wave present
+// P.V of one wave's 32 positions of a tile, from the value rows the wave
+// loaded: lane (l / 16, l % 16) holds elements 8 (l % 16) + e of rows
+// 8 (l / 16) + i (bit i of mask: the row is present; absent rows enter as
+// zeros).  Product e takes element e of the lane's 8 rows (4 v_perm) as the B
+// operand -- k = the lane's 8 positions, column l % 16 = dim 8 (l % 16) + e --
+// so its 16 output columns are dims e, 8 + e, ..., 120 + e and the 8
+// products cover all 128 dims without a transpose.  pa: p of head l % 16 at
+// the lane's 8 positions.  Value v of lane l in oacc[e]: head 4 (l / 16) + v,
+// dim 8 (l % 16) + e.
+__device__ __forceinline__ void mg_pv_rows(mg_f32x4 (&oacc)[8], const re_u32x4& pa, const Vec8<bf16_t> (&v)[8],
+                                           int mask) {
+  re_u32x4 w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = v[i].v;
+  if (__builtin_amdgcn_ballot_w64(mask != 0xff) != 0) {  // some row of the wave absent
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<re_u32x4*>(base + i * kMgD + ((l16 >> 1) ^ mg_vswz(p0 + i)) * 16) = v[i].v;
-  } else {
+      if (!((mask >> i) & 1)) w[i] = re_u32x4{0u, 0u, 0u, 0u};
+  }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const re_u32x4 x = (mask >> i) & 1 ? v[i].v : re_u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<re_u32x4*>(base + i * kMgD + ((l16 >> 1) ^ mg_vswz(p0 + i)) * 16) = x;
-    }
+  for (int e = 0; e < 8; ++e) {
+    // word i: element e of rows 2 i (low half) and 2 i + 1 (high half)
+    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+    re_u32x4 bw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bw[i] = __builtin_amdgcn_perm(w[2 * i + 1][e >> 1], w[2 * i][e >> 1], sel);
+    oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), __builtin_bit_cast(mg_bf16x8, bw),
+                                                      oacc[e], 0, 0, 0);
   }
 }
 
-// The B operand of P.V step k for wave w: dim 16 w + l % 16 of positions
-// 32 k + 8 (l / 16) ..+8, by two transposing LDS reads (ds_read_b64_tr_b16):
-// in each 16-lane group lane q + 4 r names the 8 bytes of dims 4 q ..+4 of
-// row kb + r, and lane i receives dim i's values of the 4 rows in row order.
-typedef short mg_v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) mg_v4i16* mg_v4i16_lds;
-__device__ __forceinline__ mg_bf16x8 mg_read_v(const bf16_t* vt, int k, int wave, int lane) {
-  const int gi = lane & 15, r = gi >> 2;
-  const int R = k * 32 + (lane >> 4) * 8 + r;  // rows R and R + 4 share mg_vswz
-  const bf16_t* p = vt + R * kMgD + (wave ^ mg_vswz(R)) * 16 + (gi & 3) * 4;
-  const mg_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mg_v4i16_lds)p);
-  const mg_v4i16 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mg_v4i16_lds)(p + 4 * kMgD));
-  const uint2 l2 = __builtin_bit_cast(uint2, lo), u2 = __builtin_bit_cast(uint2, up);
-  return __builtin_bit_cast(mg_bf16x8, re_u32x4{l2.x, l2.y, u2.x, u2.y});
+// The waves' partial outputs in LDS: fp32 [8 waves][8 head slots][128].
+constexpr size_t kMgPartBytes = (size_t)kMgWaves * kMgMaxG * kMgD * sizeof(float);
+__device__ __forceinline__ void mg_put_partials(float* part, const mg_f32x4 (&oacc)[8], int wave, int lane) {
+  const int lq = lane >> 4, l16 = lane & 15;
+  if (lq < 2) {  // head slots 0..7
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float* dst = part + ((size_t)wave * kMgMaxG + lq * 4 + v) * kMgD + l16 * 8;
+      *reinterpret_cast<re_f32x4*>(dst) = re_f32x4{oacc[0][v], oacc[1][v], oacc[2][v], oacc[3][v]};
+      *reinterpret_cast<re_f32x4*>(dst + 4) = re_f32x4{oacc[4][v], oacc[5][v], oacc[6][v], oacc[7][v]};
+    }
+  }
+}
+// Element e = h * 128 + d of the output: the 8 waves' partials in wave order.
+__device__ __forceinline__ float mg_sum_partials(const float* part, int e) {
+  float o = 0.f;
+#pragma unroll
+  for (int w = 0; w < kMgWaves; ++w) o += part[(size_t)w * kMgMaxG * kMgD + e];
+  return o;
 }
 
 // The window's tiles rounded up to whole chunks.
@@ -492,7 +505,7 @@ __host__ __device__ MgLayout mgroup_layout(int G, int window, int blocks_per_row
   (void)G;
   l.pb = (size_t)window * kMgMaxG * sizeof(float);
   l.part = l.pb + (size_t)kMgMaxG * span * sizeof(bf16_t);
-  l.roff = l.part + (size_t)kMgWaves * kMgMaxG * kMgD * sizeof(float);
+  l.roff = l.part + kMgPartBytes;
   l.tabs = l.roff + span * sizeof(int);
   l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
   return l;
@@ -730,38 +743,16 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   }
 
   // P.V: wave w multiplies the value rows it loaded (its 32 positions of
-  // each tile) into partial outputs of every head over all 128 columns,
-  // straight from registers.  Lane (l / 16, l % 16) holds elements
-  // 8 (l % 16) + e of rows 8 (l / 16) + i; product e takes element e of its 8
-  // rows as the B operand (k = the lane's 8 positions, column l % 16 = dim
-  // 8 (l % 16) + e), so its 16 output columns are dims e, 8 + e, ..., 120 + e.
+  // each tile) from registers into partial outputs of every head (A rows
+  // G..7 are zero; rows 8..15 repeat 0..7, and an output row depends on its
+  // A row alone, so those rows land in output rows that are never read).
   mg_f32x4 oacc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) oacc[e] = mg_f32x4{0.f, 0.f, 0.f, 0.f};
   auto pv_tile = [&](const Vec8<bf16_t>(&v)[8], int mask, int t) {
-    re_u32x4 w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = v[i].v;
-    if (__builtin_amdgcn_ballot_w64(mask != 0xff) != 0) {  // some row of the wave absent: zeros
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (!((mask >> i) & 1)) w[i] = re_u32x4{0u, 0u, 0u, 0u};
-    }
-    // A: p of head l % 16 at the wave's positions 8 (l / 16) ..+8.  Rows G..7
-    // are zero; rows 8..15 repeat 0..7, and an output row depends on its A
-    // row alone, so those rows land in output rows that are never read.
     const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * span + t * kMgTile +
                                                             wave * 32 + lq * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      // word i: element e of rows 2 i (low half) and 2 i + 1 (high half)
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      re_u32x4 bw;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) bw[i] = __builtin_amdgcn_perm(w[2 * i + 1][e >> 1], w[2 * i][e >> 1], sel);
-      oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa),
-                                                        __builtin_bit_cast(mg_bf16x8, bw), oacc[e], 0, 0, 0);
-    }
+    mg_pv_rows(oacc, pa, v, mask);
   };
   lds_barrier();  // the probabilities are written
 #pragma unroll
@@ -773,26 +764,14 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kMgChunk; ++i) pv_tile(vr[i], vmask[i], c * kMgChunk + i);
   }
-  // value v of lane l in oacc[e]: head 4 (l / 16) + v, dim 8 (l % 16) + e.
-  // Heads 0..7 of each wave go to LDS as fp32 [8][128], then the 8 waves'
-  // partials are added in wave order.
-  float* part = reinterpret_cast<float*>(mg_smem + L.part);  // [8 waves][8 heads][128]
-  if (lq < 2) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float* dst = part + ((size_t)wave * kMgMaxG + lq * 4 + v) * kMgD + l16 * 8;
-      *reinterpret_cast<re_f32x4*>(dst) = re_f32x4{oacc[0][v], oacc[1][v], oacc[2][v], oacc[3][v]};
-      *reinterpret_cast<re_f32x4*>(dst + 4) = re_f32x4{oacc[4][v], oacc[5][v], oacc[6][v], oacc[7][v]};
-    }
-  }
+  // the 8 waves' partials added in wave order
+  float* part = reinterpret_cast<float*>(mg_smem + L.part);
+  mg_put_partials(part, oacc, wave, lane);
   lds_barrier();
   for (int e = tid; e < G * kMgD; e += kMgThreads) {
-    float o = 0.f;
-#pragma unroll
-    for (int w = 0; w < kMgWaves; ++w) o += part[(size_t)w * kMgMaxG * kMgD + e];
     const int k = g * G * kMgD + e;
     static_cast<bf16_t*>(a.out)[a.packed_out ? xpack_index(b, k, a.heads * kMgD) : (size_t)b * a.heads * kMgD + k] =
-        f_to_bf16(o);
+        f_to_bf16(mg_sum_partials(part, e));
   }
 }
 
@@ -811,19 +790,19 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
 // Block b = grp + groups * tile (grp = row * KV heads + KV head).
 constexpr int kMsRows = kMgTile;  // positions per workgroup
 struct MsLayout {
-  size_t roff, sc, pb, vt, stat, tabs, total;
+  size_t roff, sc, pb, part, stat, tabs, total;
 };
 // LDS of the two kernels: row offsets [256] int, then the scores kernel's
-// scores [256][8] fp32, or the P.V kernel's probabilities [8][256] bf16, a
-// value tile [256][128] bf16 and head statistics [2][8] fp32; the block
-// table last.
+// scores [256][8] fp32, or the P.V kernel's probabilities [8][256] bf16, the
+// waves' partial outputs [8][8][128] fp32 and head statistics [2][8] fp32;
+// the block table last.
 __host__ __device__ MsLayout msplit_layout(int blocks_per_row, bool pv) {
   MsLayout l;
   l.roff = 0;
   l.sc = l.roff + kMsRows * sizeof(int);
   l.pb = l.sc;
-  l.vt = l.pb + (size_t)kMgMaxG * kMsRows * sizeof(bf16_t);
-  l.stat = l.vt + kMgVTileBytes;
+  l.part = l.pb + (size_t)kMgMaxG * kMsRows * sizeof(bf16_t);
+  l.stat = l.part + kMgPartBytes;
   l.tabs = pv ? l.stat + 2 * kMgMaxG * sizeof(float) : l.sc + (size_t)kMsRows * kMgMaxG * sizeof(float);
   l.total = l.tabs + (size_t)blocks_per_row * sizeof(int);
   return l;
@@ -978,7 +957,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
   const MsLayout L = msplit_layout(a.blocks_per_row, true);
   int* roff = reinterpret_cast<int*>(ms_smem + L.roff);
   bf16_t* pb = reinterpret_cast<bf16_t*>(ms_smem + L.pb);  // [kMgMaxG][256]
-  bf16_t* vt = reinterpret_cast<bf16_t*>(ms_smem + L.vt);  // value tile [256][D], swizzled
+  float* part = reinterpret_cast<float*>(ms_smem + L.part);  // [8 waves][8][128]
   float* stat = reinterpret_cast<float*>(ms_smem + L.stat);  // [max, 1 / sum][kMgMaxG]
   int* tabs = reinterpret_cast<int*>(ms_smem + L.tabs);
   const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
@@ -1027,23 +1006,20 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
     if (h < G && j < neff) p = round_bf16(expf(a.sp_scores[(row0 + h) * W + j] - stat[h]) * stat[kMgMaxG + h]);
     pb[(size_t)h * kMsRows + jl] = f_to_bf16(p);  // exact: p is bf16
   }
-  // The value tile, then P.V: wave w owns output columns 16 w ..+16 of every head.
-  mg_store_v(vt, vr, mask, p0, l16);
+  // P.V from registers: wave w multiplies its own 32 positions (A rows G..7
+  // zero, rows 8..15 reach only output rows that are never read), then the
+  // 8 waves' partials are added in wave order.
+  lds_barrier();  // the probabilities are written
+  mg_f32x4 oacc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) oacc[e] = mg_f32x4{0.f, 0.f, 0.f, 0.f};
+  const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * kMsRows + wave * 32 + lq * 8);
+  mg_pv_rows(oacc, pa, vr, mask);
+  mg_put_partials(part, oacc, wave, lane);
   lds_barrier();
-  mg_f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int k = 0; k < kMsRows / 32; ++k) {
-    // A: p of head l % 16 at positions 32 k + 8 (l / 16) ..+8 (rows G..7
-    // zero, rows 8..15 only reach output rows that are never stored)
-    const re_u32x4 pa = *reinterpret_cast<const re_u32x4*>(pb + (size_t)(l16 & (kMgMaxG - 1)) * kMsRows + k * 32 + lq * 8);
-    oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mg_bf16x8, pa), mg_read_v(vt, k, wave, lane), oacc,
-                                                   0, 0, 0);
-  }
-  // value v of lane l: head 4 (l / 16) + v, column 16 w + l % 16
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int h = lq * 4 + v;
-    if (h < G) a.sp_part[((row0 + h) * a.split_tiles + t) * kMgD + wave * 16 + l16] = oacc[v];
+  for (int e = tid; e < G * kMgD; e += kMgThreads) {
+    const int h = e / kMgD, d = e - h * kMgD;
+    a.sp_part[((row0 + h) * a.split_tiles + t) * kMgD + d] = mg_sum_partials(part, e);
   }
 }
 
