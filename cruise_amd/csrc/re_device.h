@@ -45,20 +45,17 @@ __device__ __forceinline__ float round_bf16(float f) {
 }
 
 // x / sqrt(128) for a bf16-valued x whose quotient is rounded to bf16 next
-// (the scaled attention score): one product and two fused corrections
-// (Markstein's division by a constant with a precomputed reciprocal) instead
-// of the IEEE division sequence.  For every finite bf16 x the bf16 rounding
-// of the result equals the bf16 rounding of the correctly rounded fp32
-// quotient (the fp32 results differ in the last bits for 28 dividends below
-// 2^-120, where the correction underflows; tests/test_div_sqrt128.py checks
-// all 65,536 inputs).  An
-// infinite x keeps the plain product, where the correction would be NaN.
+// (the scaled attention score): the product with the rounded reciprocal.
+// For every bf16 x the bf16 rounding of the product equals the bf16 rounding
+// of the correctly rounded fp32 quotient x / c, c = fp32(sqrt(128)), as the
+// reference divides: a quotient of an 8-bit mantissa by c never comes within
+// about 1e-5 (relative) of a bf16 rounding boundary, far beyond the product's
+// two roundings (the fp32 results differ for 26,650 dividends, the bf16 ones
+// for none; tests/test_div_sqrt128.py checks all 65,536 inputs).  Infinities,
+// NaN and zeros pass through as in the division.
 __device__ __forceinline__ float div_sqrt128_bf16(float x) {
-  constexpr float c = __builtin_bit_cast(float, 0x413504f3u);   // sqrt(128) rounded to fp32
-  constexpr float rc = __builtin_bit_cast(float, 0x3db504f3u);  // 1 / c rounded to fp32
-  const float q0 = x * rc;
-  const float q1 = fmaf(fmaf(-q0, c, x), rc, q0);
-  return __builtin_isinf(q0) ? q0 : q1;
+  constexpr float rc = __builtin_bit_cast(float, 0x3db504f3u);  // 1 / fp32(sqrt(128)) rounded to fp32
+  return x * rc;
 }
 
 // Element traits: the compute dtype T of a model is bf16 or fp32.

@@ -1,9 +1,12 @@
 """The scaled attention score's division by sqrt(128) on the device
-(`div_sqrt128_bf16`, re_device.h) is a product with the rounded reciprocal
-and two fused corrections.  Checked here for every finite bf16 dividend with
-exact integer arithmetic: after the bf16 rounding that follows it in the
-kernels, it equals the bf16 rounding of the correctly rounded fp32 quotient
-x / fp32(sqrt(128)), the IEEE division the reference performs."""
+(`div_sqrt128_bf16`, re_device.h) is the product with the rounded
+reciprocal.  Checked here for every bf16 dividend with exact integer
+arithmetic: after the bf16 rounding that follows it in the kernels, it
+equals the bf16 rounding of the correctly rounded fp32 quotient
+x / fp32(sqrt(128)), the IEEE division the reference performs.  Planted: a
+reciprocal held in bf16 and a truncating bf16 rounding must fail (the
+quotients sit far from every bf16 rounding boundary, so the fp32
+reciprocal's neighbours a few ulps away would still pass)."""
 from __future__ import annotations
 
 import math
@@ -48,18 +51,34 @@ def test_constants_are_the_rounded_sqrt_and_reciprocal():
     assert f32_value(RC_BITS) == rne32(1 / c)
 
 
-def test_every_finite_bf16_dividend():
-    c, rc = f32_value(C_BITS), f32_value(RC_BITS)
-    fp32_differ = 0
+def product_mismatches(rc_bits: int, rounding=None) -> tuple[int, int]:
+    """(fp32 results that differ from the division, bf16 results that differ)
+    over every finite nonzero bf16 dividend, for the product x * rc."""
+    rounding = rounding or bf16_bits
+    c, rc = f32_value(C_BITS), f32_value(rc_bits)
+    fp32_differ = bf16_differ = 0
     for hi in range(1 << 16):
         if (hi >> 7) & 0xFF == 0xFF or hi & 0x7FFF == 0:
-            continue  # inf / NaN (the kernel keeps the plain product there), zeros
+            continue  # inf / NaN and zeros pass through the product unchanged
         x = f32_value(hi << 16)
         exact = rne32(x / c)
-        q0 = rne32(x * rc)
-        q1 = rne32(q0 + rne32(x - q0 * c) * rc)  # fmaf(fmaf(-q0, c, x), rc, q0)
-        if q1 != exact:
-            fp32_differ += 1
-            assert abs(x) < Fraction(2) ** -120, hex(hi)  # only where the correction underflows
-        assert bf16_bits(q1) == bf16_bits(exact), hex(hi)
-    assert fp32_differ == 28
+        q = rne32(x * rc)
+        fp32_differ += q != exact
+        bf16_differ += rounding(q) != bf16_bits(exact)
+    return fp32_differ, bf16_differ
+
+
+def test_every_finite_bf16_dividend():
+    fp32_differ, bf16_differ = product_mismatches(RC_BITS)
+    assert bf16_differ == 0
+    assert fp32_differ == 26650  # the fp32 products differ; the bf16 roundings never do
+
+
+def test_planted_mistakes_fail():
+    # the reciprocal held in bf16, the reciprocal of a bf16 sqrt(128), and a
+    # bf16 rounding that truncates
+    assert product_mismatches(0x3DB50000)[1] > 0
+    c_bf16 = struct.unpack("<f", struct.pack("<I", 0x41350000))[0]
+    assert product_mismatches(struct.unpack("<I", struct.pack("<f", 1.0 / c_bf16))[0])[1] > 0
+    truncate = lambda v: (struct.unpack("<I", struct.pack("<f", float(v)))[0] >> 16) & 0xFFFF
+    assert product_mismatches(RC_BITS, truncate)[1] > 0
