@@ -182,6 +182,11 @@ def main() -> int:
     decoder_steps = executed_total / B
     ms_per_decoder_step = elapsed * 1e3 / decoder_steps
     step_gbs = streamed / (ms_per_decoder_step * 1e-3) / 1e9
+    # every bf16 parameter of the model once per step: the streamed bytes
+    # plus the embedding table, of which a step gathers only B rows (Qwen2.5-7B:
+    # 15.23 GB against 14.14 GB streamed)
+    param_bytes = streamed + rt.vocab * rt.info("hidden") * rt.info("dtype_bytes")
+    param_gbs = param_bytes / (ms_per_decoder_step * 1e-3) / 1e9
     # gate/up launched for layer 0, 1, ..., 27 in turn between two HIP events
     # on the engine's stream: every launch streams another layer's 272 MB of
     # weights, so none is warm in the 256 MB memory-side cache, as in the
@@ -245,6 +250,9 @@ def main() -> int:
         "ms_per_decoder_step": round(ms_per_decoder_step, 4),
         "step_weight_stream_gbs": round(step_gbs, 1),
         "step_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "step_streamed_bytes": streamed,
+        "param_bytes": param_bytes,
+        "step_param_roofline_frac": round(param_gbs / HBM_PEAK_GBS, 4),
         "host_control_wall_ms_p50": round(statistics.median(host_ms), 4),
         "native_wall_us_p50": int(statistics.median(walls)),
         "epoch_graph_nodes": nodes,

@@ -103,7 +103,8 @@ struct ProjArgs {
   // ranges): workgroup i runs in dispatch slot i / slot_cus of its CU and
   // takes a share of the units proportional to slot_w[slot].
   int slot_cus;
-  int slot_w[4];
+  int slot_shift;    // log2(slot_cus) when it is a power of two, else -1
+  int slot_base[5];  // first unit of each slot's workgroups; slot_base[4] = units
 };
 
 // Unit range of workgroup g when the grid is 4 x slot_cus workgroups,
@@ -111,16 +112,20 @@ struct ProjArgs {
 // The SIMD arbiter issues for the oldest waves first, so the later slots of
 // a CU stream more slowly; giving them fewer units lets every slot finish
 // together, which keeps enough loads in flight until the end.
+// The host splits the units over the four slots in proportion to their
+// weights (slot_base); inside a slot the workgroups split its units evenly.
+// Plain 32-bit arithmetic (a shift where slot_cus is a power of two), so the
+// first weight requests leave a few instructions into the kernel.
 __device__ __forceinline__ int slot_prefix(const ProjArgs& a, int g) {
   const int cus = a.slot_cus;
-  long long p = 0, tot = 0;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    tot += (long long)cus * a.slot_w[s];
-    if (s < g / cus) p += (long long)cus * a.slot_w[s];
-    else if (s == g / cus) p += (long long)(g % cus) * a.slot_w[s];
-  }
-  return g >= 4 * cus ? a.units : static_cast<int>((long long)a.units * p / tot);
+  if (g >= 4 * cus) return a.units;
+  const int sh = a.slot_shift;
+  const int s = sh >= 0 ? g >> sh : g / cus;
+  const int i = g - s * cus;
+  const int b0 = s == 0 ? a.slot_base[0] : s == 1 ? a.slot_base[1] : s == 2 ? a.slot_base[2] : a.slot_base[3];
+  const int b1 = s == 0 ? a.slot_base[1] : s == 1 ? a.slot_base[2] : s == 2 ? a.slot_base[3] : a.slot_base[4];
+  const int n = b1 - b0;
+  return b0 + (sh >= 0 ? (i * n) >> sh : i * n / cus);
 }
 
 template <int KIND, typename T>
@@ -746,7 +751,14 @@ static void set_slots(ProjArgs& a, const LaunchPlan& p, int grid) {
   a.slot_cus = 0;
   if (p.slot_cus > 0 && grid == 4 * p.slot_cus && p.row_tiles == 1) {
     a.slot_cus = p.slot_cus;
-    for (int s = 0; s < 4; ++s) a.slot_w[s] = p.slot_w[s];
+    a.slot_shift = (p.slot_cus & (p.slot_cus - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(p.slot_cus)) : -1;
+    long long tot = 0, pre = 0;
+    for (int s = 0; s < 4; ++s) tot += p.slot_w[s];
+    for (int s = 0; s < 4; ++s) {
+      a.slot_base[s] = static_cast<int>((long long)a.units * pre / tot);
+      pre += p.slot_w[s];
+    }
+    a.slot_base[4] = a.units;
   }
 }
 
