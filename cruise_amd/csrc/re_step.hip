@@ -567,8 +567,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_resid(ResidArgs a) {
 // h = T(h + T(x W^T)) (batched_decoder_step.py:399-403) with no fp32
 // partials in global memory and no reduce launch.  One workgroup of 16 waves
 // per CU; workgroup g owns the row pairs [g*ppw, (g+1)*ppw).  For one row
-// pair, wave w covers elements [w*K/16, (w+1)*K/16) of both rows in up to
-// three 512-element loads per row; each lane dots its elements against the B
+// pair, wave w covers its K range (about K/16 elements, down_whole_spans) of
+// both rows in up to three 512-element loads per row; each lane dots its elements against the B
 // rows and the lanes of a wave are combined by the halving exchange into LDS.
 // A lane only ever needs its own elements of the activations x [B, K], so it
 // requests them once and keeps them for every pair (the first two chunks in
@@ -590,6 +590,7 @@ struct DownWholeArgs {
   const void* w;  // bf16 [N, K]
   void* hidden;   // bf16 [B, N]
   int B, N, K, pairs_per_wg;
+  int span[4];    // K elements of each wave of wave group w / 4 (sum of 4 x span = K)
 };
 
 // Requests the weights of row pair u (rows 2u, 2u+1) for this wave's K range.
@@ -607,12 +608,33 @@ __device__ __forceinline__ void whole_issue(Vec8<bf16_t> (&w)[kWholeLoads][2], c
   }
 }
 
+// K elements per wave of each group of four waves.  The SIMD arbiter serves
+// the oldest waves first, so waves 0-3 finish their range first and 12-15
+// last; the younger groups take more of K, and every range is a whole number
+// of 128-byte lines (64 elements), so no two waves share a line: with
+// K = 18,944, 1,088 / 1,152 / 1,216 / 1,280 against 1,184 each (bench 1,476
+// -> 1,482 tok/s).  Equal ranges where K is not a multiple of 256 or the
+// ramp does not fit three loads per lane.  The fp32 sums follow the ranges
+// (wave totals still added in wave order).
+void down_whole_spans(int K, int (&span)[4]) {
+  for (int q = 0; q < 4; ++q) span[q] = K / kWholeWaves;
+  if (K % 256 != 0) return;
+  const int n = K / 256, m = n / 4;  // 64-element units per group of four ranges
+  const int u[4] = {m - 1, m, m + 1, n - 3 * m};
+  for (int q = 0; q < 4; ++q)
+    if (u[q] < 1 || u[q] * 64 > kWholeLoads * kChunk || u[q] < u[q > 0 ? q - 1 : 0]) return;
+  for (int q = 0; q < 4; ++q) span[q] = u[q] * 64;
+}
+
 __global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int MB = 4;
   float* red = reinterpret_cast<float*>(smem_raw);  // [ppw][16][8] wave totals
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  const int K = a.K, span = K / kWholeWaves, k_lo = wave * span;
+  const int K = a.K, g4 = wave >> 2, span = a.span[g4];
+  int k_lo = (wave & 3) * span;
+#pragma unroll
+  for (int q = 0; q < 3; ++q) k_lo += q < g4 ? 4 * a.span[q] : 0;
   const int units = a.N / 2;
   const int u_begin = blockIdx.x * a.pairs_per_wg;
   const int u_end = min(u_begin + a.pairs_per_wg, units);
@@ -929,6 +951,7 @@ static hipError_t decoder_step_t(const KernelEnv& env, const StepPtrs& st, hipSt
         dw.N = d.hidden;
         dw.K = d.intermediate;
         dw.pairs_per_wg = (d.hidden / 2 + p.down_whole_grid - 1) / p.down_whole_grid;
+        down_whole_spans(d.intermediate, dw.span);
         if (want())
           k_down_whole<<<p.down_whole_grid, kWholeWaves * 64, down_whole_lds_bytes(d.intermediate, dw.pairs_per_wg),
                          stream>>>(dw);
