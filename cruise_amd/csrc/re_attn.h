@@ -155,11 +155,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, int block, unsigned
 
   // Round trip 1: the row's block table (into LDS) and the query chunk.
   // Round trip 2: the first tile of keys and values, all loads in flight.
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   for (int e = tid; e < a.blocks_per_row; e += kAttnThreads) tabs[e] = tab[e];
   const Vec8<T> qv = Vec8<T>::load_cached(static_cast<const T*>(a.q) + ((size_t)b * a.heads + h) * D + c * 8);
   lds_barrier();
-  if (stop != 0) return;  // uniform over the workgroup
+  if (flag_set(stop)) return;  // uniform over the workgroup
   int off[S::kLoads];
   tile_offsets<D, P2>(off, tabs, 0, w, r, c, neff, a, g);
   Vec8<T> kr[S::kLoads], vr[S::kLoads];

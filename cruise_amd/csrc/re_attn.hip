@@ -61,10 +61,10 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_split_scores(AttnArgs a) 
   int* tabs = reinterpret_cast<int*>(smem_raw);  // [blocks_per_row]
   const int tid = threadIdx.x;
   const SplitUnit u = split_unit(a, blockIdx.x);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   const bool uniform = a.len[u.b] <= 0;
   const int neff = split_neff(a, u.b);
-  if (stop != 0 || u.t * kAttnTile >= neff) return;  // uniform over the workgroup
+  if (flag_set(stop) || u.t * kAttnTile >= neff) return;  // uniform over the workgroup
   const int lane = tid & 63, w = wave_index(tid);
   const int r = lane / L, c = lane % L;
   const int32_t* tab = a.table + (size_t)u.b * a.blocks_per_row;
@@ -109,9 +109,9 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_split_pv(AttnArgs a) {
   int* tabs = reinterpret_cast<int*>(smem_raw);  // [blocks_per_row]
   const int tid = threadIdx.x;
   const SplitUnit u = split_unit(a, blockIdx.x);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   const int neff = split_neff(a, u.b);
-  if (stop != 0 || u.t * kAttnTile >= neff) return;  // uniform over the workgroup
+  if (flag_set(stop) || u.t * kAttnTile >= neff) return;  // uniform over the workgroup
   const int lane = tid & 63, w = wave_index(tid);
   const int r = lane / L, c = lane % L;
   // Round trip 1: the block table, this thread's score and the first tile
@@ -241,7 +241,7 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
   const int neff = uniform ? W : min(n, W);
   const int ntiles = (neff + kGrpTile - 1) / kGrpTile;
 
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   for (int e = tid; e < a.blocks_per_row; e += kGrpThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
   Vec8<bf16_t> qv[kGrpMaxG];
 #pragma unroll
@@ -249,7 +249,7 @@ __global__ void __launch_bounds__(kGrpThreads) k_attn_group(AttnArgs a) {
     qv[h] = Vec8<bf16_t>::load_cached(static_cast<const bf16_t*>(a.q) +
                                       ((size_t)b * a.heads + g * G + min(h, G - 1)) * kGrpD + c * 8);
   lds_barrier();
-  if (stop != 0) return;  // uniform
+  if (flag_set(stop)) return;  // uniform
 
   // element offset of position j's row chunk in this layer's cache, or -1
   auto row_off = [&](int j) -> int {
@@ -562,7 +562,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
   const int nchunks = (ntiles + kMgChunk - 1) / kMgChunk;
   const int padded = nchunks * kMgChunk * kMgTile;  // positions the requests cover (<= span)
 
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
   // queries as the B operand: head l % 16 (zero past G), 4 k steps
   mg_bf16x8 qf[4];
@@ -575,7 +575,7 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_mgroup(AttnArgs a) {
     }
   }
   lds_barrier();
-  if (stop != 0) return;  // uniform
+  if (flag_set(stop)) return;  // uniform
 
   // Element offset of each position's row (this KV head) in the layer's
   // cache, or -1 past the context or for a slot outside the cache; one LDS
@@ -841,11 +841,11 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_scores(AttnArgs a) {
   int* roff = reinterpret_cast<int*>(ms_smem + L.roff);
   float* sc = reinterpret_cast<float*>(ms_smem + L.sc);  // [256][kMgMaxG]
   int* tabs = reinterpret_cast<int*>(ms_smem + L.tabs);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   const int n = a.len[b];
   const bool uniform = n <= 0;
   const int neff = uniform ? W : min(n, W);
-  if (stop != 0 || t * kMsRows >= neff) return;  // uniform over the workgroup
+  if (flag_set(stop) || t * kMsRows >= neff) return;  // uniform over the workgroup
   for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];
   mg_bf16x8 qf[4];
   {
@@ -960,10 +960,10 @@ __global__ void __launch_bounds__(kMgThreads) k_attn_msplit_pv(AttnArgs a) {
   float* part = reinterpret_cast<float*>(ms_smem + L.part);  // [8 waves][8][128]
   float* stat = reinterpret_cast<float*>(ms_smem + L.stat);  // [max, 1 / sum][kMgMaxG]
   int* tabs = reinterpret_cast<int*>(ms_smem + L.tabs);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   const int n = a.len[b];
   const int neff = n <= 0 ? W : min(n, W);
-  if (stop != 0 || t * kMsRows >= neff) return;  // uniform over the workgroup
+  if (flag_set(stop) || t * kMsRows >= neff) return;  // uniform over the workgroup
   const int nt = (neff + kMsRows - 1) / kMsRows;
   const size_t row0 = (size_t)b * a.heads + g * G;
   for (int e = tid; e < a.blocks_per_row; e += kMgThreads) tabs[e] = a.table[(size_t)b * a.blocks_per_row + e];

@@ -310,6 +310,18 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70)
 // tell that threadIdx.x / 64 is the same for every lane of a wave).
 __device__ __forceinline__ int wave_index(int tid) { return __builtin_amdgcn_readfirstlane(tid >> 6); }
 
+// The step's early-exit flag, requested as a vector load: its wait then sits
+// at the flag's first use (flag_set), after the kernel's weight requests.  A
+// plain load of the uniform address becomes a scalar load, which the
+// compiler waits for right away -- one more memory round trip ahead of the
+// kernel's first request.  The opaque zero index keeps it a vector load.
+__device__ __forceinline__ int32_t request_flag(const int32_t* p) {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return __builtin_nontemporal_load(p + z);
+}
+__device__ __forceinline__ bool flag_set(int32_t v) { return __builtin_amdgcn_readfirstlane(v) != 0; }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);

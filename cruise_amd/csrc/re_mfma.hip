@@ -255,8 +255,8 @@ __device__ __forceinline__ void lm_cu_body(const MfArgs& a, unsigned char* lds, 
 __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_lm_cu(MfArgs a) {
   extern __shared__ __align__(16) unsigned char lc_smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
-  if (stop != 0) return;  // uniform
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
+  if (flag_set(stop)) return;  // uniform
   const int G = gridDim.x, g = blockIdx.x, T = a.vocab / 16;
   const int s_begin = (int)((long long)g * T / G), s_end = (int)((long long)(g + 1) * T / G);
   const int ns = (s_end - s_begin - wave + kLcWaves - 1) / kLcWaves;  // strips of this wave
@@ -301,8 +301,8 @@ constexpr int kGcRing = 8;  // weight steps in flight per wave (few waves stream
 __global__ void __launch_bounds__(kLcWaves * 64, 1) k_mf_gu_cu(MfArgs a) {
   extern __shared__ __align__(16) unsigned char lc_smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(tid);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
-  if (stop != 0) return;  // uniform
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
+  if (flag_set(stop)) return;  // uniform
   const int G = gridDim.x, g = blockIdx.x, T = a.hidden_dim / 16;  // hidden_dim: I
   const int s_begin = (int)((long long)g * T / G), s_end = (int)((long long)(g + 1) * T / G);
   const int u = s_begin + wave;
@@ -370,8 +370,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_mf_part_cu(MfArgs a) {
   const int g = blockIdx.x * WAVES + wave;  // this wave's strip
   const int kstep0 = blockIdx.y * STEPS;
   const int ksteps = a.K / kMfK;
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
-  if (stop != 0) return;  // uniform
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
+  if (flag_set(stop)) return;  // uniform
   // block b's fragment f = t * steps + s (tile t, step s of the block) by
   // wave f % WAVES; a wave past the end copies the last one again
   auto stage = [&](auto bc) {
@@ -461,8 +461,8 @@ __global__ void __launch_bounds__(256) k_mf_qkv_finish(MfArgs a) {
   const int nheads = a.hidden_dim / a.head_dim;  // q, k and v heads
   const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx >= a.B * nheads * half) return;
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
-  if (stop != 0) return;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
+  if (flag_set(stop)) return;
   const int m = idx / (nheads * half), rem = idx - m * nheads * half;
   const int head = rem / half, j = rem - head * half;
   const int r0 = head * a.head_dim + j, r1 = r0 + half;

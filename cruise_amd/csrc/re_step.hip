@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   // hidden rows and norm weight, then the first row pair's weights, so the
   // norm is computed while the weights are in flight.  The flag is uniform:
   // the workgroup leaves together, after the barriers.
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   NormIn<T, MB> nin;
   norm_load<T, MB>(nin, static_cast<const T*>(a.hidden), static_cast<const T*>(a.norm_w), b0, a.B, H, tid);
   // Unconditional (a wave past its range loads a valid pair it never uses):
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(WAVES * 64, (proj_min_waves<T, MB, KIND>())) k
   if constexpr (KIND == kQkv) epi = qkv_epilogue_inputs<T>(a, min(u, a.units - 1), row0, row1, b0 + lane);
   __builtin_amdgcn_sched_barrier(0);
   norm_to_lds<T, MB>(nin, b0, a.B, H, a.eps, xs, red + 3 * WAVES * kRowsPerWave * MB, tid);
-  if (stop != 0) return;
+  if (flag_set(stop)) return;
   // argmax running state of lane m < MB (batch row b0+m), LM head only
   float best_v = 0.f;
   int best_i = -1;
@@ -380,7 +380,7 @@ __global__ void __launch_bounds__(kQkvKsWaves * 64, 1) k_qkv_ksplit(ProjArgs a) 
   const int u0 = blockIdx.x * PAIRS;
   const bf16_t* W0 = static_cast<const bf16_t*>(a.w0);
   const bf16_t* Hd = static_cast<const bf16_t*>(a.hidden);
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   Vec8<bf16_t> x[MB];
 #pragma unroll
   for (int m = 0; m < MB; ++m) x[m] = Vec8<bf16_t>::load_cached(Hd + (size_t)min(m, a.B - 1) * H + k0);
@@ -418,7 +418,7 @@ __global__ void __launch_bounds__(kQkvKsWaves * 64, 1) k_qkv_ksplit(ProjArgs a) 
   wave_reduce_transpose<MB>(ss, lane);
   if ((lane & (64 / MB - 1)) == 0) nred[wave][lane / (64 / MB)] = ss[0];
   lds_barrier();
-  if (stop != 0) return;  // uniform
+  if (flag_set(stop)) return;  // uniform
   Vec8<bf16_t> y[MB];
 #pragma unroll
   for (int m = 0; m < MB; ++m) {
@@ -517,7 +517,7 @@ __device__ __forceinline__ void resid_segment(const ResidArgs& a, T* xs, float* 
   T* Hd = static_cast<T*>(a.hidden);
   // Flag, residual values (single segment), activations, then weights; the
   // weight loads are unconditional (clamped to a valid pair).
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   // (unconditional, clamped: used by lanes < MB of single-segment launches)
   const size_t hrow = (size_t)min(b0 + lane, a.B - 1) * a.N;
   const T h0 = Hd[hrow + 2 * uc], h1 = Hd[hrow + 2 * uc + 1];
@@ -528,7 +528,7 @@ __device__ __forceinline__ void resid_segment(const ResidArgs& a, T* xs, float* 
   load_rows<T, kRowsPerWave, FULL>(w, wr, k0, len, lane);
   __builtin_amdgcn_sched_barrier(0);
   store_rows_block<T, MB>(xv, b0, a.B, len, xs, kSeg, tid);
-  if (stop != 0 || u >= units) return;
+  if (flag_set(stop) || u >= units) return;
   float acc[kRowsPerWave][MB];
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; ++r)
@@ -651,7 +651,7 @@ __global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArg
   // LDS staging and no workgroup barrier before the first products.  Loads
   // past the range or the batch are clamped to valid addresses; their
   // products are skipped or never stored.
-  const int32_t stop = a.done != nullptr ? __builtin_nontemporal_load(a.done) : 0;
+  const int32_t stop = a.done != nullptr ? request_flag(a.done) : 0;
   const int nout = (u_end - u_begin) * 8;
   const int ot = min(tid, nout - 1);
   const int o_u = u_begin + ot / 8, o_r = (ot >> 2) & 1, o_m = ot & 3;
@@ -674,7 +674,7 @@ __global__ void __launch_bounds__(kWholeWaves * 64, 1) k_down_whole(DownWholeArg
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int m = 0; m < MB; ++m) xl[m] = xr[kReg][m];
-  if (stop != 0) return;  // uniform over the workgroup
+  if (flag_set(stop)) return;  // uniform over the workgroup
 
   // One pair: products over this wave's range, wave totals to LDS.
   auto pair = [&](Vec8<bf16_t>(&w)[kWholeLoads][2], int u) {
